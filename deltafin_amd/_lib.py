@@ -1,0 +1,195 @@
+"""ctypes binding of libk3hipmoe.so (the C ABI in include/k3_hip_moe_abi.h).
+
+The library is loaded after torch so that it binds to the HIP runtime torch
+already mapped (both carry the SONAME libamdhip64.so.7); loading fails loudly if
+the library is missing or two HIP runtimes end up in the process.  There is no
+CPU fallback: every entry point runs the gfx950 code or returns an error.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libk3hipmoe.so"
+
+K3_HIP_OK = 0
+K3_HIP_E_INIT = -1
+K3_HIP_E_INVALID = -2
+K3_HIP_E_ALLOC = -3
+K3_HIP_E_COPY = -4
+K3_HIP_E_EXEC = -5
+K3_HIP_E_CAPABILITY = -6
+K3_HIP_E_DESCRIPTOR = -7
+
+K3_LAYOUT_RAW_V1 = 1
+K3_LAYOUT_SCALE4_V2 = 2
+K3_DESCRIPTOR_ABI_V1 = 1
+K3_RAW_V1_EXPERT_SPAN = 17547264
+K3_SCALE4_V2_EXPERT_SPAN = 17039360
+K3_CAP_RAW_V1 = 1 << K3_LAYOUT_RAW_V1
+K3_CAP_SCALE4_V2 = 1 << K3_LAYOUT_SCALE4_V2
+
+K3_ACT_SITU = 0
+K3_ACT_SILU = 1
+K3_DTYPE_F32 = 0
+K3_DTYPE_BF16 = 1
+K3_HIP_MAX_TOKEN_EXPERTS = 32
+K3_HIP_MAX_POSITIONS = 16
+K3_HIP_MAX_EDGES = 256
+
+
+class K3HipExpertDescriptorV1(C.Structure):
+    _fields_ = [
+        ("abi_version", C.c_uint32),
+        ("struct_bytes", C.c_uint32),
+        ("layout_id", C.c_uint32),
+        ("reserved", C.c_uint32),
+        ("blob_bytes", C.c_uint64),
+        ("blob", C.c_void_p),
+    ]
+
+
+class K3HipGeometryV1(C.Structure):
+    _fields_ = [
+        ("abi_version", C.c_uint32),
+        ("struct_bytes", C.c_uint32),
+        ("hidden", C.c_uint32),
+        ("intermediate", C.c_uint32),
+        ("activation", C.c_uint32),
+        ("reserved", C.c_uint32),
+        ("expert_span", C.c_uint64),
+    ]
+
+
+assert C.sizeof(K3HipExpertDescriptorV1) == 32
+assert C.sizeof(K3HipGeometryV1) == 32
+
+_vp = C.c_void_p
+_i32 = C.c_int
+_u32 = C.c_uint32
+_u64 = C.c_uint64
+_i64 = C.c_int64
+_GP = C.POINTER(K3HipGeometryV1)
+_DP = C.POINTER(K3HipExpertDescriptorV1)
+
+# name -> (restype, argtypes); every symbol declared in include/k3_hip_moe_abi.h
+SIGNATURES = {
+    "k3_hip_geometry_span": (_u64, [_u32, _u32]),
+    "k3_hip_geometry_preset": (_i32, [_i32, _GP]),
+    "k3_hip_last_error": (C.c_char_p, []),
+    "k3_hip_init": (_i32, [C.c_char_p]),
+    "k3_hip_available": (_i32, []),
+    "k3_hip_descriptor_abi_version": (_u32, []),
+    "k3_hip_layout_capabilities": (_u64, []),
+    "k3_hip_configure_v1": (_i32, [_GP]),
+    "k3_hip_shapes": (None, [C.POINTER(_i32), C.POINTER(_i32), C.POINTER(C.c_longlong)]),
+    "k3_hip_stats": (None, [C.POINTER(C.c_longlong)]),
+    "k3_hip_mode": (_i32, []),
+    "k3_hip_set_mode": (_i32, [_i32]),
+    "k3_hip_drop": (None, [_vp]),
+    "k3_hip_flush": (None, []),
+    "k3_hip_moe_layer_desc_v1": (_i32, [_DP, _i32, _vp, _vp, _vp]),
+    "k3_hip_moe_positions_desc_v1": (_i32, [_DP, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "k3_hip_moe_layer": (_i32, [_vp, _i32, _vp, _vp, _vp]),
+    "k3_hip_moe_positions": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "k3_hip_moe_abi_version": (_u32, []),
+    "k3_hip_moe_shapes": (None, [C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i64), C.POINTER(_u32)]),
+    "k3_hip_moe_available": (_i32, [_i32]),
+    "k3_hip_mxfp4_gemv": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "k3_hip_mxfp4_gemv_ex": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _vp]),
+    "k3_hip_moe_launch": (_i32, [_GP, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "k3_hip_moe_workspace_bytes": (_u64, [_GP, _i32, _i32]),
+    "k3_hip_moe_layer_device": (_i32, [_GP, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _u64, _vp]),
+    "k3_hip_moe_route_layer_device": (
+        _i32, [_GP, _vp, _u64, _i32, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _u64, _vp]),
+    "k3_hip_moe_verify_route_device": (
+        _i32, [_GP, _vp, _u64, _i32, _vp, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _u64, _vp]),
+    "k3_hip_moe_verify_device": (
+        _i32, [_GP, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _u64, _vp]),
+    "k3_hip_cache_create": (_vp, [_i32, _u64, _i32, _i32, _i32]),
+    "k3_hip_cache_destroy": (None, [_vp]),
+    "k3_hip_cache_plan": (_i32, [_vp, _u64, _i32, _vp, _i32, _vp, C.POINTER(_i32)]),
+    "k3_hip_cache_fetch": (_i32, [_vp, _u64, _vp, _i32]),
+    "k3_hip_cache_resolve": (_i32, [_vp, _u64, _vp, _i32, _vp, _vp]),
+    "k3_hip_cache_ready_subset": (_i32, [_vp, _u64, _vp, _i32, _vp]),
+    "k3_hip_cache_release": (None, [_vp, _u64]),
+    "k3_hip_cache_stats": (None, [_vp, C.POINTER(C.c_longlong)]),
+    "k3_hip_cache_read_back": (_i32, [_vp, _i32, C.c_uint16, _vp, _u64]),
+    "k3_hip_synth_bank": (_i32, [_GP, _vp, _u64, _i32, _u64, _u64, _i32, _i32, _vp]),
+    "k3_hip_synth_normal": (_i32, [_vp, _i32, _u64, _u64, _u64, _vp]),
+}
+
+_LIB: C.CDLL | None = None
+
+
+class K3HipError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        super().__init__(f"{what} failed with status {status}: {last_error()}")
+        self.status = status
+
+
+def _hip_runtimes_mapped() -> set[str]:
+    paths = set()
+    try:
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64.so" in line:
+                    paths.add(os.path.realpath(line.split()[-1]))
+    except OSError:
+        pass
+    return paths
+
+
+def load() -> C.CDLL:
+    """Load the library once; raises if it is missing (run deltafin_amd.build)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    try:  # bind to torch's HIP runtime when torch is present
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m deltafin_amd.build` "
+            "(the gfx950 library has no CPU fallback)")
+    lib = C.CDLL(str(LIB_PATH))
+    runtimes = _hip_runtimes_mapped()
+    if len(runtimes) > 1:
+        raise ImportError(f"two HIP runtimes are mapped in this process: {sorted(runtimes)}")
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def last_error() -> str:
+    lib = _LIB if _LIB is not None else load()
+    msg = lib.k3_hip_last_error()
+    return msg.decode(errors="replace") if msg else ""
+
+
+def check(status: int, what: str) -> None:
+    if status != K3_HIP_OK:
+        raise K3HipError(status, what)
+
+
+def geometry(hidden: int, intermediate: int, activation: int) -> K3HipGeometryV1:
+    g = K3HipGeometryV1()
+    g.abi_version = 1
+    g.struct_bytes = C.sizeof(K3HipGeometryV1)
+    g.hidden = hidden
+    g.intermediate = intermediate
+    g.activation = activation
+    g.reserved = 0
+    g.expert_span = load().k3_hip_geometry_span(hidden, intermediate)
+    return g
+
+
+def preset(which: int) -> K3HipGeometryV1:
+    g = K3HipGeometryV1()
+    check(load().k3_hip_geometry_preset(which, C.byref(g)), "k3_hip_geometry_preset")
+    return g

@@ -1,0 +1,863 @@
+// Host side of the C ABI declared in include/k3_hip_moe_abi.h.
+//
+// Surface 2 (device pointers, caller stream) is stateless: it validates, carves
+// the caller's workspace and launches.  Surface 1 (host-synchronous
+// descriptors) owns one context guarded by a mutex, like the Metal bridge's
+// global state (tools/metal_moe.mm:170-200): a stream, pinned staging for
+// activations, a device workspace and an HBM cache of uploaded host blobs
+// keyed by pointer (the counterpart of the Metal wrap cache, :584-616).
+#include <hip/hip_runtime_api.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "k3_internal.h"
+
+namespace k3 {
+
+// ---------------------------------------------------------------- errors
+namespace {
+thread_local char g_last_error[512] = "no error";
+}
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int hip_fail(const char* what, hipError_t e) {
+  return fail(K3_HIP_E_EXEC, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------- geometry
+bool make_geo(const K3HipGeometryV1* d, Geo* out) {
+  if (!d || d->abi_version != 1 || d->struct_bytes != sizeof(K3HipGeometryV1) ||
+      d->reserved != 0 || d->hidden == 0 || d->intermediate == 0 || d->hidden % 32 != 0 ||
+      d->intermediate % 32 != 0 || d->hidden > 8192 || d->intermediate > 8192 ||
+      (d->activation != K3_ACT_SITU && d->activation != K3_ACT_SILU))
+    return false;
+  Geo g;
+  g.hidden = (int)d->hidden;
+  g.inter = (int)d->intermediate;
+  g.act = (int)d->activation;
+  const uint64_t w13p = (uint64_t)g.inter * g.hidden / 2, w13s = (uint64_t)g.inter * (g.hidden / 32);
+  const uint64_t w2p = (uint64_t)g.hidden * g.inter / 2, w2s = (uint64_t)g.hidden * (g.inter / 32);
+  g.w1p = 0;
+  g.w1s = w13p;
+  g.w2p = g.w1s + w13s;
+  g.w2s = g.w2p + w2p;
+  g.w3p = g.w2s + w2s;
+  g.w3s = g.w3p + w13p;
+  g.span = g.w3s + w13s;
+  if (d->expert_span != g.span) return false;
+  *out = g;
+  return true;
+}
+
+namespace {
+uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
+}
+
+uint64_t workspace_bytes(const Geo& g, int max_edges, int max_positions) {
+  const uint64_t E = (uint64_t)std::max(max_edges, 1), P = (uint64_t)std::max(max_positions, 1);
+  uint64_t b = 0;
+  b += align256(E * g.inter * 4);   // h
+  b += align256(E * g.hidden * 4);  // y
+  b += align256(E * 4);             // ids
+  b += align256(E * 4);             // w
+  b += align256(E * 8);             // uptr
+  b += align256((E + 1) * 4);       // uoff
+  b += align256(E * 4);             // uedges
+  b += align256(E * 4);             // epos
+  b += align256((P + 1) * 4);       // poff
+  b += align256(sizeof(VerifyPlanDev));
+  return b;
+}
+
+bool carve_workspace(void* base, uint64_t bytes, const Geo& g, int max_edges, int max_positions,
+                     Workspace* ws) {
+  if (!base || ((uintptr_t)base & 255u) != 0) return false;
+  if (bytes < workspace_bytes(g, max_edges, max_positions)) return false;
+  const uint64_t E = (uint64_t)std::max(max_edges, 1), P = (uint64_t)std::max(max_positions, 1);
+  uint8_t* p = static_cast<uint8_t*>(base);
+  auto take = [&](uint64_t n) {
+    uint8_t* r = p;
+    p += align256(n);
+    return r;
+  };
+  ws->base = static_cast<uint8_t*>(base);
+  ws->bytes = bytes;
+  ws->h = reinterpret_cast<float*>(take(E * g.inter * 4));
+  ws->y = reinterpret_cast<float*>(take(E * g.hidden * 4));
+  ws->ids = reinterpret_cast<int32_t*>(take(E * 4));
+  ws->w = reinterpret_cast<float*>(take(E * 4));
+  ws->uptr = reinterpret_cast<const uint8_t**>(take(E * 8));
+  ws->uoff = reinterpret_cast<int32_t*>(take((E + 1) * 4));
+  ws->uedges = reinterpret_cast<int32_t*>(take(E * 4));
+  ws->epos = reinterpret_cast<int32_t*>(take(E * 4));
+  ws->poff = reinterpret_cast<int32_t*>(take((P + 1) * 4));
+  ws->plan = reinterpret_cast<VerifyPlanDev*>(take(sizeof(VerifyPlanDev)));
+  return true;
+}
+
+int device_cu_count() {
+  static std::mutex mu;
+  static std::unordered_map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  cache[dev] = cus;
+  return cus;
+}
+
+namespace {
+
+bool geometry_from(const K3HipGeometryV1* g, Geo* out);
+
+// ---------------------------------------------------------------- presets
+void fill_geometry(uint32_t hidden, uint32_t inter, uint32_t act, K3HipGeometryV1* out) {
+  memset(out, 0, sizeof(*out));
+  out->abi_version = 1;
+  out->struct_bytes = sizeof(K3HipGeometryV1);
+  out->hidden = hidden;
+  out->intermediate = inter;
+  out->activation = act;
+  out->expert_span = k3_hip_geometry_span(hidden, inter);
+}
+
+// ---------------------------------------------------------------- surface 1 context
+struct BlobEntry {
+  uint8_t* dev = nullptr;
+  uint64_t span = 0;
+  uint64_t last_use = 0;
+};
+
+struct Context {
+  std::mutex mu;
+  bool tried = false, ok = false;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  K3HipGeometryV1 gdesc{};
+  Geo geo{};
+  void* ws = nullptr;
+  uint64_t ws_bytes = 0;
+  float* dx = nullptr;     // [K3_HIP_MAX_POSITIONS * H] fp32
+  float* dout = nullptr;   // [K3_HIP_MAX_POSITIONS * H] fp32
+  float* hx = nullptr;     // pinned staging, same size
+  float* hout = nullptr;
+  uint64_t act_elems = 0;
+  int cache_mode = 1;
+  uint64_t cache_capacity = 0;  // entries
+  std::unordered_map<const uint8_t*, BlobEntry> blobs;
+  uint64_t clock = 0;
+  long long calls = 0, device_uses = 0, uploads = 0;
+};
+
+Context& ctx() {
+  static Context c;
+  return c;
+}
+
+void release_buffers_locked(Context& c) {
+  for (auto& kv : c.blobs) (void)hipFree(kv.second.dev);
+  c.blobs.clear();
+  if (c.ws) (void)hipFree(c.ws);
+  if (c.dx) (void)hipFree(c.dx);
+  if (c.dout) (void)hipFree(c.dout);
+  if (c.hx) (void)hipHostFree(c.hx);
+  if (c.hout) (void)hipHostFree(c.hout);
+  c.ws = nullptr;
+  c.dx = c.dout = c.hx = c.hout = nullptr;
+  c.ws_bytes = 0;
+  c.act_elems = 0;
+}
+
+// (Re)size the geometry-dependent buffers for c.geo.
+int allocate_buffers_locked(Context& c) {
+  release_buffers_locked(c);
+  hipError_t e = hipSetDevice(c.device);
+  if (e != hipSuccess) return hip_fail("hipSetDevice", e);
+  c.ws_bytes = workspace_bytes(c.geo, K3_HIP_MAX_EDGES, K3_HIP_MAX_POSITIONS);
+  c.act_elems = (uint64_t)K3_HIP_MAX_POSITIONS * c.geo.hidden;
+  if ((e = hipMalloc(&c.ws, c.ws_bytes)) != hipSuccess ||
+      (e = hipMemset(c.ws, 0, c.ws_bytes)) != hipSuccess ||
+      (e = hipMalloc(reinterpret_cast<void**>(&c.dx), c.act_elems * 4)) != hipSuccess ||
+      (e = hipMalloc(reinterpret_cast<void**>(&c.dout), c.act_elems * 4)) != hipSuccess ||
+      (e = hipHostMalloc(reinterpret_cast<void**>(&c.hx), c.act_elems * 4, hipHostMallocDefault)) !=
+          hipSuccess ||
+      (e = hipHostMalloc(reinterpret_cast<void**>(&c.hout), c.act_elems * 4,
+                         hipHostMallocDefault)) != hipSuccess) {
+    const int rc = fail(K3_HIP_E_ALLOC, "surface-1 buffer allocation: %s", hipGetErrorString(e));
+    release_buffers_locked(c);
+    return rc;
+  }
+  size_t free_b = 0, total_b = 0;
+  if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) free_b = 0;
+  const uint64_t reserve = std::max<uint64_t>(uint64_t(2) << 30, free_b / 5);
+  const uint64_t usable = free_b > reserve ? free_b - reserve : 0;
+  // The reference bounds residency at 92 layers x 16 experts
+  // (provider_cuda_moe.cpp:54-56); keep the same ceiling.
+  c.cache_capacity = std::min<uint64_t>(usable / c.geo.span, 92 * 16);
+  return K3_HIP_OK;
+}
+
+bool init_locked(Context& c, const char* selector) {
+  if (c.tried) return c.ok;
+  c.tried = true;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0) {
+    fail(K3_HIP_E_INIT, "no HIP device: %s", e == hipSuccess ? "count is 0" : hipGetErrorString(e));
+    return false;
+  }
+  int dev = 0;
+  if (selector && *selector) {
+    char* end = nullptr;
+    const long v = strtol(selector, &end, 10);
+    if (!end || *end != '\0' || v < 0 || v >= count) {
+      fail(K3_HIP_E_INIT, "invalid device selector '%s'", selector);
+      return false;
+    }
+    dev = (int)v;
+  }
+  if (k3_hip_moe_available(dev) != 1) return false;
+  c.device = dev;
+  if ((e = hipSetDevice(dev)) != hipSuccess) {
+    hip_fail("hipSetDevice", e);
+    return false;
+  }
+  if ((e = hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking)) != hipSuccess) {
+    hip_fail("hipStreamCreate", e);
+    return false;
+  }
+  fill_geometry(3584, 3072, K3_ACT_SITU, &c.gdesc);
+  make_geo(&c.gdesc, &c.geo);
+  if (allocate_buffers_locked(c) != K3_HIP_OK) return false;
+  c.ok = true;
+  return true;
+}
+
+// Classify a blob pointer: 0 = pageable host, 1 = pinned host, 2 = device.
+int classify(const void* p) {
+  hipPointerAttribute_t attr;
+  memset(&attr, 0, sizeof(attr));
+  const hipError_t e = hipPointerGetAttributes(&attr, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged) return 2;
+  if (attr.type == hipMemoryTypeHost) return 1;
+  return 0;
+}
+
+void evict_one_locked(Context& c, const std::vector<const uint8_t*>& keep) {
+  auto victim = c.blobs.end();
+  for (auto it = c.blobs.begin(); it != c.blobs.end(); ++it) {
+    if (std::find(keep.begin(), keep.end(), it->first) != keep.end()) continue;
+    if (victim == c.blobs.end() || it->second.last_use < victim->second.last_use) victim = it;
+  }
+  if (victim != c.blobs.end()) {
+    (void)hipFree(victim->second.dev);
+    c.blobs.erase(victim);
+  }
+}
+
+// Device address for one blob; uploads host blobs into the HBM cache.
+// `temps` collects uncached uploads to free after the call.
+int resolve_blob_locked(Context& c, const uint8_t* blob, const std::vector<const uint8_t*>& call,
+                        const uint8_t** out, std::vector<uint8_t*>* temps) {
+  const int kind = classify(blob);
+  if (kind == 2) {
+    ++c.device_uses;
+    *out = blob;
+    return K3_HIP_OK;
+  }
+  auto it = c.blobs.find(blob);
+  if (it != c.blobs.end() && it->second.span == c.geo.span && c.cache_mode == 1) {
+    it->second.last_use = ++c.clock;
+    *out = it->second.dev;
+    return K3_HIP_OK;
+  }
+  if (it != c.blobs.end()) {
+    (void)hipFree(it->second.dev);
+    c.blobs.erase(it);
+  }
+  const bool keep = c.cache_mode == 1 && c.cache_capacity > 0;
+  if (keep) {
+    while (c.blobs.size() >= c.cache_capacity && !c.blobs.empty()) {
+      const size_t before = c.blobs.size();
+      evict_one_locked(c, call);
+      if (c.blobs.size() == before) break;
+    }
+  }
+  uint8_t* dev = nullptr;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&dev), c.geo.span);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(K3_HIP_E_ALLOC, "expert upload allocation: %s", hipGetErrorString(e));
+  }
+  e = kind == 1 ? hipMemcpyAsync(dev, blob, c.geo.span, hipMemcpyHostToDevice, c.stream)
+                : hipMemcpy(dev, blob, c.geo.span, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(dev);
+    return fail(K3_HIP_E_COPY, "expert upload: %s", hipGetErrorString(e));
+  }
+  ++c.uploads;
+  if (keep) {
+    BlobEntry be;
+    be.dev = dev;
+    be.span = c.geo.span;
+    be.last_use = ++c.clock;
+    c.blobs[blob] = be;
+  } else {
+    temps->push_back(dev);
+  }
+  *out = dev;
+  return K3_HIP_OK;
+}
+
+int finish_call_locked(Context& c, std::vector<uint8_t*>& temps, int rc) {
+  const hipError_t e = hipStreamSynchronize(c.stream);
+  for (uint8_t* t : temps) (void)hipFree(t);
+  if (rc != K3_HIP_OK) return rc;
+  if (e != hipSuccess) return fail(K3_HIP_E_EXEC, "surface-1 execution: %s", hipGetErrorString(e));
+  return K3_HIP_OK;
+}
+
+// Descriptor validation (tools/metal_moe.mm:407-450).
+int check_descriptors(const Context& c, const K3HipExpertDescriptorV1* d, int count,
+                      std::vector<const uint8_t*>* blobs) {
+  if (count < 0 || (count > 0 && !d))
+    return fail(K3_HIP_E_DESCRIPTOR, "invalid expert descriptor array");
+  blobs->clear();
+  for (int i = 0; i < count; ++i) {
+    if (d[i].abi_version != K3_DESCRIPTOR_ABI_V1 ||
+        d[i].struct_bytes != sizeof(K3HipExpertDescriptorV1) || d[i].reserved != 0 ||
+        !d[i].blob)
+      return fail(K3_HIP_E_DESCRIPTOR, "invalid expert descriptor fields (index %d)", i);
+    if (d[i].layout_id == K3_LAYOUT_SCALE4_V2)
+      return fail(K3_HIP_E_CAPABILITY, "scale4-v2 layout is not supported by this build");
+    if (d[i].layout_id != K3_LAYOUT_RAW_V1 || d[i].blob_bytes != c.geo.span)
+      return fail(K3_HIP_E_DESCRIPTOR, "unknown expert layout or byte length (index %d)", i);
+    blobs->push_back(d[i].blob);
+  }
+  return K3_HIP_OK;
+}
+
+int layer_locked(Context& c, const uint8_t* const* blobs, int n, const float* weights,
+                 const float* x, float* out) {
+  if (!x || !out || n < 0) return fail(K3_HIP_E_INVALID, "layer: null input/output or n < 0");
+  const size_t hb = (size_t)c.geo.hidden * 4;
+  if (n == 0) {
+    memset(out, 0, hb);
+    return K3_HIP_OK;
+  }
+  if (!blobs || !weights) return fail(K3_HIP_E_INVALID, "layer: null blobs or weights");
+  if (n > K3_HIP_MAX_TOKEN_EXPERTS)
+    return fail(K3_HIP_E_INVALID, "layer: %d experts exceeds %d", n, K3_HIP_MAX_TOKEN_EXPERTS);
+  hipError_t e = hipSetDevice(c.device);
+  if (e != hipSuccess) return hip_fail("hipSetDevice", e);
+  std::vector<const uint8_t*> call(blobs, blobs + n);
+  std::vector<uint8_t*> temps;
+  TokenRoute route;
+  memset(&route, 0, sizeof(route));
+  route.n = n;
+  for (int i = 0; i < n; ++i) {
+    if (!blobs[i]) return fail(K3_HIP_E_INVALID, "layer: null blob %d", i);
+    const int rc = resolve_blob_locked(c, blobs[i], call, &route.ptr[i], &temps);
+    if (rc != K3_HIP_OK) return finish_call_locked(c, temps, rc);
+    route.w[i] = weights[i];
+  }
+  memcpy(c.hx, x, hb);
+  if ((e = hipMemcpyAsync(c.dx, c.hx, hb, hipMemcpyHostToDevice, c.stream)) != hipSuccess)
+    return finish_call_locked(c, temps, fail(K3_HIP_E_COPY, "layer input copy: %s", hipGetErrorString(e)));
+  Workspace ws;
+  carve_workspace(c.ws, c.ws_bytes, c.geo, K3_HIP_MAX_EDGES, K3_HIP_MAX_POSITIONS, &ws);
+  int rc = launch_decode_layer(c.geo, route, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws, c.stream);
+  if (rc == K3_HIP_OK &&
+      (e = hipMemcpyAsync(c.hout, c.dout, hb, hipMemcpyDeviceToHost, c.stream)) != hipSuccess)
+    rc = fail(K3_HIP_E_COPY, "layer output copy: %s", hipGetErrorString(e));
+  rc = finish_call_locked(c, temps, rc);
+  if (rc != K3_HIP_OK) return rc;
+  memcpy(out, c.hout, hb);
+  ++c.calls;
+  return K3_HIP_OK;
+}
+
+int positions_locked(Context& c, const uint8_t* const* blobs, int n_edges, const int* offs,
+                     int n_pos, const float* weights, const float* x, float* out) {
+  // Offset validation mirrors tools/metal_moe.mm:852-871.
+  if (n_edges < 0 || n_pos < 0) return fail(K3_HIP_E_INVALID, "positions: negative counts");
+  if (n_pos == 0) return n_edges == 0 ? K3_HIP_OK : fail(K3_HIP_E_INVALID, "positions: edges without positions");
+  if (!offs || !x || !out) return fail(K3_HIP_E_INVALID, "positions: null offsets/input/output");
+  if (n_pos > K3_HIP_MAX_POSITIONS || n_edges > K3_HIP_MAX_EDGES)
+    return fail(K3_HIP_E_INVALID, "positions: at most %d positions and %d edges",
+                K3_HIP_MAX_POSITIONS, K3_HIP_MAX_EDGES);
+  if (offs[0] != 0) return fail(K3_HIP_E_INVALID, "positions: offsets must start at 0");
+  for (int p = 0; p < n_pos; ++p)
+    if (offs[p] < 0 || offs[p] > offs[p + 1] || offs[p + 1] > n_edges)
+      return fail(K3_HIP_E_INVALID, "positions: offsets are not a partition");
+  if (offs[n_pos] != n_edges) return fail(K3_HIP_E_INVALID, "positions: offsets must end at edge count");
+  if (n_edges > 0 && (!blobs || !weights)) return fail(K3_HIP_E_INVALID, "positions: null blobs/weights");
+  const size_t bytes = (size_t)n_pos * c.geo.hidden * 4;
+  if (n_edges == 0) {
+    memset(out, 0, bytes);
+    return K3_HIP_OK;
+  }
+  hipError_t e = hipSetDevice(c.device);
+  if (e != hipSuccess) return hip_fail("hipSetDevice", e);
+  std::vector<const uint8_t*> call(blobs, blobs + n_edges);
+  std::vector<uint8_t*> temps;
+  EdgeTable tbl;
+  memset(&tbl, 0, sizeof(tbl));
+  tbl.n_edges = n_edges;
+  tbl.n_positions = n_pos;
+  for (int p = 0; p <= n_pos; ++p) tbl.pos_off[p] = offs[p];
+  for (int i = 0; i < n_edges; ++i) {
+    if (!blobs[i]) return fail(K3_HIP_E_INVALID, "positions: null blob %d", i);
+    // Repeated blobs resolve to the same device address, so the plan groups them.
+    const int rc = resolve_blob_locked(c, blobs[i], call, &tbl.ptr[i], &temps);
+    if (rc != K3_HIP_OK) return finish_call_locked(c, temps, rc);
+    tbl.w[i] = weights[i];
+  }
+  memcpy(c.hx, x, bytes);
+  if ((e = hipMemcpyAsync(c.dx, c.hx, bytes, hipMemcpyHostToDevice, c.stream)) != hipSuccess)
+    return finish_call_locked(c, temps, fail(K3_HIP_E_COPY, "positions input copy: %s", hipGetErrorString(e)));
+  Workspace ws;
+  carve_workspace(c.ws, c.ws_bytes, c.geo, K3_HIP_MAX_EDGES, K3_HIP_MAX_POSITIONS, &ws);
+  int rc = launch_verify_plan_table(tbl, ws, c.stream);
+  if (rc == K3_HIP_OK)
+    rc = launch_verify_layer(c.geo, n_edges, n_pos, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws,
+                             c.stream);
+  if (rc == K3_HIP_OK &&
+      (e = hipMemcpyAsync(c.hout, c.dout, bytes, hipMemcpyDeviceToHost, c.stream)) != hipSuccess)
+    rc = fail(K3_HIP_E_COPY, "positions output copy: %s", hipGetErrorString(e));
+  rc = finish_call_locked(c, temps, rc);
+  if (rc != K3_HIP_OK) return rc;
+  memcpy(out, c.hout, bytes);
+  c.calls += n_pos;
+  return K3_HIP_OK;
+}
+
+bool geometry_from(const K3HipGeometryV1* g, Geo* out) {
+  if (g) return make_geo(g, out);
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  K3HipGeometryV1 d = c.gdesc;
+  if (!c.tried) fill_geometry(3584, 3072, K3_ACT_SITU, &d);
+  return make_geo(&d, out);
+}
+
+int check_dtype(int d) { return d == K3_DTYPE_F32 || d == K3_DTYPE_BF16; }
+
+}  // namespace
+}  // namespace k3
+
+using namespace k3;
+
+extern "C" {
+
+uint64_t k3_hip_geometry_span(uint32_t hidden, uint32_t intermediate) {
+  if (hidden == 0 || intermediate == 0 || hidden % 32 != 0 || intermediate % 32 != 0) return 0;
+  const uint64_t h = hidden, i = intermediate;
+  return 2 * (i * h / 2 + i * (h / 32)) + (h * i / 2 + h * (i / 32));
+}
+
+int k3_hip_geometry_preset(int preset, K3HipGeometryV1* out) {
+  if (!out) return fail(K3_HIP_E_INVALID, "null geometry output");
+  if (preset == 1) {
+    fill_geometry(3584, 3072, K3_ACT_SITU, out);
+    return K3_HIP_OK;
+  }
+  if (preset == 2) {
+    fill_geometry(7168, 2048, K3_ACT_SILU, out);
+    return K3_HIP_OK;
+  }
+  return fail(K3_HIP_E_INVALID, "unknown geometry preset %d", preset);
+}
+
+const char* k3_hip_last_error(void) { return g_last_error; }
+
+// ------------------------------------------------------------ surface 1
+int k3_hip_init(const char* selector) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  return init_locked(c, selector) ? 0 : -1;
+}
+
+int k3_hip_available(void) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  return init_locked(c, nullptr) ? 1 : 0;
+}
+
+uint32_t k3_hip_descriptor_abi_version(void) { return K3_DESCRIPTOR_ABI_V1; }
+
+uint64_t k3_hip_layout_capabilities(void) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (!init_locked(c, nullptr)) return 0;
+  return K3_CAP_RAW_V1;
+}
+
+int k3_hip_configure_v1(const K3HipGeometryV1* geometry) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  Geo g;
+  if (!make_geo(geometry, &g)) return fail(K3_HIP_E_INVALID, "invalid geometry descriptor");
+  if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
+  c.gdesc = *geometry;
+  c.geo = g;
+  return allocate_buffers_locked(c);
+}
+
+void k3_hip_shapes(int* hidden, int* inter, long long* span) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  K3HipGeometryV1 d = c.gdesc;
+  if (!c.tried) fill_geometry(3584, 3072, K3_ACT_SITU, &d);
+  if (hidden) *hidden = (int)d.hidden;
+  if (inter) *inter = (int)d.intermediate;
+  if (span) *span = (long long)d.expert_span;
+}
+
+void k3_hip_stats(long long* five) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (!five) return;
+  five[0] = c.calls;
+  five[1] = c.device_uses;
+  five[2] = c.uploads;
+  five[3] = (long long)c.blobs.size();
+  five[4] = c.cache_mode;
+}
+
+int k3_hip_mode(void) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  return c.cache_mode;
+}
+
+int k3_hip_set_mode(int cache_host_blobs) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (!init_locked(c, nullptr)) return -1;
+  c.cache_mode = cache_host_blobs ? 1 : 0;
+  if (!c.cache_mode) {
+    for (auto& kv : c.blobs) (void)hipFree(kv.second.dev);
+    c.blobs.clear();
+  }
+  return c.cache_mode;
+}
+
+void k3_hip_drop(const uint8_t* blob) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  auto it = c.blobs.find(blob);
+  if (it == c.blobs.end()) return;
+  (void)hipStreamSynchronize(c.stream);
+  (void)hipFree(it->second.dev);
+  c.blobs.erase(it);
+}
+
+void k3_hip_flush(void) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (c.blobs.empty()) return;
+  (void)hipStreamSynchronize(c.stream);
+  for (auto& kv : c.blobs) (void)hipFree(kv.second.dev);
+  c.blobs.clear();
+}
+
+int k3_hip_moe_layer_desc_v1(const K3HipExpertDescriptorV1* experts, int expert_count,
+                             const float* weights, const float* input, float* output) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
+  std::vector<const uint8_t*> blobs;
+  const int rc = check_descriptors(c, experts, expert_count, &blobs);
+  if (rc != K3_HIP_OK) return rc;
+  return layer_locked(c, blobs.empty() ? nullptr : blobs.data(), expert_count, weights, input,
+                      output);
+}
+
+int k3_hip_moe_positions_desc_v1(const K3HipExpertDescriptorV1* experts, int edge_count,
+                                 const int* position_offsets, int position_count,
+                                 const float* weights, const float* input, float* output) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
+  std::vector<const uint8_t*> blobs;
+  const int rc = check_descriptors(c, experts, edge_count, &blobs);
+  if (rc != K3_HIP_OK) return rc;
+  return positions_locked(c, blobs.empty() ? nullptr : blobs.data(), edge_count,
+                          position_offsets, position_count, weights, input, output);
+}
+
+int k3_hip_moe_layer(const uint8_t* const* expert_blobs, int n_experts, const float* weights,
+                     const float* x, float* out) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
+  return layer_locked(c, expert_blobs, n_experts, weights, x, out);
+}
+
+int k3_hip_moe_positions(const uint8_t* const* expert_blobs, int n_edges,
+                         const int* position_offsets, int n_positions, const float* weights,
+                         const float* x, float* out) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
+  return positions_locked(c, expert_blobs, n_edges, position_offsets, n_positions, weights, x,
+                          out);
+}
+
+// ------------------------------------------------------------ surface 2
+uint32_t k3_hip_moe_abi_version(void) { return 1; }
+
+void k3_hip_moe_shapes(int* hidden, int* intermediate, int64_t* expert_span,
+                       uint32_t* pointer_layout) {
+  int h = 0, i = 0;
+  long long s = 0;
+  k3_hip_shapes(&h, &i, &s);
+  if (hidden) *hidden = h;
+  if (intermediate) *intermediate = i;
+  if (expert_span) *expert_span = s;
+  if (pointer_layout) *pointer_layout = 1;
+}
+
+int k3_hip_moe_available(int device) {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess) return fail(K3_HIP_E_INIT, "device count query: %s", hipGetErrorString(e));
+  if (device < 0 || device >= count)
+    return fail(K3_HIP_E_INVALID, "device %d outside the %d visible devices", device, count);
+  hipDeviceProp_t prop;
+  if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess)
+    return fail(K3_HIP_E_INIT, "device properties: %s", hipGetErrorString(e));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(K3_HIP_E_CAPABILITY, "device %d is %s; this library is built for gfx950 only",
+                device, prop.gcnArchName);
+  fail(K3_HIP_OK, "available: device %d %s, %d CUs, wave %d", device, prop.gcnArchName,
+       prop.multiProcessorCount, prop.warpSize);
+  return 1;
+}
+
+int k3_hip_mxfp4_gemv(const uint8_t* packed, const uint8_t* scales, const float* x,
+                      float* output, int rows, int cols, int batches, void* stream) {
+  return launch_gemv(packed, scales, x, K3_DTYPE_F32, output, K3_DTYPE_F32, rows, cols, batches,
+                     static_cast<hipStream_t>(stream));
+}
+
+int k3_hip_mxfp4_gemv_ex(const uint8_t* packed, const uint8_t* scales, const void* x,
+                         int x_dtype, void* output, int out_dtype, int rows, int cols,
+                         int batches, void* stream) {
+  return launch_gemv(packed, scales, x, x_dtype, output, out_dtype, rows, cols, batches,
+                     static_cast<hipStream_t>(stream));
+}
+
+int k3_hip_moe_launch(const K3HipGeometryV1* gd, const uint8_t* span, const float* x,
+                      int batches, float* gate, float* up, float* out, void* stream) {
+  Geo g;
+  if (!geometry_from(gd, &g)) return fail(K3_HIP_E_INVALID, "invalid geometry");
+  if (!span || !x || !gate || !up || !out)
+    return fail(K3_HIP_E_INVALID, "device MoE: null input, scratch, or output pointer");
+  if (batches <= 0) return fail(K3_HIP_E_INVALID, "device MoE: batch count must be positive");
+  if (((uintptr_t)span & 15u) != 0 || ((uintptr_t)gate & 15u) != 0)
+    return fail(K3_HIP_E_INVALID, "device MoE: span and gate must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = launch_gemv(span + g.w1p, span + g.w1s, x, K3_DTYPE_F32, gate, K3_DTYPE_F32, g.inter,
+                       g.hidden, batches, st);
+  if (rc == K3_HIP_OK)
+    rc = launch_gemv(span + g.w3p, span + g.w3s, x, K3_DTYPE_F32, up, K3_DTYPE_F32, g.inter,
+                     g.hidden, batches, st);
+  if (rc == K3_HIP_OK)
+    rc = launch_activation(gate, up, gate, (int64_t)batches * g.inter, g.act, st);
+  if (rc == K3_HIP_OK)
+    rc = launch_gemv(span + g.w2p, span + g.w2s, gate, K3_DTYPE_F32, out, K3_DTYPE_F32, g.hidden,
+                     g.inter, batches, st);
+  return rc;
+}
+
+uint64_t k3_hip_moe_workspace_bytes(const K3HipGeometryV1* gd, int max_edges, int max_positions) {
+  Geo g;
+  if (!geometry_from(gd, &g)) return 0;
+  return workspace_bytes(g, max_edges, max_positions);
+}
+
+int k3_hip_moe_layer_device(const K3HipGeometryV1* gd, const uint8_t* const* experts,
+                            const float* weights, int n_experts, const void* x, int x_dtype,
+                            void* out, int out_dtype, void* workspace, uint64_t workspace_bytes,
+                            void* stream) {
+  Geo g;
+  if (!geometry_from(gd, &g)) return fail(K3_HIP_E_INVALID, "invalid geometry");
+  if (!experts || !weights || !x || !out)
+    return fail(K3_HIP_E_INVALID, "layer: null experts/weights/x/out");
+  if (n_experts <= 0 || n_experts > K3_HIP_MAX_TOKEN_EXPERTS)
+    return fail(K3_HIP_E_INVALID, "layer: expert count %d outside [1, %d]", n_experts,
+                K3_HIP_MAX_TOKEN_EXPERTS);
+  if (!check_dtype(x_dtype) || !check_dtype(out_dtype))
+    return fail(K3_HIP_E_INVALID, "layer: unknown dtype");
+  if (((uintptr_t)x & 15u) != 0) return fail(K3_HIP_E_INVALID, "layer: x must be 16-byte aligned");
+  Workspace ws;
+  if (!carve_workspace(workspace, workspace_bytes, g, n_experts, 1, &ws))
+    return fail(K3_HIP_E_INVALID, "layer: workspace missing, misaligned or smaller than %llu bytes",
+                (unsigned long long)k3::workspace_bytes(g, n_experts, 1));
+  TokenRoute route;
+  memset(&route, 0, sizeof(route));
+  route.n = n_experts;
+  for (int i = 0; i < n_experts; ++i) {
+    if (!experts[i] || ((uintptr_t)experts[i] & 15u) != 0)
+      return fail(K3_HIP_E_INVALID, "layer: expert %d span is null or not 16-byte aligned", i);
+    route.ptr[i] = experts[i];
+    route.w[i] = weights[i];
+  }
+  return launch_decode_layer(g, route, x, x_dtype, out, out_dtype, ws,
+                             static_cast<hipStream_t>(stream));
+}
+
+int k3_hip_moe_route_layer_device(const K3HipGeometryV1* gd, const uint8_t* bank,
+                                  uint64_t expert_stride, int n_bank, const float* logits,
+                                  int top_k, const void* x, int x_dtype, void* out, int out_dtype,
+                                  int32_t* route_ids, float* route_weights, void* workspace,
+                                  uint64_t workspace_bytes, void* stream) {
+  Geo g;
+  if (!geometry_from(gd, &g)) return fail(K3_HIP_E_INVALID, "invalid geometry");
+  if (!bank || !logits || !x || !out) return fail(K3_HIP_E_INVALID, "route layer: null pointer");
+  if (expert_stride < g.span || expert_stride % 16 != 0 || ((uintptr_t)bank & 15u) != 0)
+    return fail(K3_HIP_E_INVALID, "route layer: bank must be 16-byte aligned with stride >= span");
+  if (!check_dtype(x_dtype) || !check_dtype(out_dtype))
+    return fail(K3_HIP_E_INVALID, "route layer: unknown dtype");
+  if (((uintptr_t)x & 15u) != 0) return fail(K3_HIP_E_INVALID, "route layer: x must be 16-byte aligned");
+  if (top_k <= 0 || top_k > K3_HIP_MAX_TOKEN_EXPERTS || top_k > n_bank)
+    return fail(K3_HIP_E_INVALID, "route layer: top_k %d outside [1, min(%d, n_bank)]", top_k,
+                K3_HIP_MAX_TOKEN_EXPERTS);
+  Workspace ws;
+  if (!carve_workspace(workspace, workspace_bytes, g, top_k, 1, &ws))
+    return fail(K3_HIP_E_INVALID, "route layer: workspace missing, misaligned or too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = launch_route(logits, n_bank, top_k, 1, ws.ids, ws.w, route_ids, route_weights, st);
+  if (rc != K3_HIP_OK) return rc;
+  TokenRoute route;
+  memset(&route, 0, sizeof(route));
+  route.bank = bank;
+  route.stride = expert_stride;
+  route.ids = ws.ids;
+  route.wdev = ws.w;
+  route.n = top_k;
+  return launch_decode_layer(g, route, x, x_dtype, out, out_dtype, ws, st);
+}
+
+int k3_hip_moe_verify_route_device(const K3HipGeometryV1* gd, const uint8_t* bank,
+                                   uint64_t expert_stride, int n_bank, const float* logits,
+                                   int n_positions, int top_k, const void* x, int x_dtype,
+                                   void* out, int out_dtype, int32_t* route_ids,
+                                   float* route_weights, void* workspace,
+                                   uint64_t workspace_bytes, void* stream) {
+  Geo g;
+  if (!geometry_from(gd, &g)) return fail(K3_HIP_E_INVALID, "invalid geometry");
+  if (!bank || !logits || !x || !out) return fail(K3_HIP_E_INVALID, "verify: null pointer");
+  if (expert_stride < g.span || expert_stride % 16 != 0 || ((uintptr_t)bank & 15u) != 0)
+    return fail(K3_HIP_E_INVALID, "verify: bank must be 16-byte aligned with stride >= span");
+  if (!check_dtype(x_dtype) || !check_dtype(out_dtype))
+    return fail(K3_HIP_E_INVALID, "verify: unknown dtype");
+  if (((uintptr_t)x & 15u) != 0) return fail(K3_HIP_E_INVALID, "verify: x must be 16-byte aligned");
+  if (n_positions <= 0 || n_positions > K3_HIP_MAX_POSITIONS)
+    return fail(K3_HIP_E_INVALID, "verify: positions %d outside [1, %d]", n_positions,
+                K3_HIP_MAX_POSITIONS);
+  if (top_k <= 0 || top_k > K3_HIP_MAX_TOKEN_EXPERTS || top_k > n_bank ||
+      n_positions * top_k > K3_HIP_MAX_EDGES)
+    return fail(K3_HIP_E_INVALID, "verify: top_k %d invalid for %d positions", top_k, n_positions);
+  const int n_edges = n_positions * top_k;
+  Workspace ws;
+  if (!carve_workspace(workspace, workspace_bytes, g, n_edges, n_positions, &ws))
+    return fail(K3_HIP_E_INVALID, "verify: workspace missing, misaligned or too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = launch_route(logits, n_bank, top_k, n_positions, ws.ids, ws.w, route_ids,
+                        route_weights, st);
+  if (rc == K3_HIP_OK) rc = launch_verify_plan_bank(g, bank, expert_stride, n_positions, top_k, ws, st);
+  if (rc == K3_HIP_OK)
+    rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
+  return rc;
+}
+
+int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* edge_experts,
+                             const float* edge_weights, const int* position_offsets,
+                             int n_positions, const void* x, int x_dtype, void* out,
+                             int out_dtype, void* workspace, uint64_t workspace_bytes,
+                             void* stream) {
+  Geo g;
+  if (!geometry_from(gd, &g)) return fail(K3_HIP_E_INVALID, "invalid geometry");
+  if (!position_offsets || !x || !out) return fail(K3_HIP_E_INVALID, "verify: null pointer");
+  if (!check_dtype(x_dtype) || !check_dtype(out_dtype))
+    return fail(K3_HIP_E_INVALID, "verify: unknown dtype");
+  if (((uintptr_t)x & 15u) != 0) return fail(K3_HIP_E_INVALID, "verify: x must be 16-byte aligned");
+  if (n_positions <= 0 || n_positions > K3_HIP_MAX_POSITIONS)
+    return fail(K3_HIP_E_INVALID, "verify: positions %d outside [1, %d]", n_positions,
+                K3_HIP_MAX_POSITIONS);
+  if (position_offsets[0] != 0) return fail(K3_HIP_E_INVALID, "verify: offsets must start at 0");
+  for (int p = 0; p < n_positions; ++p)
+    if (position_offsets[p] > position_offsets[p + 1])
+      return fail(K3_HIP_E_INVALID, "verify: offsets must be non-decreasing");
+  const int n_edges = position_offsets[n_positions];
+  if (n_edges < 0 || n_edges > K3_HIP_MAX_EDGES)
+    return fail(K3_HIP_E_INVALID, "verify: %d edges outside [0, %d]", n_edges, K3_HIP_MAX_EDGES);
+  if (n_edges > 0 && (!edge_experts || !edge_weights))
+    return fail(K3_HIP_E_INVALID, "verify: null edge arrays");
+  Workspace ws;
+  if (!carve_workspace(workspace, workspace_bytes, g, std::max(n_edges, 1), n_positions, &ws))
+    return fail(K3_HIP_E_INVALID, "verify: workspace missing, misaligned or too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n_edges == 0) {
+    const size_t bytes = (size_t)n_positions * g.hidden * (out_dtype == K3_DTYPE_BF16 ? 2 : 4);
+    const hipError_t e = hipMemsetAsync(out, 0, bytes, st);
+    return e == hipSuccess ? K3_HIP_OK : hip_fail("verify: zero output", e);
+  }
+  EdgeTable tbl;
+  memset(&tbl, 0, sizeof(tbl));
+  tbl.n_edges = n_edges;
+  tbl.n_positions = n_positions;
+  for (int p = 0; p <= n_positions; ++p) tbl.pos_off[p] = position_offsets[p];
+  for (int i = 0; i < n_edges; ++i) {
+    if (!edge_experts[i] || ((uintptr_t)edge_experts[i] & 15u) != 0)
+      return fail(K3_HIP_E_INVALID, "verify: edge %d span is null or misaligned", i);
+    tbl.ptr[i] = edge_experts[i];
+    tbl.w[i] = edge_weights[i];
+  }
+  int rc = launch_verify_plan_table(tbl, ws, st);
+  if (rc == K3_HIP_OK)
+    rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
+  return rc;
+}
+
+int k3_hip_synth_bank(const K3HipGeometryV1* gd, uint8_t* bank, uint64_t expert_stride,
+                      int n_experts, uint64_t first_expert, uint64_t seed, int scale_lo,
+                      int scale_hi, void* stream) {
+  Geo g;
+  if (!geometry_from(gd, &g)) return fail(K3_HIP_E_INVALID, "invalid geometry");
+  return launch_synth_bank(g, bank, expert_stride, n_experts, first_expert, seed, scale_lo,
+                           scale_hi, static_cast<hipStream_t>(stream));
+}
+
+int k3_hip_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed, uint64_t stream,
+                        void* stream_handle) {
+  return launch_synth_normal(out, dtype, n, seed, stream, static_cast<hipStream_t>(stream_handle));
+}
+
+}  // extern "C"

@@ -1,0 +1,354 @@
+// HBM expert cache: C counterpart of CudaMoeExpertCache
+// (native/provider_gate/provider_cuda_moe.{h,cpp}).
+//
+// * One slab of capacity x span bytes in HBM; a slot holds one expert span.
+// * Entries live in per-layer strata with a global recency clock; eviction picks
+//   the globally least-recent entry that no live plan pins
+//   (provider_cuda_moe.cpp:707-747).
+// * plan() snapshots hits before any miss can be admitted, pinning them for the
+//   plan's lifetime (:963-1008).
+// * fetch() admits misses with hipMemcpyAsync on the cache's own side stream,
+//   so copies overlap compute on the caller's stream; each slot records a ready
+//   event that resolve() makes the caller's stream wait on.  The reference
+//   copies on the execution stream through two pinned slabs (:757-805); here
+//   pinned sources are copied directly and pageable sources go through a ring
+//   of pinned staging slots.
+#include <hip/hip_runtime_api.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "k3_internal.h"
+
+using namespace k3;
+
+struct K3HipCache {
+  struct Slot {
+    int layer = -1;
+    int id = -1;
+    uint64_t last_use = 0;
+    int pins = 0;
+    hipEvent_t ready = nullptr;
+    bool has_event = false;
+  };
+  struct Plan {
+    int layer = 0;
+    std::vector<uint16_t> ids;      // canonical ascending
+    std::vector<int> hit_slots;     // pinned at plan time
+    std::vector<uint16_t> missing;  // ascending
+    std::vector<int> miss_slots;    // filled by fetch
+  };
+
+  std::mutex mu;
+  int device = 0;
+  uint64_t span = 0, slot_bytes = 0;
+  int capacity = 0;
+  int n_layers = 0;
+  uint8_t* slab = nullptr;
+  hipStream_t side = nullptr;
+  std::vector<Slot> slots;
+  std::vector<std::unordered_map<int, int>> strata;  // layer -> id -> slot
+  std::map<uint64_t, Plan> plans;
+  uint64_t clock = 0;
+  std::vector<uint8_t*> staging;
+  std::vector<hipEvent_t> staging_ready;
+  std::vector<bool> staging_used;
+  int staging_cursor = 0;
+  long long hits = 0, misses = 0, evictions = 0, uploaded = 0;
+
+  int resident() const {
+    int n = 0;
+    for (const Slot& s : slots) n += s.id >= 0;
+    return n;
+  }
+};
+
+namespace {
+
+int set_device(K3HipCache* c) {
+  const hipError_t e = hipSetDevice(c->device);
+  return e == hipSuccess ? K3_HIP_OK : hip_fail("cache hipSetDevice", e);
+}
+
+// Free slot, else the globally least-recent unpinned slot (evicted).
+int take_slot(K3HipCache* c) {
+  int victim = -1;
+  for (int i = 0; i < c->capacity; ++i) {
+    const K3HipCache::Slot& s = c->slots[i];
+    if (s.id < 0 && s.pins == 0) return i;
+    if (s.pins == 0 && (victim < 0 || s.last_use < c->slots[victim].last_use)) victim = i;
+  }
+  if (victim >= 0) {
+    K3HipCache::Slot& s = c->slots[victim];
+    c->strata[s.layer].erase(s.id);
+    s.layer = s.id = -1;
+    ++c->evictions;
+  }
+  return victim;
+}
+
+bool pinned_host(const void* p) {
+  hipPointerAttribute_t attr;
+  memset(&attr, 0, sizeof(attr));
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return attr.type == hipMemoryTypeHost;
+}
+
+}  // namespace
+
+extern "C" {
+
+K3HipCache* k3_hip_cache_create(int device, uint64_t span_bytes, int capacity_experts,
+                                int n_layers, int staging_slots) {
+  if (span_bytes == 0 || capacity_experts <= 0 || n_layers <= 0 || n_layers > 4096 ||
+      staging_slots < 0 || staging_slots > 16) {
+    fail(K3_HIP_E_INVALID, "cache: invalid span/capacity/layers/staging");
+    return nullptr;
+  }
+  if (k3_hip_moe_available(device) != 1) return nullptr;
+  K3HipCache* c = new K3HipCache();
+  c->device = device;
+  c->span = span_bytes;
+  c->slot_bytes = (span_bytes + 4095) & ~uint64_t(4095);
+  c->capacity = capacity_experts;
+  c->n_layers = n_layers;
+  c->slots.resize(capacity_experts);
+  c->strata.resize(n_layers);
+  hipError_t e = hipSetDevice(device);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->slab), c->slot_bytes * capacity_experts);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking);
+  for (int i = 0; e == hipSuccess && i < capacity_experts; ++i) {
+    e = hipEventCreateWithFlags(&c->slots[i].ready, hipEventDisableTiming);
+  }
+  for (int i = 0; e == hipSuccess && i < staging_slots; ++i) {
+    uint8_t* p = nullptr;
+    hipEvent_t ev = nullptr;
+    e = hipHostMalloc(reinterpret_cast<void**>(&p), span_bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e == hipSuccess) {
+      c->staging.push_back(p);
+      c->staging_ready.push_back(ev);
+      c->staging_used.push_back(false);
+    }
+  }
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    fail(K3_HIP_E_ALLOC, "cache allocation: %s", hipGetErrorString(e));
+    k3_hip_cache_destroy(c);
+    return nullptr;
+  }
+  return c;
+}
+
+void k3_hip_cache_destroy(K3HipCache* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->side) (void)hipStreamSynchronize(c->side);
+  for (auto& s : c->slots)
+    if (s.ready) (void)hipEventDestroy(s.ready);
+  for (size_t i = 0; i < c->staging.size(); ++i) {
+    (void)hipEventDestroy(c->staging_ready[i]);
+    (void)hipHostFree(c->staging[i]);
+  }
+  if (c->side) (void)hipStreamDestroy(c->side);
+  if (c->slab) (void)hipFree(c->slab);
+  delete c;
+}
+
+int k3_hip_cache_plan(K3HipCache* c, uint64_t plan_id, int layer, const uint16_t* ids, int n,
+                      uint16_t* missing_ids, int* n_missing) {
+  if (!c || plan_id == 0 || !ids || n <= 0 || n > c->capacity || !missing_ids || !n_missing)
+    return fail(K3_HIP_E_INVALID, "cache plan: invalid arguments (n must be in [1, capacity])");
+  if (layer < 0 || layer >= c->n_layers)
+    return fail(K3_HIP_E_INVALID, "cache plan: layer %d outside [0, %d)", layer, c->n_layers);
+  for (int i = 1; i < n; ++i)
+    if (ids[i - 1] >= ids[i])
+      return fail(K3_HIP_E_INVALID, "cache plan: ids must be canonical ascending IDs");
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (c->plans.count(plan_id)) return fail(K3_HIP_E_INVALID, "cache plan: plan id already live");
+  K3HipCache::Plan p;
+  p.layer = layer;
+  p.ids.assign(ids, ids + n);
+  for (int i = 0; i < n; ++i) {
+    auto it = c->strata[layer].find(ids[i]);
+    if (it != c->strata[layer].end()) {
+      K3HipCache::Slot& s = c->slots[it->second];
+      s.last_use = ++c->clock;
+      ++s.pins;
+      p.hit_slots.push_back(it->second);
+      ++c->hits;
+    } else {
+      p.missing.push_back(ids[i]);
+      p.hit_slots.push_back(-1);
+      ++c->misses;
+    }
+  }
+  for (size_t i = 0; i < p.missing.size(); ++i) missing_ids[i] = p.missing[i];
+  *n_missing = (int)p.missing.size();
+  c->plans.emplace(plan_id, std::move(p));
+  return K3_HIP_OK;
+}
+
+int k3_hip_cache_fetch(K3HipCache* c, uint64_t plan_id, const uint8_t* const* sources,
+                       int n_sources) {
+  if (!c) return fail(K3_HIP_E_INVALID, "cache fetch: null cache");
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto pit = c->plans.find(plan_id);
+  if (pit == c->plans.end()) return fail(K3_HIP_E_INVALID, "cache fetch: stale or unknown plan");
+  K3HipCache::Plan& p = pit->second;
+  if (!p.miss_slots.empty()) return fail(K3_HIP_E_INVALID, "cache fetch: plan already fetched");
+  if (n_sources != (int)p.missing.size() || (n_sources > 0 && !sources))
+    return fail(K3_HIP_E_INVALID, "cache fetch: %d sources for %zu misses", n_sources,
+                p.missing.size());
+  int rc = set_device(c);
+  if (rc != K3_HIP_OK) return rc;
+  for (int i = 0; i < n_sources; ++i) {
+    if (!sources[i]) return fail(K3_HIP_E_INVALID, "cache fetch: null source %d", i);
+    const int slot = take_slot(c);
+    if (slot < 0) return fail(K3_HIP_E_ALLOC, "cache fetch: every slot is pinned by live plans");
+    K3HipCache::Slot& s = c->slots[slot];
+    uint8_t* dst = c->slab + (uint64_t)slot * c->slot_bytes;
+    hipError_t e;
+    if (pinned_host(sources[i]) || c->staging.empty()) {
+      e = hipMemcpyAsync(dst, sources[i], c->span, hipMemcpyHostToDevice, c->side);
+    } else {
+      const int k = c->staging_cursor;
+      c->staging_cursor = (k + 1) % (int)c->staging.size();
+      if (c->staging_used[k]) {
+        e = hipEventSynchronize(c->staging_ready[k]);
+        if (e != hipSuccess) return hip_fail("cache staging wait", e);
+      }
+      memcpy(c->staging[k], sources[i], c->span);
+      e = hipMemcpyAsync(dst, c->staging[k], c->span, hipMemcpyHostToDevice, c->side);
+      if (e == hipSuccess) e = hipEventRecord(c->staging_ready[k], c->side);
+      c->staging_used[k] = true;
+    }
+    if (e == hipSuccess) e = hipEventRecord(s.ready, c->side);
+    if (e != hipSuccess) {
+      (void)hipStreamSynchronize(c->side);
+      return fail(K3_HIP_E_COPY, "cache fetch copy: %s", hipGetErrorString(e));
+    }
+    s.has_event = true;
+    s.layer = p.layer;
+    s.id = p.missing[i];
+    s.last_use = ++c->clock;
+    ++s.pins;
+    c->strata[p.layer][s.id] = slot;
+    p.miss_slots.push_back(slot);
+    c->uploaded += (long long)c->span;
+  }
+  return K3_HIP_OK;
+}
+
+static int plan_slot(const K3HipCache::Plan& p, uint16_t id) {
+  const auto it = std::lower_bound(p.ids.begin(), p.ids.end(), id);
+  if (it == p.ids.end() || *it != id) return -2;
+  const size_t idx = (size_t)(it - p.ids.begin());
+  if (p.hit_slots[idx] >= 0) return p.hit_slots[idx];
+  const auto mt = std::lower_bound(p.missing.begin(), p.missing.end(), id);
+  const size_t mi = (size_t)(mt - p.missing.begin());
+  return mi < p.miss_slots.size() ? p.miss_slots[mi] : -1;
+}
+
+int k3_hip_cache_resolve(K3HipCache* c, uint64_t plan_id, const uint16_t* ids, int n,
+                         const uint8_t** device_spans, void* stream) {
+  if (!c || !ids || n < 0 || (n > 0 && !device_spans))
+    return fail(K3_HIP_E_INVALID, "cache resolve: invalid arguments");
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto pit = c->plans.find(plan_id);
+  if (pit == c->plans.end()) return fail(K3_HIP_E_INVALID, "cache resolve: stale or unknown plan");
+  int rc = set_device(c);
+  if (rc != K3_HIP_OK) return rc;
+  for (int i = 0; i < n; ++i) {
+    const int slot = plan_slot(pit->second, ids[i]);
+    if (slot == -2) return fail(K3_HIP_E_INVALID, "cache resolve: expert %d outside the plan", ids[i]);
+    if (slot < 0) return fail(K3_HIP_E_INVALID, "cache resolve: expert %d not fetched", ids[i]);
+    K3HipCache::Slot& s = c->slots[slot];
+    if (s.has_event) {
+      const hipError_t e = hipStreamWaitEvent(static_cast<hipStream_t>(stream), s.ready, 0);
+      if (e != hipSuccess) return hip_fail("cache resolve wait", e);
+    }
+    device_spans[i] = c->slab + (uint64_t)slot * c->slot_bytes;
+  }
+  return K3_HIP_OK;
+}
+
+int k3_hip_cache_ready_subset(K3HipCache* c, uint64_t plan_id, const uint16_t* ids, int n,
+                              const uint8_t** device_spans) {
+  if (!c || !ids || n < 0 || (n > 0 && !device_spans))
+    return fail(K3_HIP_E_INVALID, "cache ready: invalid arguments");
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto pit = c->plans.find(plan_id);
+  if (pit == c->plans.end()) return fail(K3_HIP_E_INVALID, "cache ready: stale or unknown plan");
+  int rc = set_device(c);
+  if (rc != K3_HIP_OK) return rc;
+  int ready = 0;
+  for (int i = 0; i < n; ++i) {
+    device_spans[i] = nullptr;
+    const int slot = plan_slot(pit->second, ids[i]);
+    if (slot < 0) continue;
+    K3HipCache::Slot& s = c->slots[slot];
+    if (s.has_event) {
+      const hipError_t q = hipEventQuery(s.ready);
+      if (q == hipErrorNotReady) {
+        (void)hipGetLastError();
+        continue;
+      }
+      if (q != hipSuccess) return hip_fail("cache ready query", q);
+    }
+    device_spans[i] = c->slab + (uint64_t)slot * c->slot_bytes;
+    ++ready;
+  }
+  return ready;
+}
+
+void k3_hip_cache_release(K3HipCache* c, uint64_t plan_id) {
+  if (!c) return;
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto pit = c->plans.find(plan_id);
+  if (pit == c->plans.end()) return;
+  for (int s : pit->second.hit_slots)
+    if (s >= 0 && c->slots[s].pins > 0) --c->slots[s].pins;
+  for (int s : pit->second.miss_slots)
+    if (s >= 0 && c->slots[s].pins > 0) --c->slots[s].pins;
+  c->plans.erase(pit);
+}
+
+void k3_hip_cache_stats(const K3HipCache* c, long long* six) {
+  if (!c || !six) return;
+  K3HipCache* m = const_cast<K3HipCache*>(c);
+  std::lock_guard<std::mutex> lk(m->mu);
+  six[0] = c->hits;
+  six[1] = c->misses;
+  six[2] = c->evictions;
+  six[3] = c->resident();
+  six[4] = c->capacity;
+  six[5] = c->uploaded;
+}
+
+int k3_hip_cache_read_back(K3HipCache* c, int layer, uint16_t id, uint8_t* host_out,
+                           uint64_t bytes) {
+  if (!c || !host_out || bytes != c->span || layer < 0 || layer >= c->n_layers)
+    return fail(K3_HIP_E_INVALID, "cache read back: invalid arguments");
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto it = c->strata[layer].find(id);
+  if (it == c->strata[layer].end())
+    return fail(K3_HIP_E_INVALID, "cache read back: expert %d of layer %d is not resident", id, layer);
+  int rc = set_device(c);
+  if (rc != K3_HIP_OK) return rc;
+  K3HipCache::Slot& s = c->slots[it->second];
+  hipError_t e = s.has_event ? hipEventSynchronize(s.ready) : hipSuccess;
+  if (e == hipSuccess)
+    e = hipMemcpy(host_out, c->slab + (uint64_t)it->second * c->slot_bytes, bytes,
+                  hipMemcpyDeviceToHost);
+  return e == hipSuccess ? K3_HIP_OK : hip_fail("cache read back", e);
+}
+
+}  // extern "C"

@@ -1,0 +1,177 @@
+// Device helpers for the gfx950 MXFP4 kernels.
+//
+// One 16-byte chunk of a packed row holds 32 E2M1 codes (two per byte, the LOW
+// nibble is the even column, tools/fused_gemv.c:4-6) and shares one E8M0
+// scale byte: a chunk is exactly one scale group.  Codes are decoded with the
+// gfx950 hardware converts (v_cvt_scalef32_pk_{bf16,f32}_fp4) at scale 1.0; the
+// group's partial dot is then multiplied by the group scale (the
+// per-group-then-scale order of tools/metal/moe_mxfp4.metal:95-106).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k3 {
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// E8M0 byte -> fp32 scale.  The byte is the fp32 exponent field exactly as the
+// reference CPU decodes it (tools/fused_gemv.c:247-249: s = 0 -> +0.0); a 255
+// byte yields NaN so the row is poisoned (tools/cuda_moe_kernels.cu:128-131).
+__device__ __forceinline__ float e8m0_scale(uint32_t s) {
+  return __uint_as_float(s == 255u ? 0x7fc00000u : (s << 23));
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// ---------------------------------------------------------------- chunk dots
+// bf16 activations: xv holds 16 dwords, dword i = columns (2i, 2i+1) of the
+// chunk as a bf16 pair.  16 converts + 16 dot2 per 32 elements.
+__device__ __forceinline__ float chunk_dot_bf16(u32x4 w, const uint32_t* xv) {
+  float a0 = 0.0f, a1 = 0.0f;
+#define K3_DOT_DWORD(d, base)                                                  \
+  {                                                                            \
+    v2bf w0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((d), 1.0f, 0);         \
+    v2bf w1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((d), 1.0f, 1);         \
+    v2bf w2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((d), 1.0f, 2);         \
+    v2bf w3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((d), 1.0f, 3);         \
+    a0 = __builtin_amdgcn_fdot2_f32_bf16(w0, __builtin_bit_cast(v2bf, xv[(base) + 0]), a0, false); \
+    a1 = __builtin_amdgcn_fdot2_f32_bf16(w1, __builtin_bit_cast(v2bf, xv[(base) + 1]), a1, false); \
+    a0 = __builtin_amdgcn_fdot2_f32_bf16(w2, __builtin_bit_cast(v2bf, xv[(base) + 2]), a0, false); \
+    a1 = __builtin_amdgcn_fdot2_f32_bf16(w3, __builtin_bit_cast(v2bf, xv[(base) + 3]), a1, false); \
+  }
+  K3_DOT_DWORD(w.x, 0)
+  K3_DOT_DWORD(w.y, 4)
+  K3_DOT_DWORD(w.z, 8)
+  K3_DOT_DWORD(w.w, 12)
+#undef K3_DOT_DWORD
+  return a0 + a1;
+}
+
+// fp32 activations: xv holds the chunk's 32 floats.  16 converts + 32 FMA.
+__device__ __forceinline__ float chunk_dot_f32(u32x4 w, const float* xv) {
+  float a0 = 0.0f, a1 = 0.0f;
+#define K3_DOT_DWORD(d, base)                                                  \
+  {                                                                            \
+    v2f p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, 0);           \
+    v2f p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, 1);           \
+    v2f p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, 2);           \
+    v2f p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, 3);           \
+    a0 = fmaf(p0.x, xv[(base) + 0], a0);                                        \
+    a1 = fmaf(p0.y, xv[(base) + 1], a1);                                        \
+    a0 = fmaf(p1.x, xv[(base) + 2], a0);                                        \
+    a1 = fmaf(p1.y, xv[(base) + 3], a1);                                        \
+    a0 = fmaf(p2.x, xv[(base) + 4], a0);                                        \
+    a1 = fmaf(p2.y, xv[(base) + 5], a1);                                        \
+    a0 = fmaf(p3.x, xv[(base) + 6], a0);                                        \
+    a1 = fmaf(p3.y, xv[(base) + 7], a1);                                        \
+  }
+  K3_DOT_DWORD(w.x, 0)
+  K3_DOT_DWORD(w.y, 8)
+  K3_DOT_DWORD(w.z, 16)
+  K3_DOT_DWORD(w.w, 24)
+#undef K3_DOT_DWORD
+  return a0 + a1;
+}
+
+// Decode a chunk once into fp32 pairs (for reuse across several activations).
+__device__ __forceinline__ void chunk_decode_f32(u32x4 w, v2f* out16) {
+#define K3_DEC_DWORD(d, base)                                                  \
+  out16[(base) + 0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, 0);  \
+  out16[(base) + 1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, 1);  \
+  out16[(base) + 2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, 2);  \
+  out16[(base) + 3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, 3);
+  K3_DEC_DWORD(w.x, 0)
+  K3_DEC_DWORD(w.y, 4)
+  K3_DEC_DWORD(w.z, 8)
+  K3_DEC_DWORD(w.w, 12)
+#undef K3_DEC_DWORD
+}
+
+// Decode a chunk once into bf16 pairs.
+__device__ __forceinline__ void chunk_decode_bf16(u32x4 w, v2bf* out16) {
+#define K3_DEC_DWORD(d, base)                                                  \
+  out16[(base) + 0] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((d), 1.0f, 0); \
+  out16[(base) + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((d), 1.0f, 1); \
+  out16[(base) + 2] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((d), 1.0f, 2); \
+  out16[(base) + 3] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((d), 1.0f, 3);
+  K3_DEC_DWORD(w.x, 0)
+  K3_DEC_DWORD(w.y, 4)
+  K3_DEC_DWORD(w.z, 8)
+  K3_DEC_DWORD(w.w, 12)
+#undef K3_DEC_DWORD
+}
+
+__device__ __forceinline__ float dot_decoded_f32(const v2f* w16, const float* xv) {
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    a0 = fmaf(w16[i].x, xv[2 * i], a0);
+    a1 = fmaf(w16[i].y, xv[2 * i + 1], a1);
+  }
+  return a0 + a1;
+}
+
+__device__ __forceinline__ float dot_decoded_bf16(const v2bf* w16, const uint32_t* xv) {
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    a0 = __builtin_amdgcn_fdot2_f32_bf16(w16[i], __builtin_bit_cast(v2bf, xv[i]), a0, false);
+    a1 = __builtin_amdgcn_fdot2_f32_bf16(w16[i + 1], __builtin_bit_cast(v2bf, xv[i + 1]), a1, false);
+  }
+  return a0 + a1;
+}
+
+// ---------------------------------------------------------------- reductions
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+
+// Full 64-lane sum; every lane receives the same value (each step adds a
+// lane-pair symmetrically, so the order is fixed and lane-independent).
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+// ---------------------------------------------------------------- activations
+// K3 SiTU (provider_moe.cpp:524-533, tools/cuda_moe_kernels.cu:160-177) and
+// SiLU-GLU, both in fp32 with the library's IEEE math flags.
+__device__ __forceinline__ float activate(int act, float g, float u) {
+  const float sig = 1.0f / (1.0f + expf(-g));
+  if (act == 1) return g * sig * u;
+  return (4.0f * tanhf(g / 4.0f) * sig) * (25.0f * tanhf(u / 25.0f));
+}
+
+// ---------------------------------------------------------------- loads
+__device__ __forceinline__ u32x4 load_chunk(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+template <typename T>
+__device__ __forceinline__ T ld(const T* p) {
+  return *p;
+}
+
+}  // namespace k3

@@ -1,0 +1,103 @@
+// Internal declarations shared by the kernel and host translation units.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#include "../../include/k3_hip_moe_abi.h"
+
+namespace k3 {
+
+// Byte offsets of one raw-v1 expert span (provider_moe.cpp:217-243).
+struct Geo {
+  int hidden;        // H: gate/up columns, down rows, x/out length
+  int inter;         // I: gate/up rows, down columns, h length
+  int act;           // K3_ACT_*
+  uint64_t w1p, w1s, w2p, w2s, w3p, w3s, span;
+};
+
+bool make_geo(const K3HipGeometryV1* g, Geo* out);
+
+// Expert addressing for one token (decode) or one edge set: either a resident
+// bank indexed by device-side ids, or explicit span pointers passed by value.
+struct TokenRoute {
+  const uint8_t* bank;      // bank mode when non-null
+  uint64_t stride;          // bank expert stride in bytes
+  const int32_t* ids;       // bank mode: device ids [n]
+  const float* wdev;        // bank mode: device weights [n]
+  const uint8_t* ptr[K3_HIP_MAX_TOKEN_EXPERTS];
+  float w[K3_HIP_MAX_TOKEN_EXPERTS];
+  int n;
+};
+
+// Verify plan in device workspace, built by k_verify_plan.
+struct VerifyPlanDev {
+  int n_unique;
+  int n_edges;
+  int n_positions;
+  int pad;
+};
+
+// Caller route for verify, passed by value to the plan kernel.
+struct EdgeTable {
+  const uint8_t* ptr[K3_HIP_MAX_EDGES];
+  float w[K3_HIP_MAX_EDGES];
+  int pos_off[K3_HIP_MAX_POSITIONS + 1];
+  int n_edges;
+  int n_positions;
+};
+
+// Workspace carve-up (all offsets 256-byte aligned).
+struct Workspace {
+  uint8_t* base;
+  uint64_t bytes;
+  float* h;             // [max_edges][I] activations
+  float* y;             // [max_edges][H] per-edge expert outputs (verify)
+  int32_t* ids;         // [max_edges] route ids
+  float* w;             // [max_edges] route weights
+  const uint8_t** uptr; // [max_edges] unique expert pointers
+  int32_t* uoff;        // [max_edges + 1] unique -> edge-list offsets
+  int32_t* uedges;      // [max_edges] edges grouped by unique expert
+  int32_t* epos;        // [max_edges] edge -> position
+  int32_t* poff;        // [max_positions + 1]
+  VerifyPlanDev* plan;  // 1
+};
+
+uint64_t workspace_bytes(const Geo& g, int max_edges, int max_positions);
+bool carve_workspace(void* base, uint64_t bytes, const Geo& g, int max_edges,
+                     int max_positions, Workspace* ws);
+
+// Thread-local error reporting.
+int fail(int status, const char* fmt, ...);
+int hip_fail(const char* what, hipError_t e);
+
+// Kernel launchers (k3_kernels.hip).  All validate shapes on the host and
+// return a K3_HIP_* status.
+int launch_gemv(const uint8_t* packed, const uint8_t* scales, const void* x,
+                int x_dtype, void* out, int out_dtype, int rows, int cols,
+                int batches, hipStream_t stream);
+int launch_activation(const float* gate, const float* up, float* h, int64_t n,
+                      int act, hipStream_t stream);
+int launch_route(const float* logits, int n_bank, int top_k, int n_positions,
+                 int32_t* ids_ws, float* w_ws, int32_t* ids_user,
+                 float* w_user, hipStream_t stream);
+int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x,
+                        int x_dtype, void* out, int out_dtype,
+                        const Workspace& ws, hipStream_t stream);
+int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride,
+                            int n_positions, int top_k, const Workspace& ws,
+                            hipStream_t stream);
+int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws,
+                             hipStream_t stream);
+int launch_verify_layer(const Geo& g, int n_edges, int n_positions,
+                        const void* x, int x_dtype, void* out, int out_dtype,
+                        const Workspace& ws, hipStream_t stream);
+int launch_synth_bank(const Geo& g, uint8_t* bank, uint64_t stride,
+                      int n_experts, uint64_t first_expert, uint64_t seed,
+                      int lo, int hi, hipStream_t stream);
+int launch_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed,
+                        uint64_t stream_id, hipStream_t stream);
+
+int device_cu_count();
+
+}  // namespace k3

@@ -1,0 +1,319 @@
+#ifndef K3_HIP_MOE_ABI_H
+#define K3_HIP_MOE_ABI_H
+
+/*
+ * MI355X (gfx950) routed-expert MXFP4 library: C ABI.
+ *
+ * Two surfaces, both plain C (pointers, sizes, int status codes):
+ *
+ *  1. Host-synchronous descriptor surface, the HIP counterpart of the Metal
+ *     bridge (tools/metal_moe_abi.h:14-64, tools/metal_moe.mm:17-84).  Calls are
+ *     serialised by one library mutex, take host fp32 activations/weights and
+ *     return host fp32 outputs.  Expert blobs may live in host memory (they are
+ *     staged into an HBM cache keyed by pointer, released by k3_hip_drop) or in
+ *     device memory (used in place).
+ *
+ *  2. Stream-explicit device surface, the HIP counterpart of k3_cuda_*
+ *     (tools/cuda_moe_kernels.cu:244-449): device pointers in and out, caller
+ *     stream, no allocation, no synchronisation, no retained pointer.
+ *
+ * Status codes follow tools/metal_moe.mm (0 ok, -1 init, -2 invalid argument,
+ * -3 allocation, -4 copy, -5 execution, -6 capability miss, -7 invalid
+ * descriptor).  The last failure text is thread-local: k3_hip_last_error().
+ *
+ * Expert layout (raw-v1 ordering, provider_moe.cpp:217-243): one contiguous
+ * span per expert holding w1(gate) packed, w1 scales, w2(down) packed, w2
+ * scales, w3(up) packed, w3 scales.  Packed = two E2M1 codes per byte, LOW
+ * nibble first; scales = one E8M0 byte per 32 elements (tools/fused_gemv.c:4-6).
+ * A scale byte of 255 makes its row NaN (tools/cuda_moe_kernels.cu:128-131).
+ */
+
+#include <stddef.h>
+#include <stdint.h>
+
+/* ------------------------------------------------------------------ layouts */
+/* Same values as tools/metal_moe_abi.h:14-24. */
+enum {
+  K3_LAYOUT_RAW_V1 = 1,
+  K3_LAYOUT_SCALE4_V2 = 2,
+  K3_DESCRIPTOR_ABI_V1 = 1,
+};
+
+#define K3_RAW_V1_EXPERT_SPAN UINT64_C(17547264)
+#define K3_SCALE4_V2_EXPERT_SPAN UINT64_C(17039360)
+#define K3_CAP_RAW_V1 (UINT64_C(1) << K3_LAYOUT_RAW_V1)
+#define K3_CAP_SCALE4_V2 (UINT64_C(1) << K3_LAYOUT_SCALE4_V2)
+
+/* Status codes (tools/metal_moe.mm ABI comment, :17-84). */
+enum {
+  K3_HIP_OK = 0,
+  K3_HIP_E_INIT = -1,
+  K3_HIP_E_INVALID = -2,
+  K3_HIP_E_ALLOC = -3,
+  K3_HIP_E_COPY = -4,
+  K3_HIP_E_EXEC = -5,
+  K3_HIP_E_CAPABILITY = -6,
+  K3_HIP_E_DESCRIPTOR = -7,
+};
+
+/* Activation between gate/up and down.  SiTU is the reference's
+ * (provider_moe.cpp:524-533); SiLU-GLU is silu(gate) * up. */
+enum { K3_ACT_SITU = 0, K3_ACT_SILU = 1 };
+/* Activation / output element types for the device surface. */
+enum { K3_DTYPE_F32 = 0, K3_DTYPE_BF16 = 1 };
+
+/* Most experts one token may route to in one device call. */
+#define K3_HIP_MAX_TOKEN_EXPERTS 32
+/* Verify tiles: positions and edges per call (tools/metal_moe.mm:1056-1059
+ * bounds flat position batches at 16 positions x 16 edges). */
+#define K3_HIP_MAX_POSITIONS 16
+#define K3_HIP_MAX_EDGES 256
+
+/* Expert descriptor: byte-for-byte the layout of K3MetalExpertDescriptorV1
+ * (tools/metal_moe_abi.h:35-50), so a caller's descriptor arrays pass through
+ * unchanged.  blob_bytes must equal the configured geometry's span. */
+typedef struct K3HipExpertDescriptorV1 {
+  uint32_t abi_version;  /* K3_DESCRIPTOR_ABI_V1 */
+  uint32_t struct_bytes; /* sizeof(K3HipExpertDescriptorV1) == 32 */
+  uint32_t layout_id;    /* K3_LAYOUT_RAW_V1 */
+  uint32_t reserved;     /* 0 */
+  uint64_t blob_bytes;
+  const uint8_t* blob;   /* host or device pointer */
+} K3HipExpertDescriptorV1;
+
+/* Geometry.  The reference hard-codes K3 (hidden 3584, intermediate 3072,
+ * tools/cuda_moe_kernels.cu:36-40); this library takes it as data. */
+typedef struct K3HipGeometryV1 {
+  uint32_t abi_version;  /* 1 */
+  uint32_t struct_bytes; /* sizeof(K3HipGeometryV1) == 32 */
+  uint32_t hidden;       /* x / output length, positive multiple of 32 */
+  uint32_t intermediate; /* h length, positive multiple of 32 */
+  uint32_t activation;   /* K3_ACT_* */
+  uint32_t reserved;     /* 0 */
+  uint64_t expert_span;  /* must equal k3_hip_geometry_span(hidden, intermediate) */
+} K3HipGeometryV1;
+
+#ifdef __cplusplus
+static_assert(sizeof(K3HipExpertDescriptorV1) == 32, "descriptor ABI drift");
+static_assert(offsetof(K3HipExpertDescriptorV1, blob_bytes) == 16, "descriptor ABI drift");
+static_assert(offsetof(K3HipExpertDescriptorV1, blob) == 24, "descriptor ABI drift");
+static_assert(sizeof(K3HipGeometryV1) == 32, "geometry ABI drift");
+extern "C" {
+#endif
+
+/* ======================================================= common / geometry */
+
+/* Raw-v1 span for a geometry (provider_moe.cpp:217-243 offsets). 0 if invalid. */
+uint64_t k3_hip_geometry_span(uint32_t hidden, uint32_t intermediate);
+/* Fill *out with a preset: 1 = K3 (3584/3072/SiTU, 17,547,264 B),
+ * 2 = the 16-expert decode benchmark geometry (7168/2048/SiLU, 23,396,352 B).
+ * Returns 0 or K3_HIP_E_INVALID. */
+int k3_hip_geometry_preset(int preset, K3HipGeometryV1* out);
+/* Thread-local text of the last failure on this thread. */
+const char* k3_hip_last_error(void);
+
+/* ============================== surface 1: host-synchronous descriptor API */
+
+/* Replaces k3_metal_init (tools/metal_moe.mm:649-652).  selector: NULL/"" =
+ * device 0, or a decimal device index.  0 on success, -1 on failure. */
+int k3_hip_init(const char* selector);
+/* Replaces k3_metal_available (tools/metal_moe.mm:654-657): 1 or 0. */
+int k3_hip_available(void);
+/* Replaces k3_metal_descriptor_abi_version (tools/metal_moe_abi.h:56). */
+uint32_t k3_hip_descriptor_abi_version(void);
+/* Replaces k3_metal_layout_capabilities (tools/metal_moe_abi.h:57). */
+uint64_t k3_hip_layout_capabilities(void);
+/* Sets the geometry used by surface 1 (default preset 1, K3).  Drops every
+ * cached blob.  No reference counterpart: the Metal bridge fixes K3. */
+int k3_hip_configure_v1(const K3HipGeometryV1* geometry);
+/* Replaces k3_metal_shapes (tools/metal_moe.mm:669-673). */
+void k3_hip_shapes(int* hidden, int* inter, long long* span);
+/* Replaces k3_metal_stats (tools/metal_moe.mm:675-681):
+ * [calls, device_resident_uses, host_uploads, cache_entries, cache_mode]. */
+void k3_hip_stats(long long* five);
+/* Replaces k3_metal_mode / k3_metal_set_mode (:683-693): 1 = keep uploaded
+ * host blobs cached in HBM (default), 0 = upload every call. */
+int k3_hip_mode(void);
+int k3_hip_set_mode(int cache_host_blobs);
+/* Replaces k3_metal_drop / k3_metal_flush (:695-707).  A cached host blob must
+ * be dropped before its memory is modified, unmapped or freed. */
+void k3_hip_drop(const uint8_t* blob);
+void k3_hip_flush(void);
+
+/* Replaces k3_metal_moe_layer_desc_v1 (tools/metal_moe_abi.h:59-61):
+ * output[hidden] = sum_e weights[e] * expert_e(input[hidden]), summed in
+ * descriptor order.  expert_count == 0 writes zeros. */
+int k3_hip_moe_layer_desc_v1(const K3HipExpertDescriptorV1* experts,
+                             int expert_count, const float* weights,
+                             const float* input, float* output);
+/* Replaces k3_metal_moe_positions_desc_v1 (tools/metal_moe_abi.h:63-66):
+ * position_offsets[position_count+1] partitions the edges; input/output are
+ * [position_count, hidden].  Every expert is read once per call however many
+ * positions route to it. */
+int k3_hip_moe_positions_desc_v1(const K3HipExpertDescriptorV1* experts,
+                                 int edge_count, const int* position_offsets,
+                                 int position_count, const float* weights,
+                                 const float* input, float* output);
+/* Raw-pointer forms (tools/metal_moe.mm:829-837, :1023-1032): blobs are spans
+ * of the configured geometry. */
+int k3_hip_moe_layer(const uint8_t* const* expert_blobs, int n_experts,
+                     const float* weights, const float* x, float* out);
+int k3_hip_moe_positions(const uint8_t* const* expert_blobs, int n_edges,
+                         const int* position_offsets, int n_positions,
+                         const float* weights, const float* x, float* out);
+
+/* ============================== surface 2: stream-explicit device API */
+
+/* Replaces k3_cuda_moe_abi_version (tools/cuda_moe_kernels.cu:244-246). */
+uint32_t k3_hip_moe_abi_version(void);
+/* Replaces k3_cuda_moe_shapes (:248-264); reports surface 1's geometry and
+ * pointer layout 1. */
+void k3_hip_moe_shapes(int* hidden, int* intermediate, int64_t* expert_span,
+                       uint32_t* pointer_layout);
+/* Replaces k3_cuda_moe_available (:270-329): 1 when `device` is a usable gfx950,
+ * else a negative status. */
+int k3_hip_moe_available(int device);
+
+/* Replaces k3_cuda_mxfp4_gemv (:331-339): out[b, r] = sum_c W[r, c] x[b, c],
+ * x [batches, cols] fp32, out [batches, rows] fp32, cols % 32 == 0.  Each
+ * weight row is read once for all batches. */
+int k3_hip_mxfp4_gemv(const uint8_t* packed, const uint8_t* scales,
+                      const float* x, float* output, int rows, int cols,
+                      int batches, void* stream);
+/* Same contraction with a bf16 or fp32 activation and output type. */
+int k3_hip_mxfp4_gemv_ex(const uint8_t* packed, const uint8_t* scales,
+                         const void* x, int x_dtype, void* output,
+                         int out_dtype, int rows, int cols, int batches,
+                         void* stream);
+
+/* Replaces k3_cuda_moe_launch (:341-417) for geometry g (NULL = surface 1's):
+ * gate = W1 x, up = W3 x, gate <- act(gate, up), out = W2 gate, all fp32,
+ * x [batches, hidden], gate/up [batches, intermediate], out [batches, hidden]. */
+int k3_hip_moe_launch(const K3HipGeometryV1* g, const uint8_t* expert_span,
+                      const float* x, int batches, float* gate, float* up,
+                      float* expert_output, void* stream);
+
+/* Device workspace bytes needed by the layer / verify calls below for up to
+ * max_edges routed edges over max_positions positions.  The workspace must be
+ * zero-filled once before first use; every call leaves it reusable.  Calls
+ * that share one workspace must not overlap. */
+uint64_t k3_hip_moe_workspace_bytes(const K3HipGeometryV1* g, int max_edges,
+                                    int max_positions);
+
+/* Whole routed layer for one token (replaces the per-expert launch loop plus
+ * ordered_route_reduce, provider_cuda_moe.cpp:1203-1258, :252-289):
+ * out[hidden] = sum_{e < n} weights[e] * expert_e(x), summed in route order.
+ * experts: host array of n device span pointers; weights: host fp32 [n];
+ * x, out: device vectors of x_dtype / out_dtype.  n <= K3_HIP_MAX_TOKEN_EXPERTS. */
+int k3_hip_moe_layer_device(const K3HipGeometryV1* g,
+                            const uint8_t* const* experts,
+                            const float* weights, int n_experts,
+                            const void* x, int x_dtype, void* out,
+                            int out_dtype, void* workspace,
+                            uint64_t workspace_bytes, void* stream);
+
+/* Whole routed layer with the router on the device: the top_k largest of
+ * logits[n_bank] (descending, lower index on ties) select experts
+ * bank + id * expert_stride, weighted by a softmax over the selected logits.
+ * route_ids / route_weights (device, nullable) receive the route. */
+int k3_hip_moe_route_layer_device(const K3HipGeometryV1* g,
+                                  const uint8_t* bank, uint64_t expert_stride,
+                                  int n_bank, const float* logits, int top_k,
+                                  const void* x, int x_dtype, void* out,
+                                  int out_dtype, int32_t* route_ids,
+                                  float* route_weights, void* workspace,
+                                  uint64_t workspace_bytes, void* stream);
+
+/* Batched speculative verify with device routing: positions p < n_positions
+ * each route top_k of logits[p, n_bank]; experts are grouped so each routed
+ * expert's bytes are read once for all positions that chose it (no reference
+ * counterpart amortises this; semantics follow
+ * provider_cuda_moe.cpp:1260-1360 and tools/metal_moe.mm:852-1021).
+ * x, out: [n_positions, hidden]; route_ids / route_weights (nullable):
+ * [n_positions, top_k]. */
+int k3_hip_moe_verify_route_device(const K3HipGeometryV1* g,
+                                   const uint8_t* bank, uint64_t expert_stride,
+                                   int n_bank, const float* logits,
+                                   int n_positions, int top_k, const void* x,
+                                   int x_dtype, void* out, int out_dtype,
+                                   int32_t* route_ids, float* route_weights,
+                                   void* workspace, uint64_t workspace_bytes,
+                                   void* stream);
+
+/* Batched verify with a caller route: edge e of position p (edges of p are
+ * [position_offsets[p], position_offsets[p+1])) uses expert span
+ * edge_experts[e] (host array of device pointers) with weight
+ * edge_weights[e] (host).  Same grouping and ordered per-position combine. */
+int k3_hip_moe_verify_device(const K3HipGeometryV1* g,
+                             const uint8_t* const* edge_experts,
+                             const float* edge_weights,
+                             const int* position_offsets, int n_positions,
+                             const void* x, int x_dtype, void* out,
+                             int out_dtype, void* workspace,
+                             uint64_t workspace_bytes, void* stream);
+
+/* ============================== host-side expert staging (HBM LRU cache) */
+/* C counterpart of CudaMoeExpertCache (provider_cuda_moe.h:83-132): a
+ * device-resident LRU of expert spans over layer strata, plan-before-I/O
+ * snapshots (hits pinned, misses reported), uploads from pinned host memory
+ * on a side stream with per-slot ready events. */
+
+typedef struct K3HipCache K3HipCache;
+
+/* capacity_experts slots of span_bytes each in HBM; n_layers strata.  staging
+ * slots = pinned host staging buffers used for pageable sources.
+ * Returns NULL on failure (see k3_hip_last_error). */
+K3HipCache* k3_hip_cache_create(int device, uint64_t span_bytes,
+                                int capacity_experts, int n_layers,
+                                int staging_slots);
+void k3_hip_cache_destroy(K3HipCache* cache);
+/* Plan (provider_cuda_moe.cpp:963-1008): snapshot hits for `ids` of `layer`
+ * (canonical ascending, unique), LRU-promoting them; misses are written to
+ * missing_ids (capacity n) and *n_missing.  plan_id must be non-zero and not
+ * live.  */
+int k3_hip_cache_plan(K3HipCache* cache, uint64_t plan_id, int layer,
+                      const uint16_t* ids, int n, uint16_t* missing_ids,
+                      int* n_missing);
+/* Admit the plan's misses from host memory: sources[i] holds the span of
+ * missing_ids[i] (pinned memory is copied directly, pageable memory through
+ * a staging slot).  Copies run on the cache's side stream; per-expert ready
+ * events are recorded.  Non-blocking for pinned sources. */
+int k3_hip_cache_fetch(K3HipCache* cache, uint64_t plan_id,
+                       const uint8_t* const* sources, int n_sources);
+/* Device pointers of the plan's experts in `ids` order, and make `stream`
+ * wait for every one of them to be resident. */
+int k3_hip_cache_resolve(K3HipCache* cache, uint64_t plan_id,
+                         const uint16_t* ids, int n,
+                         const uint8_t** device_spans, void* stream);
+/* Device pointers for the subset of `ids` already resident and ready (no
+ * wait); others get NULL.  Returns the number resident. */
+int k3_hip_cache_ready_subset(K3HipCache* cache, uint64_t plan_id,
+                              const uint16_t* ids, int n,
+                              const uint8_t** device_spans);
+/* Finish or cancel a plan (provider_cuda_moe.cpp:1166-1168). */
+void k3_hip_cache_release(K3HipCache* cache, uint64_t plan_id);
+/* [hits, misses, evictions, resident, capacity, bytes_uploaded]. */
+void k3_hip_cache_stats(const K3HipCache* cache, long long* six);
+/* Copy the resident span of (layer, id) to host (bounded D2H, the CPU fallback
+ * materialisation of provider_cuda_moe.cpp:1170-1201).  0 or -2 if absent. */
+int k3_hip_cache_read_back(K3HipCache* cache, int layer, uint16_t id,
+                           uint8_t* host_out, uint64_t bytes);
+
+/* ============================== synthetic inputs (benchmark support) */
+/* No reference counterpart.  Fill device memory with the counter-based
+ * synthetic distribution shared with oracle/orc.c: packed bytes uniform,
+ * scale bytes uniform in [scale_lo, scale_hi]; expert e of a bank uses
+ * matrix streams 3(first_expert+e)+{0,1,2}. */
+int k3_hip_synth_bank(const K3HipGeometryV1* g, uint8_t* bank,
+                      uint64_t expert_stride, int n_experts,
+                      uint64_t first_expert, uint64_t seed, int scale_lo,
+                      int scale_hi, void* stream);
+/* Normal(0,1) values (fp32 or bf16) from (seed, stream), n elements. */
+int k3_hip_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed,
+                        uint64_t stream, void* stream_handle);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
