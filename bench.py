@@ -1,0 +1,362 @@
+#!/usr/bin/env python3
+"""Routed-expert MXFP4 decode benchmark on one MI355X.
+
+Workload: a bank of 384 synthetic MXFP4 experts
+(hidden 7168, intermediate 2048, raw-v1 spans of 23,396,352 B, 8.98 GB) resident
+in HBM; 1000 seeded tokens, each with fp32 N(0,1) router logits over the 384
+experts and a bf16 N(0,1) activation.  One step = one token-layer: the device
+router picks the top 16 experts (softmax weights over them), then the gate/up
+projections with SiLU-GLU and the down projection with the route-ordered
+weighted combine write a bf16 output row.  Inputs are resident in HBM when the
+timed region starts.
+
+Printed: one JSON line with the step throughput, the roofline of the dominant
+kernel (algorithmic bytes per launch / average launch duration measured with
+HIP events on the launch stream), parity of sampled tokens against the fp64
+oracle, and the reference CPU path (tools/fused_gemv_batch.c, compiled from the
+reference sources into oracle/_ref) timed on this host over a bounded sample of
+the same tokens.
+
+    python bench.py [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "achieved HBM GB/s + MoE-layer decode tokens/s (16 experts, MXFP4, batch 1)"
+HIDDEN, INTER, N_BANK, TOP_K, N_TOKENS = 7168, 2048, 384, 16, 1000
+SEED = 20261201
+HBM_PEAK_GBS = 8000.0
+
+# Algorithmic bytes (what the computation must move at least once).
+MAT_BYTES = INTER * HIDDEN // 2 + INTER * (HIDDEN // 32)  # one 2048x7168 MXFP4 matrix: 7,798,784
+SPAN = 3 * MAT_BYTES                                      # 23,396,352
+X_BYTES = HIDDEN * 2                                      # bf16 activation
+OUT_BYTES = HIDDEN * 2                                    # bf16 output
+LOGIT_BYTES = N_BANK * 4
+H_BYTES = TOP_K * INTER * 4                               # fp32 h handed from gate/up to down
+LAYER_BYTES = TOP_K * SPAN + X_BYTES + LOGIT_BYTES + OUT_BYTES  # 374,371,840
+KERNEL_BYTES = {
+    "glu_decode": 2 * TOP_K * MAT_BYTES + X_BYTES + H_BYTES,
+    "down_decode": TOP_K * MAT_BYTES + H_BYTES + OUT_BYTES,
+    "route": LOGIT_BYTES + TOP_K * 8,
+    "layer_decode": LAYER_BYTES,
+}
+KERNEL_FLOPS = {
+    "glu_decode": 2 * 2 * TOP_K * INTER * HIDDEN,
+    "down_decode": 2 * TOP_K * INTER * HIDDEN,
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=N_TOKENS)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU work budget for the reference CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--parity-tokens", type=int, default=2)
+    return ap.parse_args()
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    # The reference pool caps at 32 threads (tools/fused_gemv_batch.c:36); one
+    # GPU's share of the box is 16 CPUs.
+    return max(1, min(n, 16))
+
+
+def cpu_baseline(bank_host: np.ndarray, logits: np.ndarray, x_f32: np.ndarray,
+                 seconds: float, threads: int) -> tuple[dict, np.ndarray, int]:
+    """The reference CPU composition for config 2 (provider_moe.cpp:867-971 with
+    SiLU-GLU in place of SiTU): mxfp4_moe_layer over the 32 gate/up matrices with
+    the shared x, fp32 SiLU-GLU, mxfp4_gemv_batch over the 16 down matrices, then
+    the ordered combine.  Tokens are run in order until `seconds` of CPU work."""
+    import oracle
+
+    ref = oracle.ref()
+    ref.mxfp4_pool_init(threads)
+    u8p = C.POINTER(C.c_uint8)
+    f32p = C.POINTER(C.c_float)
+    off = oracle.expert_offsets(HIDDEN, INTER)
+    base = bank_host.ctypes.data
+    rows13 = (C.c_int * (2 * TOP_K))(*([INTER] * (2 * TOP_K)))
+    cols13 = (C.c_int * (2 * TOP_K))(*([HIDDEN] * (2 * TOP_K)))
+    rows2 = (C.c_int * TOP_K)(*([HIDDEN] * TOP_K))
+    cols2 = (C.c_int * TOP_K)(*([INTER] * TOP_K))
+    gu = np.empty(2 * TOP_K * INTER, np.float32)
+    yb = np.empty((TOP_K, HIDDEN), np.float32)
+    outs = []
+
+    def token(t: int) -> np.ndarray:
+        ids, w64 = oracle.topk_softmax(logits[t], TOP_K)
+        w = w64.astype(np.float32)
+        p13 = (u8p * (2 * TOP_K))()
+        s13 = (u8p * (2 * TOP_K))()
+        p2 = (u8p * TOP_K)()
+        s2 = (u8p * TOP_K)()
+        for j, e in enumerate(ids):
+            b = base + int(e) * SPAN
+            p13[2 * j] = C.cast(b + off[0], u8p)
+            s13[2 * j] = C.cast(b + off[1], u8p)
+            p13[2 * j + 1] = C.cast(b + off[4], u8p)
+            s13[2 * j + 1] = C.cast(b + off[5], u8p)
+            p2[j] = C.cast(b + off[2], u8p)
+            s2[j] = C.cast(b + off[3], u8p)
+        xt = np.ascontiguousarray(x_f32[t])
+        ref.mxfp4_moe_layer(p13, s13, rows13, cols13, 2 * TOP_K, xt.ctypes.data_as(f32p),
+                            gu.ctypes.data_as(f32p), threads)
+        g = gu.reshape(TOP_K, 2, INTER)[:, 0, :]
+        u = gu.reshape(TOP_K, 2, INTER)[:, 1, :]
+        with np.errstate(over="ignore"):
+            h = np.ascontiguousarray(g / (np.float32(1.0) + np.exp(-g)) * u, dtype=np.float32)
+        xs = (f32p * TOP_K)(*[h[j].ctypes.data_as(f32p) for j in range(TOP_K)])
+        ys = (f32p * TOP_K)(*[yb[j].ctypes.data_as(f32p) for j in range(TOP_K)])
+        ref.mxfp4_gemv_batch(p2, s2, xs, ys, rows2, cols2, TOP_K, threads)
+        out = np.zeros(HIDDEN, np.float32)
+        for j in range(TOP_K):
+            out += w[j] * yb[j]
+        return out
+
+    token(0)  # warm the pool and the pages of the first token's experts
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        outs.append(token(n % logits.shape[0]))
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= logits.shape[0]:
+            break
+    rate = n / el
+    res = {
+        "value": rate,
+        "unit": "token-layers/s",
+        "cores": threads,
+        "kind": "reference",
+        "sample": (f"first {n} of the {logits.shape[0]} tokens of the same workload, "
+                   f"384-expert bank copied to host DRAM; mxfp4_moe_layer + fp32 SiLU-GLU + "
+                   f"mxfp4_gemv_batch + ordered combine per token ({el:.1f} s)"),
+        "achieved_gbs": rate * LAYER_BYTES / 1e9,
+        "avx2": int(ref.mxfp4_have_avx2()),
+        "cpu_model": _cpu_model(),
+    }
+    return res, np.stack(outs), n
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: the routed-expert path is built and measured "
+              f"on a single MI355X (asked for --gpus {args.gpus}); multi-GPU sharding is a "
+              f"design note, not a measured configuration.", file=sys.stderr, flush=True)
+        return 2
+    import torch
+
+    import oracle
+    from deltafin_amd import _lib, moe, synth
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    torch.cuda.set_device(0)
+    lib = _lib.load()
+    avail = lib.k3_hip_moe_available(0)
+    if avail != 1:
+        raise _lib.K3HipError(avail, "k3_hip_moe_available")
+    props = torch.cuda.get_device_properties(0)
+    log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+
+    g = moe.preset(2)
+    assert g.hidden == HIDDEN and g.intermediate == INTER and g.expert_span == SPAN
+    stride = SPAN
+    bank = torch.empty(N_BANK * stride, dtype=torch.uint8, device="cuda")
+    moe.synth_bank(g, bank, stride, N_BANK, 0, SEED)
+    logits = moe.synth_normal(N_TOKENS * N_BANK, torch.float32, SEED, 1).view(N_TOKENS, N_BANK)
+    x = moe.synth_normal(N_TOKENS * HIDDEN, torch.bfloat16, SEED, 2).view(N_TOKENS, HIDDEN)
+    out = torch.empty((N_TOKENS, HIDDEN), dtype=torch.bfloat16, device="cuda")
+    ws = moe.workspace(g, TOP_K)
+    torch.cuda.synchronize()
+    log(f"bank of {N_BANK} experts ({N_BANK * stride / 1e9:.2f} GB) synthesised in HBM")
+
+    fn = lib.k3_hip_moe_route_layer_device
+    gref = C.byref(g)
+    ws_base, ws_bytes = moe._ws_args(ws)
+    st = moe.stream_handle()
+    bank_p, lg_p, x_p, o_p = bank.data_ptr(), logits.data_ptr(), x.data_ptr(), out.data_ptr()
+    BF16 = _lib.K3_DTYPE_BF16
+
+    def step(t: int) -> None:
+        t %= N_TOKENS
+        rc = fn(gref, bank_p, stride, N_BANK, lg_p + t * N_BANK * 4, TOP_K, x_p + t * HIDDEN * 2,
+                BF16, o_p + t * HIDDEN * 2, BF16, None, None, ws_base, ws_bytes, st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_moe_route_layer_device")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    log(f"warmup {args.warmup} steps done")
+
+    # ---- timed region: exactly K steps, synchronised on both sides
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dev_ms = ev0.elapsed_time(ev1)
+    ms_per_step = wall * 1e3 / args.steps
+    log(f"timed {args.steps} steps: wall {wall * 1e3:.2f} ms, device {dev_ms:.2f} ms")
+
+    # ---- per-kernel durations: the same K steps again, each launch bracketed by
+    # HIP events on the launch stream
+    _lib.timing_begin(4 * args.steps + 16)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    kern, dropped = _lib.timing_end()
+    log("kernels: " + ", ".join(f"{k} {v['avg_ms'] * 1e3:.2f} us x{v['launches']}" for k, v in kern.items()))
+    dom = max((k for k in kern if k in KERNEL_BYTES), key=lambda k: kern[k]["total_ms"])
+    dom_s = kern[dom]["avg_ms"] / 1e3
+    achieved = KERNEL_BYTES[dom] / dom_s / 1e9
+    traffic = _traffic_from_profiles(dom)
+    roofline = {
+        "bound": "hbm",
+        "kernel": dom,
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "algorithmic_bytes_per_launch": KERNEL_BYTES[dom],
+        "avg_launch_us": round(dom_s * 1e6, 3),
+    }
+
+    # ---- parity of sampled tokens (fp32 output before rounding) against the fp64 oracle
+    parity = _parity(moe, oracle, synth, g, bank, stride, logits, x, ws, args.parity_tokens)
+
+    value = args.steps / wall
+    res = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "token-layers/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": ("16-of-384 routed-expert MXFP4 decode layer, batch 1 "
+                         "(BASELINE configs[2]): hidden 7168, intermediate 2048, SiLU-GLU, "
+                         "device top-16 + softmax router, bf16 x/out, 1000 seeded tokens"),
+            "n_bank": N_BANK, "top_k": TOP_K, "hidden": HIDDEN, "intermediate": INTER,
+            "bank_bytes": N_BANK * SPAN, "layer_bytes_per_token": LAYER_BYTES,
+            "weights": "MXFP4 (E2M1 + E8M0 per 32)", "x_dtype": "bf16", "out_dtype": "bf16",
+        },
+        "achieved_gbs": round(value * LAYER_BYTES / 1e9, 1),
+        "hbm_frac": round(value * LAYER_BYTES / 1e9 / HBM_PEAK_GBS, 4),
+        "device_ms_per_step": round(dev_ms / args.steps, 5),
+        "roofline": roofline,
+        "kernels_us": {k: round(v["avg_ms"] * 1e3, 3) for k, v in kern.items()},
+        "timing_dropped": dropped,
+        "parity": parity,
+    }
+    if not args.no_cpu:
+        log("cpu baseline: copying the bank to host DRAM")
+        bank_host = bank.cpu().numpy()
+        lg_host = logits.cpu().numpy()
+        x_host = x.float().cpu().numpy()  # bf16 -> fp32 widening outside the timed region
+        threads = cpu_threads()
+        cpu, cpu_out, n_cpu = cpu_baseline(bank_host, lg_host, x_host, args.cpu_seconds, threads)
+        gpu_out = out[:n_cpu].float().cpu().numpy()
+        den = np.maximum(np.abs(cpu_out), 1e-2)
+        cpu["gpu_vs_cpu_max_rel_diff"] = float(np.max(np.abs(gpu_out - cpu_out) / den))
+        res["cpu_baseline"] = cpu
+        log(f"cpu baseline {cpu['value']:.2f} tok/s with {threads} threads")
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def _traffic_from_profiles(kernel: str):
+    """HBM bytes per launch measured by rocprofv3 PMC runs, recorded in
+    profiles/traffic.txt as `<kernel> <bytes_per_launch>` lines (null when absent)."""
+    p = ROOT / "profiles" / "traffic.txt"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        f = line.split()
+        if len(f) >= 2 and f[0] == kernel:
+            try:
+                return int(float(f[1]))
+            except ValueError:
+                return None
+    return None
+
+
+def _parity(moe, oracle, synth, g, bank, stride, logits, x, ws, n_tokens: int) -> dict:
+    import torch
+
+    if n_tokens <= 0:
+        return {"tokens_checked": 0}
+    worst = 0.0
+    ids_ok = True
+    host_bank = {}
+    for t in range(n_tokens):
+        o32, ids, wts = moe.moe_route_layer(g, bank, stride, N_BANK, logits[t], TOP_K, x[t], ws,
+                                            out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        lg = logits[t].cpu().numpy()
+        rid, rw = oracle.topk_softmax(lg, TOP_K)
+        ids_ok &= ids.cpu().numpy().tolist() == rid.tolist()
+        spans = []
+        for e in rid:
+            e = int(e)
+            if e not in host_bank:
+                host_bank[e] = bank[e * stride: e * stride + SPAN].cpu().numpy()
+            spans.append(host_bank[e])
+        xf = x[t].float().cpu().numpy()
+        ref, mag = oracle.moe_layer_f64(spans, rw, HIDDEN, INTER, oracle.ACT_SILU, xf)
+        worst = max(worst, oracle.cond_rel_err(o32.cpu().numpy(), ref, mag, INTER))
+    log(f"parity: {n_tokens} tokens, max cond rel err {worst:.3e}, top-k identical {ids_ok}")
+    return {"tokens_checked": n_tokens, "max_cond_rel_err_fp32": worst, "tolerance": 1e-3,
+            "topk_ids_identical": bool(ids_ok), "pass": bool(ids_ok and worst <= 1e-3)}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -62,6 +62,17 @@ class K3HipGeometryV1(C.Structure):
     ]
 
 
+class K3HipKernelTimingV1(C.Structure):
+    _fields_ = [
+        ("kernel", C.c_char * 32),
+        ("launches", C.c_int64),
+        ("total_ms", C.c_double),
+        ("min_ms", C.c_double),
+        ("max_ms", C.c_double),
+    ]
+
+
+assert C.sizeof(K3HipKernelTimingV1) == 64
 assert C.sizeof(K3HipExpertDescriptorV1) == 32
 assert C.sizeof(K3HipGeometryV1) == 32
 
@@ -116,6 +127,9 @@ SIGNATURES = {
     "k3_hip_cache_release": (None, [_vp, _u64]),
     "k3_hip_cache_stats": (None, [_vp, C.POINTER(C.c_longlong)]),
     "k3_hip_cache_read_back": (_i32, [_vp, _i32, C.c_uint16, _vp, _u64]),
+    "k3_hip_timing_begin": (_i32, [_i32]),
+    "k3_hip_timing_end": (_i32, [C.POINTER(K3HipKernelTimingV1), _i32, C.POINTER(_i32),
+                                 C.POINTER(C.c_longlong)]),
     "k3_hip_synth_bank": (_i32, [_GP, _vp, _u64, _i32, _u64, _u64, _i32, _i32, _vp]),
     "k3_hip_synth_normal": (_i32, [_vp, _i32, _u64, _u64, _u64, _vp]),
 }
@@ -193,3 +207,22 @@ def preset(which: int) -> K3HipGeometryV1:
     g = K3HipGeometryV1()
     check(load().k3_hip_geometry_preset(which, C.byref(g)), "k3_hip_geometry_preset")
     return g
+
+
+def timing_begin(max_launches: int) -> None:
+    """Open a per-launch timing window (k3_hip_timing_begin)."""
+    check(load().k3_hip_timing_begin(max_launches), "k3_hip_timing_begin")
+
+
+def timing_end() -> tuple[dict[str, dict[str, float]], int]:
+    """Close the window; returns ({kernel: {launches, total_ms, min_ms, max_ms, avg_ms}}, dropped)."""
+    rows = (K3HipKernelTimingV1 * 16)()
+    n = C.c_int()
+    dropped = C.c_longlong()
+    check(load().k3_hip_timing_end(rows, 16, C.byref(n), C.byref(dropped)), "k3_hip_timing_end")
+    out = {}
+    for r in rows[: n.value]:
+        out[r.kernel.decode()] = {
+            "launches": int(r.launches), "total_ms": r.total_ms, "min_ms": r.min_ms,
+            "max_ms": r.max_ms, "avg_ms": r.total_ms / max(r.launches, 1)}
+    return out, int(dropped.value)

@@ -50,7 +50,7 @@ CXX_FLAGS = [
     "-Wno-unused-parameter",
 ]
 KERNEL_SOURCES = ["k3_kernels.hip"]
-HOST_SOURCES = ["k3_abi.cpp", "k3_cache.cpp"]
+HOST_SOURCES = ["k3_abi.cpp", "k3_cache.cpp", "k3_timing.cpp"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -65,14 +65,18 @@ def _run(cmd: list[str]) -> None:
         print(out)
 
 
-def build(verbose: bool = True) -> Path:
+def build(verbose: bool = True, defines: list[str] | None = None, out: Path | None = None) -> Path:
+    """Compile the library; `defines` (NAME=VALUE) override kernel tuning
+    constants and `out` redirects the library (both for tuning sweeps)."""
     hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
-    LIBDIR.mkdir(parents=True, exist_ok=True)
+    target = Path(out) if out is not None else LIB
+    target.parent.mkdir(parents=True, exist_ok=True)
+    dflags = [f"-D{d}" for d in (defines or [])]
     with tempfile.TemporaryDirectory(prefix="k3build_") as tmp:
         objs = []
         for src in KERNEL_SOURCES:
             obj = Path(tmp) / (src + ".o")
-            _run([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)])
+            _run([hipcc, *HIP_FLAGS, *dflags, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)])
             objs.append(str(obj))
         for src in HOST_SOURCES:
             obj = Path(tmp) / (src + ".o")
@@ -81,10 +85,10 @@ def build(verbose: bool = True) -> Path:
         tmp_lib = Path(tmp) / LIB.name
         _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp_lib), *objs,
               f"-L{ROCM / 'lib'}", "-lamdhip64"])
-        shutil.move(str(tmp_lib), str(LIB))
+        shutil.move(str(tmp_lib), str(target))
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {target}")
+    return target
 
 
 if __name__ == "__main__":

@@ -80,6 +80,7 @@ uint64_t workspace_bytes(const Geo& g, int max_edges, int max_positions) {
   b += align256(E * 4);             // epos
   b += align256((P + 1) * 4);       // poff
   b += align256(sizeof(VerifyPlanDev));
+  b += align256((uint64_t)kWorkspaceCounters * 4);  // cnt
   return b;
 }
 
@@ -106,6 +107,7 @@ bool carve_workspace(void* base, uint64_t bytes, const Geo& g, int max_edges, in
   ws->epos = reinterpret_cast<int32_t*>(take(E * 4));
   ws->poff = reinterpret_cast<int32_t*>(take((P + 1) * 4));
   ws->plan = reinterpret_cast<VerifyPlanDev*>(take(sizeof(VerifyPlanDev)));
+  ws->cnt = reinterpret_cast<int32_t*>(take((uint64_t)kWorkspaceCounters * 4));
   return true;
 }
 
@@ -123,6 +125,26 @@ int device_cu_count() {
     cus = 256;
   cache[dev] = cus;
   return cus;
+}
+
+int occupancy_blocks_per_cu(const void* kernel, int block, size_t dynamic_lds) {
+  static std::mutex mu;
+  static std::unordered_map<std::string, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  char key[96];
+  snprintf(key, sizeof(key), "%p/%d/%zu/%d", kernel, block, dynamic_lds, dev);
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, dynamic_lds) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = 1;
+  }
+  cache[key] = n;
+  return n;
 }
 
 namespace {

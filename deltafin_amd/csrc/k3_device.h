@@ -155,6 +155,74 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Cross-lane partner exchange for the butterfly below.  Lanes are split by one
+// lane bit ("upper" = bit set); a lane's partner has that bit flipped:
+//   32: v_permlane32_swap (halves of the wave), 16: v_permlane16_swap (rows),
+//   8: row_mirror (lane i <-> 15-i in a row), 4: row_half_mirror (i <-> 7-i),
+//   2, 1: quad_perm xor.
+// pair_step<o>(lo, hi, upper) returns, in every lane, the sum of the value this
+// lane keeps (lo in lower lanes, hi in upper lanes) and the partner's value of
+// the same index.
+template <int kOff>
+__device__ __forceinline__ float pair_step(float lo, float hi, bool upper) {
+  if constexpr (kOff == 32 || kOff == 16) {
+    // swap(vdst = lo, vsrc = hi): lower lanes get the partner's lo in the
+    // second result, upper lanes get the partner's hi in the first.
+    const auto r = kOff == 32
+                       ? __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi),
+                                                          false, false)
+                       : __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi),
+                                                          false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    constexpr int kCtrl = kOff == 8 ? 0x140 : kOff == 4 ? 0x141 : kOff == 2 ? 0x4E : 0xB1;
+    const float keep = upper ? hi : lo;
+    const float send = upper ? lo : hi;
+    return keep + dpp_f32<kCtrl>(send);
+  }
+}
+
+template <int kOff>
+__device__ __forceinline__ float pair_all(float v) {
+  return pair_step<kOff>(v, v, false);
+}
+
+// Butterfly reduction of N values per lane over the 64 lanes (N a power of two,
+// N <= 64).  Afterwards v[0] in lane l holds the wave-wide sum of value
+// index l >> (6 - log2 N); every lane of that group holds the same bits.  Each
+// halving step costs one exchange per remaining pair, so reducing N values
+// takes about N exchanges instead of 6 N.
+template <int N>
+__device__ __forceinline__ void wave_reduce_multi(float* v, int lane) {
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two <= 64");
+#define K3_HALVE(OFF, CNT)                                                       \
+  if constexpr (N >= (CNT)) {                                                    \
+    const bool up = (lane & (OFF)) != 0;                                         \
+    _Pragma("unroll") for (int i = 0; i < (CNT) / 2; ++i)                        \
+      v[i] = pair_step<OFF>(v[i], v[i + (CNT) / 2], up);                         \
+  }
+  // Step s halves the count with lane bit 5-s; N values need log2 N steps.
+  if constexpr (N >= 2) { K3_HALVE(32, N) }
+  if constexpr (N >= 4) { K3_HALVE(16, N / 2) }
+  if constexpr (N >= 8) { K3_HALVE(8, N / 4) }
+  if constexpr (N >= 16) { K3_HALVE(4, N / 8) }
+  if constexpr (N >= 32) { K3_HALVE(2, N / 16) }
+  if constexpr (N >= 64) { K3_HALVE(1, N / 32) }
+#undef K3_HALVE
+  // Remaining lane bits: plain all-reduce of the single value.
+  if constexpr (N < 2) v[0] = pair_all<32>(v[0]);
+  if constexpr (N < 4) v[0] = pair_all<16>(v[0]);
+  if constexpr (N < 8) v[0] = pair_all<8>(v[0]);
+  if constexpr (N < 16) v[0] = pair_all<4>(v[0]);
+  if constexpr (N < 32) v[0] = pair_all<2>(v[0]);
+  if constexpr (N < 64) v[0] = pair_all<1>(v[0]);
+}
+
+template <int N>
+constexpr int log2c() {
+  return N <= 1 ? 0 : 1 + log2c<N / 2>();
+}
+
 // ---------------------------------------------------------------- activations
 // K3 SiTU (provider_moe.cpp:524-533, tools/cuda_moe_kernels.cu:160-177) and
 // SiLU-GLU, both in fp32 with the library's IEEE math flags.
@@ -165,8 +233,18 @@ __device__ __forceinline__ float activate(int act, float g, float u) {
 }
 
 // ---------------------------------------------------------------- loads
+// Global-address-space views: loads through them compile to global_load (vmcnt
+// only) rather than flat_load, which would also count against lgkmcnt and make
+// every LDS wait drain the in-flight weight loads.
+typedef __attribute__((address_space(1))) const u32x4 gu32x4;
+typedef __attribute__((address_space(1))) const uint8_t gu8;
+
 __device__ __forceinline__ u32x4 load_chunk(const uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return __builtin_nontemporal_load((gu32x4*)(p));
+}
+
+__device__ __forceinline__ uint32_t load_scale(const uint8_t* p) {
+  return *(gu8*)(p);
 }
 
 template <typename T>

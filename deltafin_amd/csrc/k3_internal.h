@@ -61,7 +61,12 @@ struct Workspace {
   int32_t* epos;        // [max_edges] edge -> position
   int32_t* poff;        // [max_positions + 1]
   VerifyPlanDev* plan;  // 1
+  int32_t* cnt;         // [kWorkspaceCounters] arrival counters, zero between calls
 };
+
+// Arrival counters in every workspace (one per output row range of the
+// decode down kernel).  Each call returns them to zero.
+constexpr int kWorkspaceCounters = 4096;
 
 uint64_t workspace_bytes(const Geo& g, int max_edges, int max_positions);
 bool carve_workspace(void* base, uint64_t bytes, const Geo& g, int max_edges,
@@ -99,5 +104,37 @@ int launch_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed,
                         uint64_t stream_id, hipStream_t stream);
 
 int device_cu_count();
+// Resident workgroups per CU for `kernel` at `block` threads (cached per
+// kernel and device; 1 when the runtime cannot say).
+int occupancy_blocks_per_cu(const void* kernel, int block, size_t dynamic_lds);
+
+// Kernel classes for the optional per-launch timing (k3_hip_timing_begin/end).
+enum KernelClass : int {
+  KC_GEMV = 0,
+  KC_ACTIVATE,
+  KC_ROUTE,
+  KC_GLU_DECODE,
+  KC_DOWN_DECODE,
+  KC_VERIFY_PLAN,
+  KC_GLU_VERIFY,
+  KC_DOWN_VERIFY,
+  KC_COMBINE,
+  KC_SYNTH,
+  KC_COUNT
+};
+
+// Brackets one kernel launch with two hipEvents on its stream while timing is
+// enabled; a no-op otherwise.
+class TimedLaunch {
+ public:
+  TimedLaunch(int kernel_class, hipStream_t stream);
+  ~TimedLaunch();
+  TimedLaunch(const TimedLaunch&) = delete;
+  TimedLaunch& operator=(const TimedLaunch&) = delete;
+
+ private:
+  int slot_;
+  hipStream_t stream_;
+};
 
 }  // namespace k3

@@ -21,6 +21,8 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
+#include <unordered_map>
 
 #include "k3_device.h"
 #include "k3_internal.h"
@@ -105,6 +107,47 @@ __device__ __forceinline__ const uint8_t* route_span(const TokenRoute& r, int e)
 }
 __device__ __forceinline__ float route_weight(const TokenRoute& r, int e) {
   return r.bank ? r.wdev[e] : r.w[e];
+}
+
+// A wave's copy of the route: lane e (< n) holds expert e's span address and
+// weight, loaded once so later lookups are register reads (v_readlane) rather
+// than memory loads queued behind in-flight weight batches.
+struct RouteRegs {
+  uint32_t lo, hi;
+  float w;
+};
+
+__device__ __forceinline__ RouteRegs route_regs(const TokenRoute& r, int lane) {
+  RouteRegs o;
+  o.lo = o.hi = 0u;
+  o.w = 0.0f;
+  if (lane < r.n) {
+    const uint64_t p = reinterpret_cast<uint64_t>(route_span(r, lane));
+    o.lo = (uint32_t)p;
+    o.hi = (uint32_t)(p >> 32);
+    o.w = route_weight(r, lane);
+  }
+  return o;
+}
+
+// e must be uniform across the wave.
+__device__ __forceinline__ const uint8_t* span_of(const RouteRegs& rr, int e) {
+  const uint32_t lo = __builtin_amdgcn_readlane(rr.lo, e);
+  const uint32_t hi = __builtin_amdgcn_readlane(rr.hi, e);
+  return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ float weight_of(const RouteRegs& rr, int e) {
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rr.w), e));
+}
+
+// Wait until every memory operation this wave issued has completed (stores
+// acknowledged by the level their scope names).  The signal fences keep the
+// compiler from moving memory operations across the wait.
+__device__ __forceinline__ void wait_mem_complete() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt unconstrained
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // ======================================================================
@@ -210,70 +253,355 @@ __global__ __launch_bounds__(256) void k_gemv_multi(const uint8_t* __restrict__ 
 }
 
 // ======================================================================
-// decode phase A: gate/up rows of one expert + activation -> h
+// column split: the S waves of a workgroup share a block of rows, wave w
+// owning chunks [w*cw, w*cw + cw) of every row (cw = ceil(G / S) <= 64), so
+// each lane holds exactly one activation chunk and every load instruction of a
+// wave reads cw * 16 contiguous bytes of one row.  Lanes past the row's end
+// load the row's last chunk again (same cache lines, no extra HBM traffic) and
+// multiply it by a zero activation, so the load stream has no branches and the
+// compiler issues a whole row block's loads back to back.
 // ======================================================================
-template <typename XT, int CPL, int kRows>
-__global__ __launch_bounds__(256) void k_glu_decode(const TokenRoute route, const Geo g,
-                                                    const XT* __restrict__ x,
-                                                    float* __restrict__ h) {
-  const int lane = threadIdx.x & 63;
-  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int upe = g.inter / kRows;
-  if (unit >= route.n * upe) return;
-  const int e = unit / upe;
-  const int r0 = (unit - e * upe) * kRows;
+struct ColSplit {
+  int cc;      // chunk this lane loads (clamped into the row)
+  bool valid;  // lane owns a real chunk
+};
+
+__device__ __forceinline__ ColSplit col_split(int G, int S, int wave, int lane) {
+  const int cw = (G + S - 1) / S;
+  const int c = wave * cw + lane;
+  ColSplit r;
+  r.valid = lane < cw && c < G;
+  r.cc = r.valid ? c : G - 1;
+  return r;
+}
+
+template <typename XT>
+__device__ __forceinline__ void load_x_chunk(XChunk<XT>& xc, const XT* x, const ColSplit& cs);
+
+template <>
+__device__ __forceinline__ void load_x_chunk<uint16_t>(XChunk<uint16_t>& xc, const uint16_t* x,
+                                                       const ColSplit& cs) {
+  xc.load(x, cs.cc);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) xc.v[i] = cs.valid ? xc.v[i] : 0u;
+}
+
+template <>
+__device__ __forceinline__ void load_x_chunk<float>(XChunk<float>& xc, const float* x,
+                                                    const ColSplit& cs) {
+  xc.load(x, cs.cc);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) xc.v[i] = cs.valid ? xc.v[i] : 0.0f;
+}
+
+// Workgroup barrier ordering only LDS: outstanding global loads (prefetched
+// weight batches) and global stores stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// ======================================================================
+// decode phase A: gate/up rows + activation -> h, streamed
+// The grid is sized to the resident capacity (one round).  Workgroup b owns a
+// contiguous run of (gate row, up row) pairs of the flattened [expert][row]
+// space; its S waves split every row's chunks (column split above).  A batch
+// is kR row pairs: each wave issues its 2 kR quarter-row loads at once while
+// the previous batch is reduced (double buffer), forms one partial per row, and
+// one butterfly reduces the 2 kR partials across the wave.  The S wave
+// partials meet in LDS (two slots, one LDS-only barrier per batch); kR lanes
+// of wave 0 sum them in wave order, apply the activation and store h.
+// ======================================================================
+template <typename XT, int kR>
+struct GluBatch {
+  u32x4 wg[kR], wu[kR];
+  uint32_t sg[kR], su[kR];
+};
+
+template <typename XT, int kR>
+__device__ __forceinline__ void glu_load(GluBatch<XT, kR>& bt, const RouteRegs& rr,
+                                         const Geo& g, int pair0, const ColSplit& cs) {
+  const int e = pair0 / g.inter;
+  const int r0 = pair0 - e * g.inter;
   const int G = g.hidden >> 5;
   const size_t cp = (size_t)g.hidden >> 1;
-  const uint8_t* span = route_span(route, e);
-  const uint8_t* gp = span + g.w1p + (size_t)r0 * cp;
-  const uint8_t* gs = span + g.w1s + (size_t)r0 * G;
-  const uint8_t* up = span + g.w3p + (size_t)r0 * cp;
-  const uint8_t* us = span + g.w3s + (size_t)r0 * G;
+  const uint8_t* span = span_of(rr, e);
+  const uint8_t* gp = span + g.w1p + (size_t)r0 * cp + (size_t)cs.cc * 16;
+  const uint8_t* up = span + g.w3p + (size_t)r0 * cp + (size_t)cs.cc * 16;
+  const uint8_t* gs = span + g.w1s + (size_t)r0 * G + cs.cc;
+  const uint8_t* us = span + g.w3s + (size_t)r0 * G + cs.cc;
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    bt.wg[r] = load_chunk(gp + (size_t)r * cp);
+    bt.wu[r] = load_chunk(up + (size_t)r * cp);
+    bt.sg[r] = load_scale(gs + (size_t)r * G);
+    bt.su[r] = load_scale(us + (size_t)r * G);
+  }
+}
 
-  XChunk<XT> xs[CPL];
+template <typename XT, int kR>
+__device__ __forceinline__ void glu_finish(const GluBatch<XT, kR>& bt, const XChunk<XT>& xc,
+                                           const Geo& g, int pair0, int lane, int wave, int S,
+                                           float (*red)[4][2 * kR], int slot,
+                                           float* __restrict__ h) {
+  constexpr int N = 2 * kR;
+  constexpr int L = log2c<N>();
+  float v[N];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const int chunk = lane + 64 * c;
-    if (chunk < G) xs[c].load(x, chunk);
+  for (int r = 0; r < kR; ++r) {
+    v[r] = xc.dot(bt.wg[r]) * e8m0_scale(bt.sg[r]);
+    v[kR + r] = xc.dot(bt.wu[r]) * e8m0_scale(bt.su[r]);
   }
-  float ag[kRows], au[kRows];
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    float a = 0.0f, b = 0.0f;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int chunk = lane + 64 * c;
-      if (chunk < G) {
-        const u32x4 wg = load_chunk(gp + (size_t)r * cp + (size_t)chunk * 16);
-        const u32x4 wu = load_chunk(up + (size_t)r * cp + (size_t)chunk * 16);
-        const float sg = e8m0_scale(gs[(size_t)r * G + chunk]);
-        const float su = e8m0_scale(us[(size_t)r * G + chunk]);
-        a = fmaf(xs[c].dot(wg), sg, a);
-        b = fmaf(xs[c].dot(wu), su, b);
-      }
+  wave_reduce_multi<N>(v, lane);
+  if ((lane & ((1 << (6 - L)) - 1)) == 0) red[slot][wave][lane >> (6 - L)] = v[0];
+  lds_barrier();
+  if (wave == 0 && lane < kR) {
+    float gv = red[slot][0][lane], uv = red[slot][0][kR + lane];
+    for (int w = 1; w < S; ++w) {
+      gv += red[slot][w][lane];
+      uv += red[slot][w][kR + lane];
     }
-    ag[r] = a;
-    au[r] = b;
+    h[(size_t)pair0 + lane] = activate(g.act, gv, uv);
   }
-  float* hrow = h + (size_t)e * g.inter + r0;
+}
+
+template <typename XT, int kR>
+__global__ __launch_bounds__(256) void k_glu_stream(const TokenRoute route, const Geo g,
+                                                    const XT* __restrict__ x,
+                                                    float* __restrict__ h,
+                                                    int batches_per_block) {
+  __shared__ float red[2][4][2 * kR];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int S = blockDim.x >> 6;
+  // Workgroup b takes batches b, b + NB, b + 2 NB, ... (NB = grid size): at
+  // any moment the grid works through one contiguous window of the weights,
+  // which keeps the HBM channels evenly and sequentially loaded.  The host
+  // makes batches_per_block even and the batch count a multiple of the grid,
+  // so the pipeline below has no conditional loads: two batches are always in
+  // flight while one is reduced.
+  const int NB = gridDim.x;
+  const int nb = batches_per_block;
+  const int b0 = blockIdx.x;
+  const ColSplit cs = col_split(g.hidden >> 5, S, wave, lane);
+  const RouteRegs rr = route_regs(route, lane);
+  XChunk<XT> xc;
+  load_x_chunk<XT>(xc, x, cs);
+  GluBatch<XT, kR> A, B;
+  glu_load<XT, kR>(A, rr, g, b0 * kR, cs);
+  glu_load<XT, kR>(B, rr, g, (b0 + NB) * kR, cs);
+  int k = 0;
+  for (; k + 2 < nb; k += 2) {
+    glu_finish<XT, kR>(A, xc, g, (b0 + k * NB) * kR, lane, wave, S, red, 0, h);
+    glu_load<XT, kR>(A, rr, g, (b0 + (k + 2) * NB) * kR, cs);
+    glu_finish<XT, kR>(B, xc, g, (b0 + (k + 1) * NB) * kR, lane, wave, S, red, 1, h);
+    glu_load<XT, kR>(B, rr, g, (b0 + (k + 3) * NB) * kR, cs);
+  }
+  glu_finish<XT, kR>(A, xc, g, (b0 + k * NB) * kR, lane, wave, S, red, 0, h);
+  glu_finish<XT, kR>(B, xc, g, (b0 + (k + 1) * NB) * kR, lane, wave, S, red, 1, h);
+}
+
+// ======================================================================
+// Short-wave decode kernels (scheme 1): one workgroup per (expert, kR row
+// pairs) for gate/up; one workgroup per block of output rows (one wave per
+// expert) for down.  Selected with K3_DECODE_SCHEME=1.
+// ======================================================================
+template <typename XT, int kR>
+__global__ __launch_bounds__(256) void k_glu_short(const TokenRoute route, const Geo g,
+                                                   const XT* __restrict__ x,
+                                                   float* __restrict__ h) {
+  constexpr int N = 2 * kR;
+  constexpr int L = log2c<N>();
+  __shared__ float red[4][N];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int S = blockDim.x >> 6;
+  const int G = g.hidden >> 5;
+  const int upe = g.inter / kR;
+  const int e = blockIdx.x / upe;
+  const int r0 = (blockIdx.x - e * upe) * kR;
+  const ColSplit cs = col_split(G, S, wave, lane);
+  const uint8_t* span = route_span(route, e);
+  GluBatch<XT, kR> bt;
+  {
+    const size_t cp = (size_t)g.hidden >> 1;
+    const uint8_t* gp = span + g.w1p + (size_t)r0 * cp + (size_t)cs.cc * 16;
+    const uint8_t* up = span + g.w3p + (size_t)r0 * cp + (size_t)cs.cc * 16;
+    const uint8_t* gs = span + g.w1s + (size_t)r0 * G + cs.cc;
+    const uint8_t* us = span + g.w3s + (size_t)r0 * G + cs.cc;
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const float gv = wave_sum(ag[r]);
-    const float uv = wave_sum(au[r]);
-    if (lane == 0) hrow[r] = activate(g.act, gv, uv);
+    for (int r = 0; r < kR; ++r) {
+      bt.wg[r] = load_chunk(gp + (size_t)r * cp);
+      bt.wu[r] = load_chunk(up + (size_t)r * cp);
+      bt.sg[r] = load_scale(gs + (size_t)r * G);
+      bt.su[r] = load_scale(us + (size_t)r * G);
+    }
+  }
+  XChunk<XT> xc;
+  load_x_chunk<XT>(xc, x, cs);
+  float v[N];
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    v[r] = xc.dot(bt.wg[r]) * e8m0_scale(bt.sg[r]);
+    v[kR + r] = xc.dot(bt.wu[r]) * e8m0_scale(bt.su[r]);
+  }
+  wave_reduce_multi<N>(v, lane);
+  if ((lane & ((1 << (6 - L)) - 1)) == 0) red[wave][lane >> (6 - L)] = v[0];
+  __syncthreads();
+  if ((int)threadIdx.x < kR) {
+    const int t = threadIdx.x;
+    float gv = red[0][t], uv = red[0][kR + t];
+    for (int w = 1; w < S; ++w) {
+      gv += red[w][t];
+      uv += red[w][kR + t];
+    }
+    h[(size_t)e * g.inter + r0 + t] = activate(g.act, gv, uv);
   }
 }
 
 // ======================================================================
 // decode phase B: down rows of every routed expert + ordered combine
+// k_down_rows: every workgroup stages the routed experts' h (n x I fp32) in
+// LDS; wave j owns output rows [j kB, j kB + kB) (grid-stride over row
+// batches, so the grid sweeps each expert's down matrix as one window) and
+// walks the experts in route order: kB x CPL row loads per expert, two experts
+// in flight, one butterfly per expert, and the route-weighted sum
+// out = sum over e in route order of w_e * y_e (tools/metal/moe_mxfp4.metal:
+// 410-445 order) accumulated in registers.
 // ======================================================================
+template <int CPL, int kB>
+struct DownBatch {
+  u32x4 w[kB][CPL];
+  uint32_t s[kB][CPL];
+};
+
+template <int CPL, int kB>
+__device__ __forceinline__ void down_load(DownBatch<CPL, kB>& bt, const uint8_t* span,
+                                          const Geo& g, const int* cc, int r0, int nrows) {
+  const int GB = g.inter >> 5;
+  const size_t cpb = (size_t)g.inter >> 1;
+  const uint8_t* dp = span + g.w2p;
+  const uint8_t* ds = span + g.w2s;
+#pragma unroll
+  for (int u = 0; u < kB; ++u) {
+    const int r = r0 + min(u, nrows - 1);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      bt.w[u][c] = load_chunk(dp + (size_t)r * cpb + (size_t)cc[c] * 16);
+      bt.s[u][c] = load_scale(ds + (size_t)r * GB + cc[c]);
+    }
+  }
+}
+
+template <int CPL, int kB>
+__device__ __forceinline__ float down_expert(const DownBatch<CPL, kB>& bt, const float* hl,
+                                             const Geo& g, const int* cc, const bool* valid,
+                                             int e, int lane) {
+  float v[kB];
+  XChunk<float> hs[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    hs[c].load(hl + (size_t)e * g.inter, cc[c]);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) hs[c].v[i] = valid[c] ? hs[c].v[i] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < kB; ++u) {
+    float a = hs[0].dot(bt.w[u][0]) * e8m0_scale(bt.s[u][0]);
+#pragma unroll
+    for (int c = 1; c < CPL; ++c) a += hs[c].dot(bt.w[u][c]) * e8m0_scale(bt.s[u][c]);
+    v[u] = a;
+  }
+  wave_reduce_multi<kB>(v, lane);
+  return v[0];
+}
+
+template <typename OT, int CPL, int kB>
+__global__ __launch_bounds__(512) void k_down_rows(const TokenRoute route, const Geo g,
+                                                   const float* __restrict__ h,
+                                                   OT* __restrict__ out, int n_batches) {
+  extern __shared__ uint4 smem_h[];
+  float* hl = reinterpret_cast<float*>(smem_h);
+  constexpr int L = log2c<kB>();
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  const int n = route.n;
+  const int GB = g.inter >> 5;
+  int cc[CPL];
+  bool valid[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    valid[c] = lane + 64 * c < GB;
+    cc[c] = min(lane + 64 * c, GB - 1);
+  }
+  const RouteRegs rreg = route_regs(route, lane);
+  const int first = blockIdx.x * nw + wave;
+  const int stride = gridDim.x * nw;
+  // First expert's rows are requested before the h staging so HBM is busy
+  // while the workgroup copies h into LDS.
+  DownBatch<CPL, kB> A, B;
+  if (first < n_batches) {
+    const int r0 = first * kB;
+    const int nrows = min(kB, g.hidden - r0);
+    down_load<CPL, kB>(A, span_of(rreg, 0), g, cc, r0, nrows);
+    down_load<CPL, kB>(B, span_of(rreg, min(1, n - 1)), g, cc, r0, nrows);
+  }
+  {
+    // h copy into LDS, 8 loads in flight per thread per round.
+    const int n16 = n * g.inter / 4;
+    const uint4* src = reinterpret_cast<const uint4*>(h);
+    for (int i0 = threadIdx.x; i0 < n16; i0 += 8 * blockDim.x) {
+      uint4 t[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) t[k] = src[min(i0 + k * (int)blockDim.x, n16 - 1)];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (i0 + k * (int)blockDim.x < n16) smem_h[i0 + k * blockDim.x] = t[k];
+    }
+  }
+  __syncthreads();
+  for (int jb = first; jb < n_batches; jb += stride) {
+    const int r0 = jb * kB;
+    const int nrows = min(kB, g.hidden - r0);
+    if (jb != first) {
+      down_load<CPL, kB>(A, span_of(rreg, 0), g, cc, r0, nrows);
+      down_load<CPL, kB>(B, span_of(rreg, min(1, n - 1)), g, cc, r0, nrows);
+    }
+    float acc = 0.0f;
+    int e = 0;
+    // Experts past the last (odd n) repeat the last expert's loads; their
+    // results are not accumulated.
+    for (; e + 2 < n; e += 2) {
+      acc += weight_of(rreg, e) * down_expert<CPL, kB>(A, hl, g, cc, valid, e, lane);
+      down_load<CPL, kB>(A, span_of(rreg, e + 2), g, cc, r0, nrows);
+      acc += weight_of(rreg, e + 1) * down_expert<CPL, kB>(B, hl, g, cc, valid, e + 1, lane);
+      down_load<CPL, kB>(B, span_of(rreg, min(e + 3, n - 1)), g, cc, r0, nrows);
+    }
+    acc += weight_of(rreg, e) * down_expert<CPL, kB>(A, hl, g, cc, valid, e, lane);
+    if (e + 1 < n) acc += weight_of(rreg, e + 1) * down_expert<CPL, kB>(B, hl, g, cc, valid, e + 1, lane);
+    const int idx = lane >> (6 - L);
+    if ((lane & ((1 << (6 - L)) - 1)) == 0 && idx < nrows) store_out(out + r0 + idx, acc);
+  }
+}
+
+// k_down_blocks: fallback when n x I fp32 does not fit in LDS.  A workgroup
+// owns rows_per_block output rows, wave w takes experts w, w + nw, ...  with
+// its h slice in registers, loads its rows kB at a time, and the ordered
+// weighted sum is formed from LDS.
 constexpr int kDownMaxRows = 64;
 
-template <typename OT, int CPLB>
-__global__ __launch_bounds__(1024) void k_down_decode(const TokenRoute route, const Geo g,
-                                                      const float* __restrict__ h,
-                                                      OT* __restrict__ out,
-                                                      int rows_per_block) {
+template <int CPLB>
+constexpr int down_max_threads() {
+  return CPLB <= 2 ? 1024 : 512;
+}
+
+template <typename OT, int CPLB, int kB>
+__global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
+    const TokenRoute route, const Geo g, const float* __restrict__ h, OT* __restrict__ out,
+    int rows_per_block) {
+  constexpr int L = log2c<kB>();
   __shared__ float ybuf[K3_HIP_MAX_TOKEN_EXPERTS][kDownMaxRows];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -281,36 +609,28 @@ __global__ __launch_bounds__(1024) void k_down_decode(const TokenRoute route, co
   const int row0 = blockIdx.x * rows_per_block;
   const int nrows = min(rows_per_block, g.hidden - row0);
   const int GB = g.inter >> 5;
-  const size_t cpb = (size_t)g.inter >> 1;
-
+  int cc[CPLB];
+  bool valid[CPLB];
+#pragma unroll
+  for (int c = 0; c < CPLB; ++c) {
+    valid[c] = lane + 64 * c < GB;
+    cc[c] = min(lane + 64 * c, GB - 1);
+  }
+  const RouteRegs rreg = route_regs(route, lane);
   for (int e = wave; e < route.n; e += nw) {
-    const uint8_t* span = route_span(route, e);
-    const uint8_t* dp = span + g.w2p + (size_t)row0 * cpb;
-    const uint8_t* ds = span + g.w2s + (size_t)row0 * GB;
-    XChunk<float> hs[CPLB];
-#pragma unroll
-    for (int c = 0; c < CPLB; ++c) {
-      const int chunk = lane + 64 * c;
-      if (chunk < GB) hs[c].load(h + (size_t)e * g.inter, chunk);
-    }
-    for (int r = 0; r < nrows; ++r) {
-      float a = 0.0f;
-#pragma unroll
-      for (int c = 0; c < CPLB; ++c) {
-        const int chunk = lane + 64 * c;
-        if (chunk < GB) {
-          const u32x4 w = load_chunk(dp + (size_t)r * cpb + (size_t)chunk * 16);
-          a = fmaf(hs[c].dot(w), e8m0_scale(ds[(size_t)r * GB + chunk]), a);
-        }
-      }
-      a = wave_sum(a);
-      if (lane == 0) ybuf[e][r] = a;
+    const uint8_t* span = span_of(rreg, e);
+    for (int rb = 0; rb < nrows; rb += kB) {
+      DownBatch<CPLB, kB> bt;
+      down_load<CPLB, kB>(bt, span, g, cc, row0 + rb, min(kB, nrows - rb));
+      const float v = down_expert<CPLB, kB>(bt, h, g, cc, valid, e, lane);
+      const int idx = lane >> (6 - L);
+      if ((lane & ((1 << (6 - L)) - 1)) == 0 && rb + idx < nrows) ybuf[e][rb + idx] = v;
     }
   }
   __syncthreads();
   for (int t = threadIdx.x; t < nrows; t += blockDim.x) {
     float acc = 0.0f;
-    for (int e = 0; e < route.n; ++e) acc += route_weight(route, e) * ybuf[e][t];
+    for (int e = 0; e < route.n; ++e) acc += weight_of(rreg, e) * ybuf[e][t];
     store_out(out + row0 + t, acc);
   }
 }
@@ -325,41 +645,76 @@ __global__ void k_activate(const float* __restrict__ gate, const float* __restri
 }
 
 // ======================================================================
-// router: top-k (descending, lower index on ties, NaN never selected ahead of
-// a number) + softmax over the selected logits; one workgroup per position
+// router: top-k (descending value, lower index on ties, NaN ranked as -inf,
+// -0 equal to +0) + softmax over the selected logits; one workgroup per
+// position.  Each logit becomes a 64-bit key (order-preserving value bits,
+// then the complemented index), so "better" is plain unsigned ">".
+//   stage 1: within each 64-logit segment, a logit's rank is the number of
+//            larger keys in the segment; ranks < k are candidates (the global
+//            top k is always inside the union of the segments' top k);
+//   stage 2: each candidate's rank among all candidates is its global rank.
 // ======================================================================
-__global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits, int n_bank,
-                                               int top_k, int32_t* __restrict__ ids_ws,
-                                               float* __restrict__ w_ws,
-                                               int32_t* __restrict__ ids_user,
-                                               float* __restrict__ w_user) {
-  extern __shared__ float lg[];
+constexpr int kRouteMaxBank = 4096;
+
+__device__ __forceinline__ uint64_t route_key(float v, int i) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) u = 0xff800000u;  // NaN -> -inf
+  if (u == 0x80000000u) u = 0u;                           // -0 -> +0
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint64_t)(~(uint32_t)i);
+}
+
+__global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits, int n_bank,
+                                                int top_k, int32_t* __restrict__ ids_ws,
+                                                float* __restrict__ w_ws,
+                                                int32_t* __restrict__ ids_user,
+                                                float* __restrict__ w_user) {
+  extern __shared__ uint64_t rsm[];  // keys [nseg * 64], then candidates [nseg * top_k]
   __shared__ int sel[K3_HIP_MAX_TOKEN_EXPERTS];
+  __shared__ float ex[K3_HIP_MAX_TOKEN_EXPERTS];
   const int p = blockIdx.x;
   const float* src = logits + (size_t)p * n_bank;
-  for (int i = threadIdx.x; i < n_bank; i += blockDim.x) {
-    const float v = src[i];
-    lg[i] = (v != v) ? -INFINITY : v;
+  const int nseg = (n_bank + 63) >> 6;
+  uint64_t* keys = rsm;
+  uint64_t* cand = rsm + (size_t)nseg * 64;
+  const int ncand = nseg * top_k;
+  for (int i = threadIdx.x; i < nseg * 64; i += blockDim.x)
+    keys[i] = i < n_bank ? route_key(src[i], i) : 0ull;  // 0 ranks below every real key
+  for (int i = threadIdx.x; i < ncand; i += blockDim.x) cand[i] = 0ull;
+  __syncthreads();
+  // stage 1
+  for (int i = threadIdx.x; i < nseg * 64; i += blockDim.x) {
+    const uint64_t k = keys[i];
+    const uint64_t* seg = keys + (i & ~63);
+    int rank = 0;
+#pragma unroll 16
+    for (int j = 0; j < 64; ++j) rank += seg[j] > k;
+    if (i < n_bank && rank < top_k) cand[(i >> 6) * top_k + rank] = k;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < n_bank; i += blockDim.x) {
-    const float li = lg[i];
+  // stage 2
+  for (int t = threadIdx.x; t < ncand; t += blockDim.x) {
+    const uint64_t k = cand[t];
+    if (k == 0ull) continue;
     int rank = 0;
-    for (int j = 0; j < n_bank; ++j) {
-      const float lj = lg[j];
-      rank += (lj > li) || (lj == li && j < i);
+#pragma unroll 8
+    for (int j = 0; j < ncand; ++j) rank += cand[j] > k;
+    if (rank < top_k) sel[rank] = (int)(~(uint32_t)k);
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int j = threadIdx.x;
+    if (j < top_k) {
+      const float top = src[sel[0]];
+      float lj = src[sel[j]];
+      if (lj != lj) lj = -INFINITY;
+      ex[j] = expf(lj - top);
     }
-    if (rank < top_k) sel[rank] = i;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    const float top = lg[sel[0]];
-    float ex[K3_HIP_MAX_TOKEN_EXPERTS];
     float sum = 0.0f;
-    for (int j = 0; j < top_k; ++j) {
-      ex[j] = expf(lg[sel[j]] - top);
-      sum += ex[j];
-    }
+    for (int j = 0; j < top_k; ++j) sum += ex[j];
     for (int j = 0; j < top_k; ++j) {
       const float w = ex[j] / sum;
       const int o = p * top_k + j;
@@ -678,7 +1033,26 @@ __global__ void k_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed, 
 namespace {
 
 constexpr int kRowsGemv = 8;
-constexpr int kRowsGlu = 8;
+// Rows per wave of the decode gate/up kernel (gate and up each).
+#ifndef K3_GLU_ROWS
+#define K3_GLU_ROWS 8
+#endif
+constexpr int kRowsGlu = K3_GLU_ROWS;
+// Rows per expert load of the decode down kernel with a one-chunk h slice.
+#ifndef K3_DOWN_BATCH
+#define K3_DOWN_BATCH 4
+#endif
+constexpr int kDownBatch = K3_DOWN_BATCH;
+// Resident workgroups per CU the streaming decode kernels aim for (capped by
+// the kernel's occupancy): enough waves to keep ~64 KB of loads in flight per
+// CU without crowding the memory queues.
+// 2: streaming decode kernels (default); 1: short-wave kernels.
+#ifndef K3_DECODE_SCHEME
+#define K3_DECODE_SCHEME 2
+#endif
+#ifndef K3_GLU_BPC
+#define K3_GLU_BPC 2
+#endif
 constexpr int kRowsVerifyA = 8;
 constexpr int kRowsVerifyB = 16;
 
@@ -696,6 +1070,8 @@ int gemv1_dispatch(const uint8_t* p, const uint8_t* s, const XT* x, OT* y, int r
   const int cpl = (G + 63) / 64;
   const int waves = (rows + kRowsGemv - 1) / kRowsGemv;
   const dim3 grid((waves + 3) / 4), block(256);
+  if (cpl > 4) return -1;  // caller falls back to the LDS kernel
+  TimedLaunch tl(KC_GEMV, st);
   switch (cpl) {
     case 1: hipLaunchKernelGGL((k_gemv1<XT, OT, 1, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
     case 2: hipLaunchKernelGGL((k_gemv1<XT, OT, 2, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
@@ -715,6 +1091,7 @@ int gemv_multi_dispatch(const uint8_t* p, const uint8_t* s, const XT* x, OT* y, 
   if (group < 1) return fail(K3_HIP_E_INVALID, "mxfp4 GEMV: cols=%d too wide for LDS staging", cols);
   group = std::min(group, batches);
   const int waves = (rows + kRowsGemv - 1) / kRowsGemv;
+  TimedLaunch tl(KC_GEMV, st);
   hipLaunchKernelGGL((k_gemv_multi<XT, OT, kRowsGemv>), dim3((waves + 3) / 4), dim3(256),
                      (unsigned)(group * per), st, p, s, x, y, rows, cols, batches, group);
   return launched("mxfp4 GEMV (multi) launch");
@@ -762,6 +1139,7 @@ int launch_activation(const float* gate, const float* up, float* h, int64_t n, i
                       hipStream_t st) {
   const int64_t blocks = (n + 255) / 256;
   if (blocks > INT32_MAX) return fail(K3_HIP_E_INVALID, "activation grid too large");
+  TimedLaunch tl(KC_ACTIVATE, st);
   hipLaunchKernelGGL(k_activate, dim3((unsigned)blocks), dim3(256), 0, st, gate, up, h, n, act);
   return launched("activation launch");
 }
@@ -769,13 +1147,18 @@ int launch_activation(const float* gate, const float* up, float* h, int64_t n, i
 int launch_route(const float* logits, int n_bank, int top_k, int n_positions, int32_t* ids_ws,
                  float* w_ws, int32_t* ids_user, float* w_user, hipStream_t st) {
   if (!logits) return fail(K3_HIP_E_INVALID, "router: null logits");
-  if (n_bank <= 0 || n_bank > 16384)
-    return fail(K3_HIP_E_INVALID, "router: n_bank must be in [1, 16384]");
+  if (n_bank <= 0 || n_bank > kRouteMaxBank)
+    return fail(K3_HIP_E_INVALID, "router: n_bank must be in [1, %d]", kRouteMaxBank);
   if (top_k <= 0 || top_k > K3_HIP_MAX_TOKEN_EXPERTS || top_k > n_bank)
     return fail(K3_HIP_E_INVALID, "router: top_k must be in [1, min(%d, n_bank)]",
                 K3_HIP_MAX_TOKEN_EXPERTS);
-  hipLaunchKernelGGL(k_route, dim3(n_positions), dim3(256), (unsigned)(n_bank * sizeof(float)),
-                     st, logits, n_bank, top_k, ids_ws, w_ws, ids_user, w_user);
+  if (n_positions <= 0) return fail(K3_HIP_E_INVALID, "router: no positions");
+  const int nseg = (n_bank + 63) / 64;
+  const int threads = std::min(1024, nseg * 64);
+  const size_t lds = (size_t)nseg * (64 + top_k) * sizeof(uint64_t);
+  TimedLaunch tl(KC_ROUTE, st);
+  hipLaunchKernelGGL(k_route, dim3(n_positions), dim3(threads), (unsigned)lds, st, logits, n_bank,
+                     top_k, ids_ws, w_ws, ids_user, w_user);
   return launched("router launch");
 }
 
@@ -785,38 +1168,116 @@ template <typename XT>
 int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, float* h,
                         hipStream_t st) {
   const int G = g.hidden / 32;
-  const int cpl = (G + 63) / 64;
-  const int units = route.n * (g.inter / kRowsGlu);
-  const dim3 grid((units + 3) / 4), block(256);
-  switch (cpl) {
-    case 1: hipLaunchKernelGGL((k_glu_decode<XT, 1, kRowsGlu>), grid, block, 0, st, route, g, x, h); break;
-    case 2: hipLaunchKernelGGL((k_glu_decode<XT, 2, kRowsGlu>), grid, block, 0, st, route, g, x, h); break;
-    case 3: hipLaunchKernelGGL((k_glu_decode<XT, 3, kRowsGlu>), grid, block, 0, st, route, g, x, h); break;
-    case 4: hipLaunchKernelGGL((k_glu_decode<XT, 4, kRowsGlu>), grid, block, 0, st, route, g, x, h); break;
-    default: return fail(K3_HIP_E_INVALID, "decode layer: hidden %d exceeds 8192", g.hidden);
+  const int S = (G + 63) / 64;
+  if (S > 4) return fail(K3_HIP_E_INVALID, "decode layer: hidden %d exceeds 8192", g.hidden);
+  if (g.inter % kRowsGlu != 0) return fail(K3_HIP_E_INVALID, "decode layer: bad intermediate");
+#if K3_DECODE_SCHEME == 1
+  {
+    TimedLaunch tl(KC_GLU_DECODE, st);
+    hipLaunchKernelGGL((k_glu_short<XT, kRowsGlu>), dim3(route.n * (g.inter / kRowsGlu)),
+                       dim3(64 * S), 0, st, route, g, x, h);
+    return launched("decode gate/up launch");
   }
+#endif
+  const void* kern = reinterpret_cast<const void*>(&k_glu_stream<XT, kRowsGlu>);
+  const int occ = std::min(K3_GLU_BPC, occupancy_blocks_per_cu(kern, 64 * S, 0));
+  const int slots = std::max(1, device_cu_count() * occ);
+  // The grid must divide the batch count into an even number per workgroup:
+  // take the largest such grid that fits the resident slots.
+  const int nbt = route.n * g.inter / kRowsGlu;
+  int grid = 0;
+  for (int cand = std::min(slots, nbt / 2); cand >= 1; --cand) {
+    if (nbt % (2 * cand) == 0) {
+      grid = cand;
+      break;
+    }
+  }
+  if (grid == 0) return fail(K3_HIP_E_INVALID, "decode layer: batch count %d is odd", nbt);
+  TimedLaunch tl(KC_GLU_DECODE, st);
+  hipLaunchKernelGGL((k_glu_stream<XT, kRowsGlu>), dim3(grid), dim3(64 * S), 0, st, route, g, x,
+                     h, nbt / grid);
   return launched("decode gate/up launch");
 }
 
-template <typename OT>
-int down_decode_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
-                         hipStream_t st) {
-  const int GB = g.inter / 32;
-  const int cplb = (GB + 63) / 64;
+int max_dynamic_lds() {
+  static std::mutex mu;
+  static std::unordered_map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 65536;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+      v <= 0) {
+    (void)hipGetLastError();
+    v = 65536;
+  }
+  cache[dev] = v;
+  return v;
+}
+
+template <typename OT, int CPL, int kB>
+int down_rows_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
+                     hipStream_t st) {
+  const size_t lds = (size_t)route.n * g.inter * sizeof(float);
+  const void* kern = reinterpret_cast<const void*>(&k_down_rows<OT, CPL, kB>);
+  if (lds > 65536) {
+    static std::mutex mu;
+    static std::unordered_map<int, size_t> raised;  // per device
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(mu);
+    if (raised[dev] < lds) {
+      const hipError_t e =
+          hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return hip_fail("decode down: LDS attribute", e);
+      raised[dev] = lds;
+    }
+  }
+  const int cus = std::max(1, device_cu_count());
+  const int n_batches = (g.hidden + kB - 1) / kB;
+  const int nw = std::max(1, std::min(8, (n_batches + cus - 1) / cus));
+  const int blocks = std::min(cus, (n_batches + nw - 1) / nw);
+  TimedLaunch tl(KC_DOWN_DECODE, st);
+  hipLaunchKernelGGL((k_down_rows<OT, CPL, kB>), dim3(blocks), dim3(64 * nw), (unsigned)lds, st,
+                     route, g, h, out, n_batches);
+  return launched("decode down/combine launch");
+}
+
+template <typename OT, int CPL, int kB>
+int down_blocks_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
+                       hipStream_t st) {
   const int cus = std::max(1, device_cu_count());
   int rpb = (g.hidden + cus - 1) / cus;
   rpb = std::min(std::max(rpb, 1), kDownMaxRows);
   const int blocks = (g.hidden + rpb - 1) / rpb;
-  const int nw = std::min(route.n, 16);
-  const dim3 grid(blocks), block(64 * nw);
-  switch (cplb) {
-    case 1: hipLaunchKernelGGL((k_down_decode<OT, 1>), grid, block, 0, st, route, g, h, out, rpb); break;
-    case 2: hipLaunchKernelGGL((k_down_decode<OT, 2>), grid, block, 0, st, route, g, h, out, rpb); break;
-    case 3: hipLaunchKernelGGL((k_down_decode<OT, 3>), grid, block, 0, st, route, g, h, out, rpb); break;
-    case 4: hipLaunchKernelGGL((k_down_decode<OT, 4>), grid, block, 0, st, route, g, h, out, rpb); break;
+  const int max_waves = down_max_threads<CPL>() / 64;
+  const int nw = std::min(route.n, max_waves);
+  TimedLaunch tl(KC_DOWN_DECODE, st);
+  hipLaunchKernelGGL((k_down_blocks<OT, CPL, kB>), dim3(blocks), dim3(64 * nw), 0, st, route, g,
+                     h, out, rpb);
+  return launched("decode down/combine launch");
+}
+
+template <typename OT>
+int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace& ws, OT* out,
+                         hipStream_t st) {
+  const int GB = g.inter / 32;
+  const int cpl = (GB + 63) / 64;
+  const size_t lds = (size_t)route.n * g.inter * sizeof(float);
+  const bool rows = K3_DECODE_SCHEME != 1 && lds <= (size_t)max_dynamic_lds();
+  switch (cpl) {
+    case 1:
+      return rows ? down_rows_launch<OT, 1, kDownBatch>(g, route, ws.h, out, st)
+                  : down_blocks_launch<OT, 1, 8>(g, route, ws.h, out, st);
+    case 2:
+      return rows ? down_rows_launch<OT, 2, 4>(g, route, ws.h, out, st)
+                  : down_blocks_launch<OT, 2, 4>(g, route, ws.h, out, st);
+    case 3: return down_blocks_launch<OT, 3, 2>(g, route, ws.h, out, st);
+    case 4: return down_blocks_launch<OT, 4, 2>(g, route, ws.h, out, st);
     default: return fail(K3_HIP_E_INVALID, "decode layer: intermediate %d exceeds 8192", g.inter);
   }
-  return launched("decode down/combine launch");
 }
 
 }  // namespace
@@ -826,25 +1287,26 @@ int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x, in
   if (route.n <= 0 || route.n > K3_HIP_MAX_TOKEN_EXPERTS)
     return fail(K3_HIP_E_INVALID, "decode layer: expert count %d outside [1, %d]", route.n,
                 K3_HIP_MAX_TOKEN_EXPERTS);
-  if (g.inter % kRowsGlu != 0) return fail(K3_HIP_E_INVALID, "decode layer: bad intermediate");
   int rc = x_dtype == K3_DTYPE_BF16
                ? glu_decode_dispatch<uint16_t>(g, route, static_cast<const uint16_t*>(x), ws.h, st)
                : glu_decode_dispatch<float>(g, route, static_cast<const float*>(x), ws.h, st);
   if (rc != K3_HIP_OK) return rc;
   return out_dtype == K3_DTYPE_BF16
-             ? down_decode_dispatch<uint16_t>(g, route, ws.h, static_cast<uint16_t*>(out), st)
-             : down_decode_dispatch<float>(g, route, ws.h, static_cast<float*>(out), st);
+             ? down_decode_dispatch<uint16_t>(g, route, ws, static_cast<uint16_t*>(out), st)
+             : down_decode_dispatch<float>(g, route, ws, static_cast<float*>(out), st);
 }
 
 int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride, int n_positions,
                             int top_k, const Workspace& ws, hipStream_t st) {
   (void)g;
+  TimedLaunch tl(KC_VERIFY_PLAN, st);
   hipLaunchKernelGGL(k_verify_plan_bank, dim3(1), dim3(256), 0, st, bank, stride, n_positions,
                      top_k, ws);
   return launched("verify plan launch");
 }
 
 int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws, hipStream_t st) {
+  TimedLaunch tl(KC_VERIFY_PLAN, st);
   hipLaunchKernelGGL(k_verify_plan_table, dim3(1), dim3(256), 0, st, table, ws);
   return launched("verify plan launch");
 }
@@ -858,6 +1320,7 @@ int glu_verify_dispatch(const Geo& g, int n_edges, const XT* x, const Workspace&
   const size_t lds = (size_t)kG * g.hidden * sizeof(XT);
   if (lds > 96 * 1024) return fail(K3_HIP_E_INVALID, "verify: hidden %d too wide", g.hidden);
   const int upe = g.inter / (4 * kRowsVerifyA);
+  TimedLaunch tl(KC_GLU_VERIFY, st);
   hipLaunchKernelGGL((k_glu_verify<XT, kRowsVerifyA>), dim3(upe * n_edges), dim3(256),
                      (unsigned)lds, st, g, x, ws);
   return launched("verify gate/up launch");
@@ -868,6 +1331,8 @@ int down_verify_dispatch(const Geo& g, int n_edges, const Workspace& ws, hipStre
   const int cplb = (GB + 63) / 64;
   const int upe = (g.hidden + 4 * kRowsVerifyB - 1) / (4 * kRowsVerifyB);
   const dim3 grid(upe * n_edges), block(256);
+  if (cplb > 4) return fail(K3_HIP_E_INVALID, "verify: intermediate %d exceeds 8192", g.inter);
+  TimedLaunch tl(KC_DOWN_VERIFY, st);
   switch (cplb) {
     case 1: hipLaunchKernelGGL((k_down_verify<1, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
     case 2: hipLaunchKernelGGL((k_down_verify<2, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
@@ -892,6 +1357,7 @@ int launch_verify_layer(const Geo& g, int n_edges, int n_positions, const void* 
   if (rc != K3_HIP_OK) return rc;
   const int64_t n = (int64_t)g.hidden * n_positions;
   const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  TimedLaunch tl(KC_COMBINE, st);
   if (out_dtype == K3_DTYPE_BF16)
     hipLaunchKernelGGL(k_combine_positions<uint16_t>, grid, block, 0, st, ws, g.hidden,
                        n_positions, static_cast<uint16_t*>(out));
@@ -906,6 +1372,7 @@ int launch_synth_bank(const Geo& g, uint8_t* bank, uint64_t stride, int n_expert
   if (!bank || n_experts <= 0 || n_experts > 65535 || stride < g.span || stride % 8 != 0 ||
       ((uintptr_t)bank & 7u) != 0 || lo < 0 || hi > 255 || lo > hi)
     return fail(K3_HIP_E_INVALID, "synth bank: invalid arguments");
+  TimedLaunch tl(KC_SYNTH, st);
   hipLaunchKernelGGL(k_synth_bank, dim3(1024, n_experts), dim3(256), 0, st, g, bank, stride,
                      first_expert, seed, lo, hi);
   return launched("synth bank launch");
@@ -917,6 +1384,7 @@ int launch_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed, uint64_
     return fail(K3_HIP_E_INVALID, "synth normal: invalid arguments");
   if (n == 0) return K3_HIP_OK;
   const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 4096);
+  TimedLaunch tl(KC_SYNTH, st);
   hipLaunchKernelGGL(k_synth_normal, dim3((unsigned)blocks), dim3(256), 0, st, out, dtype, n, seed,
                      stream_id);
   return launched("synth normal launch");

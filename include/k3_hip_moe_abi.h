@@ -299,6 +299,26 @@ void k3_hip_cache_stats(const K3HipCache* cache, long long* six);
 int k3_hip_cache_read_back(K3HipCache* cache, int layer, uint16_t id,
                            uint8_t* host_out, uint64_t bytes);
 
+/* ============================== per-launch device timing */
+/* No reference counterpart beyond the Metal bridge counters
+ * (tools/metal_moe.mm:675-681) and the per-layer phase profile
+ * (native/deltafin/src/engine.rs:4705-4902).  Between begin and end every
+ * kernel this library launches, on any stream, is bracketed by two hipEvents
+ * recorded on that stream (up to max_launches launches; later ones are
+ * counted as dropped).  end synchronises on the recorded events and returns
+ * one row per kernel class that ran. */
+typedef struct K3HipKernelTimingV1 {
+  char kernel[32];   /* kernel class: "glu_decode", "down_decode", ... */
+  int64_t launches;
+  double total_ms;
+  double min_ms;
+  double max_ms;
+} K3HipKernelTimingV1;
+
+int k3_hip_timing_begin(int max_launches);
+int k3_hip_timing_end(K3HipKernelTimingV1* out, int capacity, int* n_out,
+                      long long* dropped);
+
 /* ============================== synthetic inputs (benchmark support) */
 /* No reference counterpart.  Fill device memory with the counter-based
  * synthetic distribution shared with oracle/orc.c: packed bytes uniform,

@@ -1,0 +1,326 @@
+"""CPU pins of the oracle (no GPU).
+
+Each oracle function is checked against something it does not restate itself:
+the reference's own CPU kernels compiled from /root/reference into oracle/_ref
+(bit-exact GEMV lane order, the whole-set SiTU call), the reference's in-code
+known answers (provider_cpu_isa_test.c:60-76, provider_cuda_moe.cpp:297-422),
+the closed forms of the E2M1/E8M0 encodings, and invariants of the
+contraction (linearity, constant-code rows).  A planted-mistake test shows
+which known answers separate a swapped nibble order and a dropped scale from
+the truth (the reference's all-codes KAT misses the nibble swap; a random x
+catches it).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from deltafin_amd import synth
+
+needs_ref = pytest.mark.skipif(not oracle.ref_available(),
+                               reason="oracle/_ref not built (reference sources absent)")
+
+
+def e2m1_closed_form(code: int) -> float:
+    """OCP MX E2M1: sign bit 3, exponent bits 2..1 (bias 1), mantissa bit 0;
+    exponent 0 is subnormal (0.5 * mantissa)."""
+    sign = -1.0 if code & 8 else 1.0
+    e, m = (code >> 1) & 3, code & 1
+    mag = 0.5 * m if e == 0 else (1.0 + 0.5 * m) * 2.0 ** (e - 1)
+    return math.copysign(mag, sign)
+
+
+def dense_decode(packed, scales, rows, cols):
+    """numpy decode of the row-major layout: low nibble = even column."""
+    tab = np.array([e2m1_closed_form(c) for c in range(16)], np.float64)
+    p = np.asarray(packed, np.uint8).reshape(rows, cols // 2)
+    codes = np.empty((rows, cols), np.uint8)
+    codes[:, 0::2] = p & 15
+    codes[:, 1::2] = p >> 4
+    s = np.asarray(scales, np.uint8).reshape(rows, cols // 32).astype(np.int64)
+    sc = np.where(s == 0, 0.0, np.ldexp(1.0, (s - 127).astype(np.int32)))
+    return tab[codes] * np.repeat(sc, 32, axis=1)
+
+
+# ------------------------------------------------------------------ encodings
+def test_e2m1_all_codes():
+    for c in range(16):
+        got = oracle.e2m1(c)
+        want = e2m1_closed_form(c)
+        assert got == want and math.copysign(1, got) == math.copysign(1, want), c
+    assert oracle.e2m1(8) == 0.0 and math.copysign(1, oracle.e2m1(8)) == -1.0
+
+
+def test_e8m0_all_bytes():
+    """tools/fused_gemv.c:247-249: the byte is the fp32 exponent field."""
+    assert oracle.e8m0(0) == 0.0
+    for s in range(1, 255):
+        assert oracle.e8m0(s) == math.ldexp(1.0, s - 127), s
+    assert math.isinf(oracle.e8m0(255))
+
+
+# ------------------------------------------------------------------ GEMV
+@pytest.mark.parametrize("rows,cols,seed", [(7, 64, 1), (33, 256, 2), (64, 7168, 3), (5, 2048, 4)])
+def test_gemv_f64_matches_dense_numpy(rows, cols, seed):
+    p, s = oracle.synth_mxfp4(seed, 0, rows * cols // 2, rows * cols // 32, 110, 135)
+    x = np.random.default_rng(seed).standard_normal(cols)
+    want = dense_decode(p, s, rows, cols) @ x
+    got, mag = oracle.gemv_f64(p, s, x, rows, cols, with_mag=True)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12 * np.max(mag))
+    np.testing.assert_allclose(mag, np.abs(dense_decode(p, s, rows, cols) * x).sum(1), rtol=1e-12)
+
+
+def test_gemv_f64_linearity():
+    rows, cols = 16, 512
+    p, s = oracle.synth_mxfp4(9, 1, rows * cols // 2, rows * cols // 32)
+    rng = np.random.default_rng(9)
+    x1, x2 = rng.standard_normal(cols), rng.standard_normal(cols)
+    a, b = 0.75, -2.5
+    lhs = oracle.gemv_f64(p, s, a * x1 + b * x2, rows, cols)
+    rhs = a * oracle.gemv_f64(p, s, x1, rows, cols) + b * oracle.gemv_f64(p, s, x2, rows, cols)
+    np.testing.assert_allclose(lhs, rhs, rtol=1e-11, atol=1e-11)
+
+
+def test_gemv_constant_code_rows():
+    """Every byte 0x33 (code 3 = 1.5 in both nibbles): y_r = 1.5 * 2^(s_r-127) * sum(x)."""
+    rows, cols = 6, 256
+    p = np.full(rows * cols // 2, 0x33, np.uint8)
+    s = np.repeat(np.arange(120, 120 + rows, dtype=np.uint8), cols // 32)
+    x = np.random.default_rng(2).standard_normal(cols)
+    y = oracle.gemv_f64(p, s, x, rows, cols)
+    for r in range(rows):
+        assert y[r] == pytest.approx(1.5 * 2.0 ** (120 + r - 127) * x.sum(), rel=1e-13)
+
+
+def test_gemv_nan_on_255():
+    rows, cols = 4, 64
+    p, s = oracle.synth_mxfp4(4, 0, rows * cols // 2, rows * cols // 32)
+    s = s.copy()
+    s[2 * 2 + 1] = 255
+    y = oracle.gemv_f64(p, s, np.ones(cols), rows, cols)
+    assert np.isnan(y[2]) and np.all(np.isfinite(np.delete(y, 2)))
+
+
+def _kat_all_codes():
+    """provider_cuda_moe.cpp:297-360 known-answer inputs."""
+    packed = np.zeros(32, np.uint8)
+    for i in range(16):
+        ph = (2 * i) % 16
+        packed[i] = ph | (((ph + 1) % 16) << 4)
+        packed[16 + i] = (15 - ph) | ((14 - ph) << 4)
+    scales = np.array([127, 126], np.uint8)
+    x = np.zeros((2, 32), np.float32)
+    x[0] = np.arange(32) / 32.0
+    x[1] = (np.arange(32) - 15.0) / 17.0
+    return packed, scales, x
+
+
+def _kat_expected(packed, scales, x, swap_nibbles=False, drop_scale=False):
+    out = np.zeros((2, 2))
+    for b in range(2):
+        for r in range(2):
+            tot = 0.0
+            for c in range(32):
+                byte = int(packed[r * 16 + c // 2])
+                lo, hi = byte & 15, byte >> 4
+                if swap_nibbles:
+                    lo, hi = hi, lo
+                code = lo if c % 2 == 0 else hi
+                sc = 0 if drop_scale else int(scales[r]) - 127
+                tot += math.ldexp(e2m1_closed_form(code), sc) * float(x[b, c])
+            out[b, r] = tot
+    return out
+
+
+def test_kat_all_codes_and_planted_mistakes():
+    packed, scales, x = _kat_all_codes()
+    want = _kat_expected(packed, scales, x)
+    for b in range(2):
+        got = oracle.gemv_f64(packed, scales, x[b], 2, 32)
+        assert np.max(np.abs(got - want[b])) <= 2e-4
+        lanes = oracle.gemv_f32_lanes(packed, scales, x[b], 2, 32)
+        assert np.max(np.abs(lanes - want[b])) <= 2e-4
+    # The reference KAT separates a dropped scale from the truth but NOT a
+    # swapped nibble order: x is linear in the column and the code pairs'
+    # differences cancel over the row.  A non-linear x does separate it.
+    assert np.max(np.abs(_kat_expected(packed, scales, x, drop_scale=True) - want)) > 1e-2
+    assert np.max(np.abs(_kat_expected(packed, scales, x, swap_nibbles=True) - want)) < 1e-6
+    xr = np.random.default_rng(0).standard_normal((2, 32)).astype(np.float32)
+    want_r = _kat_expected(packed, scales, xr)
+    assert np.max(np.abs(_kat_expected(packed, scales, xr, swap_nibbles=True) - want_r)) > 1e-2
+    for b in range(2):
+        assert np.max(np.abs(oracle.gemv_f64(packed, scales, xr[b], 2, 32) - want_r[b])) <= 1e-12
+
+
+def test_kat_all_0x22():
+    """provider_cpu_isa_test.c:60-76: all codes +1.0, scale 127, x = 1 -> 32.0 exactly."""
+    p = np.full(32, 0x22, np.uint8)
+    s = np.full(2, 127, np.uint8)
+    assert oracle.gemv_f64(p, s, np.ones(32), 2, 32).tolist() == [32.0, 32.0]
+    assert oracle.gemv_f32_lanes(p, s, np.ones(32, np.float32), 2, 32).tolist() == [32.0, 32.0]
+
+
+@needs_ref
+def test_kat_all_0x22_reference():
+    p = np.full(32, 0x22, np.uint8)
+    s = np.full(2, 127, np.uint8)
+    for v in ("auto", "compat"):
+        assert oracle.ref_gemv(p, s, np.ones(32, np.float32), 2, 32, v).tolist() == [32.0, 32.0]
+
+
+@needs_ref
+@pytest.mark.parametrize("rows,cols,seed", [(3, 32, 1), (17, 96, 2), (64, 7168, 3),
+                                            (128, 2048, 4), (9, 3584, 5)])
+def test_gemv_f32_lanes_bit_exact_vs_reference(rows, cols, seed):
+    """The restated lane order equals the reference CPU kernel bit for bit, in
+    both its AVX2 and 128-bit builds (tools/fused_gemv.c:282-414, :584-645)."""
+    p, s = oracle.synth_mxfp4(seed, 3, rows * cols // 2, rows * cols // 32, 2, 252)
+    x = np.random.default_rng(seed).standard_normal(cols).astype(np.float32)
+    mine = oracle.gemv_f32_lanes(p, s, x, rows, cols)
+    for v in ("auto", "compat"):
+        theirs = oracle.ref_gemv(p, s, x, rows, cols, v)
+        assert np.array_equal(mine.view(np.uint32), theirs.view(np.uint32)), v
+    mt = oracle.ref_gemv(p, s, x, rows, cols, "auto", threads=4)
+    assert np.array_equal(mine.view(np.uint32), mt.view(np.uint32))
+
+
+@needs_ref
+def test_reference_gemv_within_tolerance_of_f64():
+    rows, cols = 256, 7168
+    p, s = oracle.synth_mxfp4(31, 0, rows * cols // 2, rows * cols // 32)
+    x = np.random.default_rng(31).standard_normal(cols).astype(np.float32)
+    ref, mag = oracle.gemv_f64(p, s, x, rows, cols, with_mag=True)
+    assert oracle.cond_rel_err(oracle.ref_gemv(p, s, x, rows, cols), ref, mag, cols) <= 1e-5
+
+
+# ------------------------------------------------------------------ activations
+@pytest.mark.parametrize("g,u", [(0.0, 1.0), (1.5, -2.0), (-30.0, 3.0), (12.0, 0.5), (-0.25, 7.0)])
+def test_activations_closed_form(g, u):
+    sig = 1.0 / (1.0 + math.exp(-g))
+    assert oracle.act(oracle.ACT_SILU, g, u) == pytest.approx(g * sig * u, rel=1e-15, abs=1e-300)
+    situ = 4.0 * math.tanh(g / 4.0) * sig * 25.0 * math.tanh(u / 25.0)
+    assert oracle.act(oracle.ACT_SITU, g, u) == pytest.approx(situ, rel=1e-15, abs=1e-300)
+
+
+# ------------------------------------------------------------------ expert / layer
+def test_expert_offsets_k3_and_baseline():
+    # provider_moe.cpp:217-243 ordering; K3 span from tools/metal_moe_abi.h:20
+    assert oracle.expert_offsets(3584, 3072)[6] == 17547264
+    off = oracle.expert_offsets(7168, 2048)
+    assert off == [0, 7340032, 7798784, 15138816, 15597568, 22937600, 23396352]
+
+
+def test_expert_f64_matches_dense_numpy():
+    hidden, inter = 128, 64
+    span = oracle.synth_expert(3, 0, hidden, inter)
+    off = oracle.expert_offsets(hidden, inter)
+    x = np.random.default_rng(1).standard_normal(hidden)
+    w1 = dense_decode(span[off[0]:off[1]], span[off[1]:off[2]], inter, hidden)
+    w2 = dense_decode(span[off[2]:off[3]], span[off[3]:off[4]], hidden, inter)
+    w3 = dense_decode(span[off[4]:off[5]], span[off[5]:off[6]], inter, hidden)
+    for act in (oracle.ACT_SILU, oracle.ACT_SITU):
+        g, u = w1 @ x, w3 @ x
+        sig = 1.0 / (1.0 + np.exp(-g))
+        h = g * sig * u if act == oracle.ACT_SILU else \
+            4 * np.tanh(g / 4) * sig * 25 * np.tanh(u / 25)
+        y, hh, mag = oracle.expert_f64(span, hidden, inter, act, x)
+        np.testing.assert_allclose(hh, h, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(y, w2 @ h, rtol=1e-10, atol=1e-10 * np.max(mag))
+
+
+def test_moe_layer_f64_is_ordered_weighted_sum():
+    hidden, inter, n = 96, 64, 5
+    spans = [oracle.synth_expert(8, e, hidden, inter) for e in range(n)]
+    w = np.random.default_rng(4).random(n)
+    x = np.random.default_rng(5).standard_normal(hidden)
+    out, mag = oracle.moe_layer_f64(spans, w, hidden, inter, oracle.ACT_SILU, x)
+    want = np.zeros(hidden)
+    for e in range(n):
+        want += w[e] * oracle.expert_f64(spans[e], hidden, inter, oracle.ACT_SILU, x)[0]
+    np.testing.assert_allclose(out, want, rtol=1e-13, atol=1e-13)
+
+
+@needs_ref
+@pytest.mark.parametrize("hidden,inter,n", [(256, 128, 3), (3584, 3072, 2)])
+def test_moe_layer_situ_vs_reference_expert_set(hidden, inter, n):
+    """The reference's whole-set call (tools/fused_gemv_batch.c:465-518, SiTU,
+    libm transcendentals) agrees with the fp64 oracle to 2e-4 of the output's
+    condition scale (the provider KAT bound, provider_moe_test.cpp:268-296)."""
+    spans = [oracle.synth_expert(12, e, hidden, inter) for e in range(n)]
+    w = np.random.default_rng(6).random(n).astype(np.float32)
+    x = np.random.default_rng(7).standard_normal(hidden).astype(np.float32)
+    got = oracle.ref_expert_set(spans, w, x, hidden, inter)
+    ref, mag = oracle.moe_layer_f64(spans, w.astype(np.float64), hidden, inter, oracle.ACT_SITU, x)
+    assert oracle.cond_rel_err(got, ref, mag, inter) <= 2e-4
+
+
+def test_one_hot_expert_kat():
+    """provider_cuda_moe.cpp:362-422 at K3 shape: one nonzero per matrix gives
+    out[0] = SiTU(x0, 2 x0) and zeros elsewhere."""
+    hidden, inter = 3584, 3072
+    off = oracle.expert_offsets(hidden, inter)
+    span = np.zeros(off[6], np.uint8)
+    span[off[0]] = 0x02
+    span[off[1]] = 127
+    span[off[2]] = 0x02
+    span[off[3]] = 127
+    span[off[4]] = 0x04
+    span[off[5]] = 127
+    for v in (1.0, -0.5):
+        x = np.zeros(hidden)
+        x[0] = v
+        y, _, _ = oracle.expert_f64(span, hidden, inter, oracle.ACT_SITU, x)
+        g, u = v, 2 * v
+        want = 4 * math.tanh(g / 4) / (1 + math.exp(-g)) * 25 * math.tanh(u / 25)
+        assert y[0] == pytest.approx(want, rel=1e-14)
+        assert np.all(y[1:] == 0)
+
+
+# ------------------------------------------------------------------ router
+@pytest.mark.parametrize("n,k,seed", [(384, 16, 0), (384, 16, 1), (40, 16, 2), (16, 16, 3), (5, 1, 4)])
+def test_topk_softmax_vs_numpy(n, k, seed):
+    lg = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+    ids, w = oracle.topk_softmax(lg, k)
+    order = np.argsort(-lg.astype(np.float64), kind="stable")[:k]
+    assert ids.tolist() == order.tolist()
+    sel = lg[order].astype(np.float64)
+    e = np.exp(sel - sel.max())
+    np.testing.assert_allclose(w, e / e.sum(), rtol=1e-14)
+
+
+def test_topk_ties_prefer_lower_index():
+    lg = np.array([0.5, 2.0, 0.5, 2.0, -1.0, 0.5], np.float32)
+    ids, w = oracle.topk_softmax(lg, 4)
+    assert ids.tolist() == [1, 3, 0, 2]
+    assert w[0] == w[1] and w[2] == w[3]
+
+
+# ------------------------------------------------------------------ synthetic generator
+def test_synth_c_equals_numpy_restatement():
+    for stream in (0, 5, 1151):
+        pc, sc = oracle.synth_mxfp4(77, stream, 1000, 77, 119, 127)
+        pn, sn = synth.mxfp4_planes(77, stream, 1000, 77, 119, 127)
+        assert np.array_equal(pc, pn) and np.array_equal(sc, sn)
+    span_c = oracle.synth_expert(3, 9, 256, 64)
+    span_n = synth.expert_span(3, 9, 256, 64)
+    assert np.array_equal(span_c, span_n)
+
+
+def test_synth_distribution():
+    p, s = oracle.synth_mxfp4(1, 0, 1 << 16, 1 << 14, 119, 127)
+    nib = np.concatenate([p & 15, p >> 4])
+    counts = np.bincount(nib, minlength=16)
+    assert counts.min() > 0.9 * nib.size / 16 and counts.max() < 1.1 * nib.size / 16
+    assert s.min() == 119 and s.max() == 127
+    z = synth.normal(1, 2, 1 << 16)
+    assert abs(float(z.mean())) < 0.02 and abs(float(z.std()) - 1) < 0.02
+
+
+def test_bf16_round_trip():
+    x = np.array([1.0, -2.5, 1.00390625, 1.005859375, 3.4e38, -0.0], np.float32)
+    b = synth.to_bf16_bits(x)
+    back = synth.bf16_bits_to_f32(b)
+    assert back[0] == 1.0 and back[1] == -2.5
+    assert back[2] == 1.0            # tie -> even
+    assert back[3] == 1.0078125      # above half -> up
