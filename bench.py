@@ -48,11 +48,12 @@ OUT_BYTES = HIDDEN * 2                                    # bf16 output
 LOGIT_BYTES = N_BANK * 4
 H_BYTES = TOP_K * INTER * 4                               # fp32 h handed from gate/up to down
 LAYER_BYTES = TOP_K * SPAN + X_BYTES + LOGIT_BYTES + OUT_BYTES  # 374,371,840
+# Per launch of each decode kernel: gate/up (with the router folded in) reads
+# the logits, x and 32 gate/up matrices and writes h; down reads 16 down
+# matrices and h and writes the output row.
 KERNEL_BYTES = {
-    "glu_decode": 2 * TOP_K * MAT_BYTES + X_BYTES + H_BYTES,
+    "glu_decode": 2 * TOP_K * MAT_BYTES + X_BYTES + LOGIT_BYTES + H_BYTES,
     "down_decode": TOP_K * MAT_BYTES + H_BYTES + OUT_BYTES,
-    "route": LOGIT_BYTES + TOP_K * 8,
-    "layer_decode": LAYER_BYTES,
 }
 KERNEL_FLOPS = {
     "glu_decode": 2 * 2 * TOP_K * INTER * HIDDEN,

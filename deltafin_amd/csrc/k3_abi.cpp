@@ -773,15 +773,19 @@ int k3_hip_moe_route_layer_device(const K3HipGeometryV1* gd, const uint8_t* bank
   Workspace ws;
   if (!carve_workspace(workspace, workspace_bytes, g, top_k, 1, &ws))
     return fail(K3_HIP_E_INVALID, "route layer: workspace missing, misaligned or too small");
+  if (n_bank > 4096) return fail(K3_HIP_E_INVALID, "route layer: n_bank must be at most 4096");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int rc = launch_route(logits, n_bank, top_k, 1, ws.ids, ws.w, route_ids, route_weights, st);
-  if (rc != K3_HIP_OK) return rc;
+  // Router mode: the gate/up kernel ranks the logits and publishes the route.
   TokenRoute route;
   memset(&route, 0, sizeof(route));
   route.bank = bank;
   route.stride = expert_stride;
-  route.ids = ws.ids;
-  route.wdev = ws.w;
+  route.logits = logits;
+  route.n_bank = n_bank;
+  route.ids_pub = ws.ids;
+  route.w_pub = ws.w;
+  route.ids_user = route_ids;
+  route.w_user = route_weights;
   route.n = top_k;
   return launch_decode_layer(g, route, x, x_dtype, out, out_dtype, ws, st);
 }

@@ -25,6 +25,15 @@ struct TokenRoute {
   uint64_t stride;          // bank expert stride in bytes
   const int32_t* ids;       // bank mode: device ids [n]
   const float* wdev;        // bank mode: device weights [n]
+  // Router mode (bank mode with logits): the kernel that consumes the route
+  // computes the top n of logits[n_bank] itself and publishes ids/weights to
+  // ids_pub/w_pub (and the optional user copies) for later kernels.
+  const float* logits;
+  int n_bank;
+  int32_t* ids_pub;
+  float* w_pub;
+  int32_t* ids_user;
+  float* w_user;
   const uint8_t* ptr[K3_HIP_MAX_TOKEN_EXPERTS];
   float w[K3_HIP_MAX_TOKEN_EXPERTS];
   int n;
@@ -86,9 +95,13 @@ int launch_activation(const float* gate, const float* up, float* h, int64_t n,
 int launch_route(const float* logits, int n_bank, int top_k, int n_positions,
                  int32_t* ids_ws, float* w_ws, int32_t* ids_user,
                  float* w_user, hipStream_t stream);
+// Decode layer.  When route.logits is set (router mode) the gate/up kernel
+// routes the token itself and publishes the route to ws.ids / ws.w.
 int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x,
                         int x_dtype, void* out, int out_dtype,
                         const Workspace& ws, hipStream_t stream);
+// LDS bytes the in-kernel router needs for a bank of n_bank logits and top_k.
+size_t route_scratch_bytes(int n_bank, int top_k);
 int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride,
                             int n_positions, int top_k, const Workspace& ws,
                             hipStream_t stream);

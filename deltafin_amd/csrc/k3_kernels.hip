@@ -303,15 +303,16 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // ======================================================================
-// decode phase A: gate/up rows + activation -> h, streamed
-// The grid is sized to the resident capacity (one round).  Workgroup b owns a
-// contiguous run of (gate row, up row) pairs of the flattened [expert][row]
-// space; its S waves split every row's chunks (column split above).  A batch
-// is kR row pairs: each wave issues its 2 kR quarter-row loads at once while
-// the previous batch is reduced (double buffer), forms one partial per row, and
-// one butterfly reduces the 2 kR partials across the wave.  The S wave
-// partials meet in LDS (two slots, one LDS-only barrier per batch); kR lanes
-// of wave 0 sum them in wave order, apply the activation and store h.
+// decode phase A: gate/up rows + activation -> h
+// A unit is kR (gate row, up row) pairs of one expert; unit u covers pairs
+// [u kR, u kR + kR) of the flattened [expert][row] space.  The grid is one
+// round of resident workgroups; workgroup b takes units b, b + NB, ... so the
+// whole grid sweeps the routed weights as one advancing window.  The S waves
+// of a workgroup split every row's chunks (column split above); each wave
+// issues its 2 kR row loads at once, forms one partial per row, and a single
+// butterfly reduces the 2 kR partials across the wave.  The S wave partials
+// meet in LDS (two slots by unit parity, one barrier per unit); kR lanes of
+// wave 0 sum them in wave order, apply the activation and store h.
 // ======================================================================
 template <typename XT, int kR>
 struct GluBatch {
@@ -340,135 +341,122 @@ __device__ __forceinline__ void glu_load(GluBatch<XT, kR>& bt, const RouteRegs& 
   }
 }
 
-template <typename XT, int kR>
-__device__ __forceinline__ void glu_finish(const GluBatch<XT, kR>& bt, const XChunk<XT>& xc,
-                                           const Geo& g, int pair0, int lane, int wave, int S,
-                                           float (*red)[4][2 * kR], int slot,
-                                           float* __restrict__ h) {
-  constexpr int N = 2 * kR;
-  constexpr int L = log2c<N>();
-  float v[N];
-#pragma unroll
-  for (int r = 0; r < kR; ++r) {
-    v[r] = xc.dot(bt.wg[r]) * e8m0_scale(bt.sg[r]);
-    v[kR + r] = xc.dot(bt.wu[r]) * e8m0_scale(bt.su[r]);
-  }
-  wave_reduce_multi<N>(v, lane);
-  if ((lane & ((1 << (6 - L)) - 1)) == 0) red[slot][wave][lane >> (6 - L)] = v[0];
-  lds_barrier();
-  if (wave == 0 && lane < kR) {
-    float gv = red[slot][0][lane], uv = red[slot][0][kR + lane];
-    for (int w = 1; w < S; ++w) {
-      gv += red[slot][w][lane];
-      uv += red[slot][w][kR + lane];
-    }
-    h[(size_t)pair0 + lane] = activate(g.act, gv, uv);
-  }
-}
+__device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
+                           uint64_t* keys, int* sel, float* wsel);
+
+// Unit pipelines per gate/up workgroup (each S column-split waves) and rows
+// per unit; the launch bound follows so the register budget matches the
+// resident waves (16 waves/CU -> 128 VGPRs, 8 -> 256).
+#ifndef K3_GLU_GROUPS
+#define K3_GLU_GROUPS 2
+#endif
+#ifndef K3_GLU_ROWS
+#define K3_GLU_ROWS 4
+#endif
+constexpr int kGluMaxThreads = 256 * K3_GLU_GROUPS;
 
 template <typename XT, int kR>
-__global__ __launch_bounds__(256) void k_glu_stream(const TokenRoute route, const Geo g,
-                                                    const XT* __restrict__ x,
-                                                    float* __restrict__ h,
-                                                    int batches_per_block) {
-  __shared__ float red[2][4][2 * kR];
+__global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute route, const Geo g,
+                                                     const XT* __restrict__ x,
+                                                     float* __restrict__ h, int n_units,
+                                                     int S) {
+  constexpr int N = 2 * kR;
+  constexpr int L = log2c<N>();
+  extern __shared__ __attribute__((aligned(16))) uint64_t route_scratch[];
+  __shared__ float red[2][16][N];
+  __shared__ int sel[K3_HIP_MAX_TOKEN_EXPERTS];
+  __shared__ float wsel[K3_HIP_MAX_TOKEN_EXPERTS];
+  // The workgroup holds `groups` unit pipelines of S column-split waves; one
+  // workgroup per CU, so the router below runs once per CU.
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int S = blockDim.x >> 6;
-  // Workgroup b takes batches b, b + NB, b + 2 NB, ... (NB = grid size): at
-  // any moment the grid works through one contiguous window of the weights,
-  // which keeps the HBM channels evenly and sequentially loaded.  The host
-  // makes batches_per_block even and the batch count a multiple of the grid,
-  // so the pipeline below has no conditional loads: two batches are always in
-  // flight while one is reduced.
-  const int NB = gridDim.x;
-  const int nb = batches_per_block;
-  const int b0 = blockIdx.x;
-  const ColSplit cs = col_split(g.hidden >> 5, S, wave, lane);
-  const RouteRegs rr = route_regs(route, lane);
+  const int groups = blockDim.x / (64 * S);
+  const int grp = wave / S;
+  const int gw = wave - grp * S;  // wave within its group
+  const ColSplit cs = col_split(g.hidden >> 5, S, gw, lane);
   XChunk<XT> xc;
   load_x_chunk<XT>(xc, x, cs);
-  GluBatch<XT, kR> A, B;
-  glu_load<XT, kR>(A, rr, g, b0 * kR, cs);
-  glu_load<XT, kR>(B, rr, g, (b0 + NB) * kR, cs);
-  int k = 0;
-  for (; k + 2 < nb; k += 2) {
-    glu_finish<XT, kR>(A, xc, g, (b0 + k * NB) * kR, lane, wave, S, red, 0, h);
-    glu_load<XT, kR>(A, rr, g, (b0 + (k + 2) * NB) * kR, cs);
-    glu_finish<XT, kR>(B, xc, g, (b0 + (k + 1) * NB) * kR, lane, wave, S, red, 1, h);
-    glu_load<XT, kR>(B, rr, g, (b0 + (k + 3) * NB) * kR, cs);
+  RouteRegs rr;
+  if (route.logits) {
+    // Router mode: every workgroup ranks the logits itself (no separate
+    // launch); workgroup 0 publishes the route for the down kernel.
+    block_topk(route.logits, route.n_bank, route.n, route_scratch, sel, wsel);
+    if (blockIdx.x == 0) {
+      for (int j = threadIdx.x; j < route.n; j += blockDim.x) {
+        route.ids_pub[j] = sel[j];
+        route.w_pub[j] = wsel[j];
+        if (route.ids_user) route.ids_user[j] = sel[j];
+        if (route.w_user) route.w_user[j] = wsel[j];
+      }
+    }
+    rr.lo = rr.hi = 0u;
+    rr.w = 0.0f;
+    if (lane < route.n) {
+      const uint64_t p = reinterpret_cast<uint64_t>(route.bank) + (uint64_t)sel[lane] * route.stride;
+      rr.lo = (uint32_t)p;
+      rr.hi = (uint32_t)(p >> 32);
+      rr.w = wsel[lane];
+    }
+  } else {
+    rr = route_regs(route, lane);
   }
-  glu_finish<XT, kR>(A, xc, g, (b0 + k * NB) * kR, lane, wave, S, red, 0, h);
-  glu_finish<XT, kR>(B, xc, g, (b0 + (k + 1) * NB) * kR, lane, wave, S, red, 1, h);
-}
-
-// ======================================================================
-// Short-wave decode kernels (scheme 1): one workgroup per (expert, kR row
-// pairs) for gate/up; one workgroup per block of output rows (one wave per
-// expert) for down.  Selected with K3_DECODE_SCHEME=1.
-// ======================================================================
-template <typename XT, int kR>
-__global__ __launch_bounds__(256) void k_glu_short(const TokenRoute route, const Geo g,
-                                                   const XT* __restrict__ x,
-                                                   float* __restrict__ h) {
-  constexpr int N = 2 * kR;
-  constexpr int L = log2c<N>();
-  __shared__ float red[4][N];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int S = blockDim.x >> 6;
-  const int G = g.hidden >> 5;
-  const int upe = g.inter / kR;
-  const int e = blockIdx.x / upe;
-  const int r0 = (blockIdx.x - e * upe) * kR;
-  const ColSplit cs = col_split(G, S, wave, lane);
-  const uint8_t* span = route_span(route, e);
-  GluBatch<XT, kR> bt;
-  {
-    const size_t cp = (size_t)g.hidden >> 1;
-    const uint8_t* gp = span + g.w1p + (size_t)r0 * cp + (size_t)cs.cc * 16;
-    const uint8_t* up = span + g.w3p + (size_t)r0 * cp + (size_t)cs.cc * 16;
-    const uint8_t* gs = span + g.w1s + (size_t)r0 * G + cs.cc;
-    const uint8_t* us = span + g.w3s + (size_t)r0 * G + cs.cc;
+  // Unit pipelines: global pipeline index q = blockIdx.x * groups + grp takes
+  // units q, q + Q, q + 2Q, ... (Q = pipelines in the grid).  Every pipeline
+  // of the grid runs the same number of iterations (the host sizes the grid
+  // so), which keeps the workgroup-wide barrier below uniform.
+  const int Q = gridDim.x * groups;
+  const int iters = (n_units + Q - 1) / Q;
+  const int q0 = blockIdx.x * groups + grp;
+  // Unit of iteration `it` (a unit past the end repeats unit 0's loads and
+  // stores nothing, so every wave reaches every barrier).
+  auto unit_pair0 = [&](int it) {
+    const int u = q0 + it * Q;
+    return (u < n_units ? u : 0) * kR;
+  };
+  auto finish = [&](const GluBatch<XT, kR>& bt, int it) {
+    const int u = q0 + it * Q;
+    const int parity = it & 1;
+    float v[N];
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
-      bt.wg[r] = load_chunk(gp + (size_t)r * cp);
-      bt.wu[r] = load_chunk(up + (size_t)r * cp);
-      bt.sg[r] = load_scale(gs + (size_t)r * G);
-      bt.su[r] = load_scale(us + (size_t)r * G);
+      v[r] = xc.dot(bt.wg[r]) * e8m0_scale(bt.sg[r]);
+      v[kR + r] = xc.dot(bt.wu[r]) * e8m0_scale(bt.su[r]);
     }
-  }
-  XChunk<XT> xc;
-  load_x_chunk<XT>(xc, x, cs);
-  float v[N];
-#pragma unroll
-  for (int r = 0; r < kR; ++r) {
-    v[r] = xc.dot(bt.wg[r]) * e8m0_scale(bt.sg[r]);
-    v[kR + r] = xc.dot(bt.wu[r]) * e8m0_scale(bt.su[r]);
-  }
-  wave_reduce_multi<N>(v, lane);
-  if ((lane & ((1 << (6 - L)) - 1)) == 0) red[wave][lane >> (6 - L)] = v[0];
-  __syncthreads();
-  if ((int)threadIdx.x < kR) {
-    const int t = threadIdx.x;
-    float gv = red[0][t], uv = red[0][kR + t];
-    for (int w = 1; w < S; ++w) {
-      gv += red[w][t];
-      uv += red[w][kR + t];
+    wave_reduce_multi<N>(v, lane);
+    if ((lane & ((1 << (6 - L)) - 1)) == 0) red[parity][wave][lane >> (6 - L)] = v[0];
+    lds_barrier();
+    if (u < n_units && gw == 0 && lane < kR) {
+      const int w0 = grp * S;
+      float gv = red[parity][w0][lane], uv = red[parity][w0][kR + lane];
+      for (int w = 1; w < S; ++w) {
+        gv += red[parity][w0 + w][lane];
+        uv += red[parity][w0 + w][kR + lane];
+      }
+      h[(size_t)u * kR + lane] = activate(g.act, gv, uv);
     }
-    h[(size_t)e * g.inter + r0 + t] = activate(g.act, gv, uv);
+  };
+  // Two units in flight: unit it + 1 is requested before unit it is reduced.
+  GluBatch<XT, kR> A, B;
+  glu_load<XT, kR>(A, rr, g, unit_pair0(0), cs);
+  glu_load<XT, kR>(B, rr, g, unit_pair0(min(1, iters - 1)), cs);
+  for (int it = 0;; it += 2) {
+    finish(A, it);
+    if (it + 2 >= iters) {
+      if (it + 1 < iters) finish(B, it + 1);
+      break;
+    }
+    glu_load<XT, kR>(A, rr, g, unit_pair0(it + 2), cs);
+    finish(B, it + 1);
+    if (it + 3 >= iters) {
+      finish(A, it + 2);
+      break;
+    }
+    glu_load<XT, kR>(B, rr, g, unit_pair0(it + 3), cs);
   }
 }
 
 // ======================================================================
 // decode phase B: down rows of every routed expert + ordered combine
-// k_down_rows: every workgroup stages the routed experts' h (n x I fp32) in
-// LDS; wave j owns output rows [j kB, j kB + kB) (grid-stride over row
-// batches, so the grid sweeps each expert's down matrix as one window) and
-// walks the experts in route order: kB x CPL row loads per expert, two experts
-// in flight, one butterfly per expert, and the route-weighted sum
-// out = sum over e in route order of w_e * y_e (tools/metal/moe_mxfp4.metal:
-// 410-445 order) accumulated in registers.
 // ======================================================================
 template <int CPL, int kB>
 struct DownBatch {
@@ -494,18 +482,21 @@ __device__ __forceinline__ void down_load(DownBatch<CPL, kB>& bt, const uint8_t*
   }
 }
 
-template <int CPL, int kB>
-__device__ __forceinline__ float down_expert(const DownBatch<CPL, kB>& bt, const float* hl,
-                                             const Geo& g, const int* cc, const bool* valid,
-                                             int e, int lane) {
-  float v[kB];
-  XChunk<float> hs[CPL];
+template <int CPL>
+__device__ __forceinline__ void load_h_slice(XChunk<float>* hs, const float* he, const int* cc,
+                                             const bool* valid) {
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    hs[c].load(hl + (size_t)e * g.inter, cc[c]);
+    hs[c].load(he, cc[c]);
 #pragma unroll
     for (int i = 0; i < 32; ++i) hs[c].v[i] = valid[c] ? hs[c].v[i] : 0.0f;
   }
+}
+
+template <int CPL, int kB>
+__device__ __forceinline__ float down_dots(const DownBatch<CPL, kB>& bt, const XChunk<float>* hs,
+                                           int lane) {
+  float v[kB];
 #pragma unroll
   for (int u = 0; u < kB; ++u) {
     float a = hs[0].dot(bt.w[u][0]) * e8m0_scale(bt.s[u][0]);
@@ -517,84 +508,25 @@ __device__ __forceinline__ float down_expert(const DownBatch<CPL, kB>& bt, const
   return v[0];
 }
 
-template <typename OT, int CPL, int kB>
-__global__ __launch_bounds__(512) void k_down_rows(const TokenRoute route, const Geo g,
-                                                   const float* __restrict__ h,
-                                                   OT* __restrict__ out, int n_batches) {
-  extern __shared__ uint4 smem_h[];
-  float* hl = reinterpret_cast<float*>(smem_h);
-  constexpr int L = log2c<kB>();
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int nw = blockDim.x >> 6;
-  const int n = route.n;
-  const int GB = g.inter >> 5;
-  int cc[CPL];
-  bool valid[CPL];
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    valid[c] = lane + 64 * c < GB;
-    cc[c] = min(lane + 64 * c, GB - 1);
-  }
-  const RouteRegs rreg = route_regs(route, lane);
-  const int first = blockIdx.x * nw + wave;
-  const int stride = gridDim.x * nw;
-  // First expert's rows are requested before the h staging so HBM is busy
-  // while the workgroup copies h into LDS.
-  DownBatch<CPL, kB> A, B;
-  if (first < n_batches) {
-    const int r0 = first * kB;
-    const int nrows = min(kB, g.hidden - r0);
-    down_load<CPL, kB>(A, span_of(rreg, 0), g, cc, r0, nrows);
-    down_load<CPL, kB>(B, span_of(rreg, min(1, n - 1)), g, cc, r0, nrows);
-  }
-  {
-    // h copy into LDS, 8 loads in flight per thread per round.
-    const int n16 = n * g.inter / 4;
-    const uint4* src = reinterpret_cast<const uint4*>(h);
-    for (int i0 = threadIdx.x; i0 < n16; i0 += 8 * blockDim.x) {
-      uint4 t[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) t[k] = src[min(i0 + k * (int)blockDim.x, n16 - 1)];
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (i0 + k * (int)blockDim.x < n16) smem_h[i0 + k * blockDim.x] = t[k];
-    }
-  }
-  __syncthreads();
-  for (int jb = first; jb < n_batches; jb += stride) {
-    const int r0 = jb * kB;
-    const int nrows = min(kB, g.hidden - r0);
-    if (jb != first) {
-      down_load<CPL, kB>(A, span_of(rreg, 0), g, cc, r0, nrows);
-      down_load<CPL, kB>(B, span_of(rreg, min(1, n - 1)), g, cc, r0, nrows);
-    }
-    float acc = 0.0f;
-    int e = 0;
-    // Experts past the last (odd n) repeat the last expert's loads; their
-    // results are not accumulated.
-    for (; e + 2 < n; e += 2) {
-      acc += weight_of(rreg, e) * down_expert<CPL, kB>(A, hl, g, cc, valid, e, lane);
-      down_load<CPL, kB>(A, span_of(rreg, e + 2), g, cc, r0, nrows);
-      acc += weight_of(rreg, e + 1) * down_expert<CPL, kB>(B, hl, g, cc, valid, e + 1, lane);
-      down_load<CPL, kB>(B, span_of(rreg, min(e + 3, n - 1)), g, cc, r0, nrows);
-    }
-    acc += weight_of(rreg, e) * down_expert<CPL, kB>(A, hl, g, cc, valid, e, lane);
-    if (e + 1 < n) acc += weight_of(rreg, e + 1) * down_expert<CPL, kB>(B, hl, g, cc, valid, e + 1, lane);
-    const int idx = lane >> (6 - L);
-    if ((lane & ((1 << (6 - L)) - 1)) == 0 && idx < nrows) store_out(out + r0 + idx, acc);
-  }
+template <int CPL, int kB>
+__device__ __forceinline__ float down_expert(const DownBatch<CPL, kB>& bt, const float* hl,
+                                             const Geo& g, const int* cc, const bool* valid,
+                                             int e, int lane) {
+  XChunk<float> hs[CPL];
+  load_h_slice<CPL>(hs, hl + (size_t)e * g.inter, cc, valid);
+  return down_dots<CPL, kB>(bt, hs, lane);
 }
 
-// k_down_blocks: fallback when n x I fp32 does not fit in LDS.  A workgroup
-// owns rows_per_block output rows, wave w takes experts w, w + nw, ...  with
-// its h slice in registers, loads its rows kB at a time, and the ordered
-// weighted sum is formed from LDS.
+// k_down_blocks: a workgroup owns rows_per_block output rows (one block of
+// rows per CU); wave w takes routed experts w, w + nw, ... with its h slice in
+// registers, loads its rows kB at a time (one butterfly per batch), and the
+// route-ordered weighted sum out = sum over e in route order of w_e * y_e
+// (tools/metal/moe_mxfp4.metal:410-445 order) is formed out of LDS.
 constexpr int kDownMaxRows = 64;
 
 template <int CPLB>
 constexpr int down_max_threads() {
-  return CPLB <= 2 ? 1024 : 512;
+  return CPLB <= 1 ? 1024 : 512;
 }
 
 template <typename OT, int CPLB, int kB>
@@ -617,14 +549,39 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
     cc[c] = min(lane + 64 * c, GB - 1);
   }
   const RouteRegs rreg = route_regs(route, lane);
+  const int nb = (nrows + kB - 1) / kB;
+  const int idx = lane >> (6 - L);
+  const bool writer = (lane & ((1 << (6 - L)) - 1)) == 0;
   for (int e = wave; e < route.n; e += nw) {
     const uint8_t* span = span_of(rreg, e);
-    for (int rb = 0; rb < nrows; rb += kB) {
-      DownBatch<CPLB, kB> bt;
-      down_load<CPLB, kB>(bt, span, g, cc, row0 + rb, min(kB, nrows - rb));
-      const float v = down_expert<CPLB, kB>(bt, h, g, cc, valid, e, lane);
-      const int idx = lane >> (6 - L);
-      if ((lane & ((1 << (6 - L)) - 1)) == 0 && rb + idx < nrows) ybuf[e][rb + idx] = v;
+    // Two batches in flight: batch b + 1 is requested before batch b is
+    // reduced.  Loads are unconditional inside the loop (the loop exits
+    // instead), so the compiler's wait counts stay partial.
+    DownBatch<CPLB, kB> A, B;
+    down_load<CPLB, kB>(A, span, g, cc, row0, min(kB, nrows));
+    const int rb1 = min(1, nb - 1) * kB;
+    down_load<CPLB, kB>(B, span, g, cc, row0 + rb1, min(kB, nrows - rb1));
+    XChunk<float> hs[CPLB];
+    load_h_slice<CPLB>(hs, h + (size_t)e * g.inter, cc, valid);
+    for (int b = 0;; b += 2) {
+      const float va = down_dots<CPLB, kB>(A, hs, lane);
+      if (writer && b * kB + idx < nrows) ybuf[e][b * kB + idx] = va;
+      if (b + 2 >= nb) {
+        if (b + 1 < nb) {
+          const float vb = down_dots<CPLB, kB>(B, hs, lane);
+          if (writer && (b + 1) * kB + idx < nrows) ybuf[e][(b + 1) * kB + idx] = vb;
+        }
+        break;
+      }
+      down_load<CPLB, kB>(A, span, g, cc, row0 + (b + 2) * kB, min(kB, nrows - (b + 2) * kB));
+      const float vb = down_dots<CPLB, kB>(B, hs, lane);
+      if (writer && (b + 1) * kB + idx < nrows) ybuf[e][(b + 1) * kB + idx] = vb;
+      if (b + 3 >= nb) {
+        const float va2 = down_dots<CPLB, kB>(A, hs, lane);
+        if (writer && (b + 2) * kB + idx < nrows) ybuf[e][(b + 2) * kB + idx] = va2;
+        break;
+      }
+      down_load<CPLB, kB>(B, span, g, cc, row0 + (b + 3) * kB, min(kB, nrows - (b + 3) * kB));
     }
   }
   __syncthreads();
@@ -632,6 +589,91 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
     float acc = 0.0f;
     for (int e = 0; e < route.n; ++e) acc += weight_of(rreg, e) * ybuf[e][t];
     store_out(out + row0 + t, acc);
+  }
+}
+
+// k_down_stream: a unit is (row range rr, routed expert e), u = rr * n + e, so
+// the n experts of one row range run side by side; each wave normally owns one
+// unit and streams its R contiguous rows with two kB-row batches in flight,
+// holding h_e's slice in registers.  Row results go to y[e][row] with
+// device-scope stores (written through to the level every XCD reads).  After
+// its last store is acknowledged the wave bumps the row range's arrival
+// counter; the wave that brings it to n forms out[row] = sum over e in route
+// order of w_e * y[e][row] and returns the counter to zero.
+template <typename OT, int CPL, int kB>
+__global__ __launch_bounds__(256) void k_down_stream(const TokenRoute route, const Geo g,
+                                                     const float* __restrict__ h,
+                                                     float* __restrict__ y,
+                                                     int* __restrict__ cnt,
+                                                     OT* __restrict__ out, int R,
+                                                     int n_units) {
+  constexpr int L = log2c<kB>();
+  const int lane = threadIdx.x & 63;
+  const int gw = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+  const int W = (int)((gridDim.x * blockDim.x) >> 6);
+  const int GB = g.inter >> 5;
+  const int n = route.n;
+  int cc[CPL];
+  bool valid[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    valid[c] = lane + 64 * c < GB;
+    cc[c] = min(lane + 64 * c, GB - 1);
+  }
+  const RouteRegs rreg = route_regs(route, lane);
+  const int idx = lane >> (6 - L);
+  const bool writer = (lane & ((1 << (6 - L)) - 1)) == 0;
+  for (int u = gw; u < n_units; u += W) {
+    const int rr = u / n;
+    const int e = u - rr * n;
+    const int row0 = rr * R;
+    const int nrows = min(R, g.hidden - row0);
+    const int nb = (nrows + kB - 1) / kB;
+    const uint8_t* span = span_of(rreg, e);
+    float* ye = y + (size_t)e * g.hidden + row0;
+    auto put = [&](float v, int b) {
+      if (writer && b * kB + idx < nrows)
+        __hip_atomic_store(ye + b * kB + idx, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    DownBatch<CPL, kB> A, B;
+    down_load<CPL, kB>(A, span, g, cc, row0, min(kB, nrows));
+    const int rb1 = min(1, nb - 1) * kB;
+    down_load<CPL, kB>(B, span, g, cc, row0 + rb1, min(kB, nrows - rb1));
+    XChunk<float> hs[CPL];
+    load_h_slice<CPL>(hs, h + (size_t)e * g.inter, cc, valid);
+    for (int b = 0;; b += 2) {
+      put(down_dots<CPL, kB>(A, hs, lane), b);
+      if (b + 2 >= nb) {
+        if (b + 1 < nb) put(down_dots<CPL, kB>(B, hs, lane), b + 1);
+        break;
+      }
+      down_load<CPL, kB>(A, span, g, cc, row0 + (b + 2) * kB, min(kB, nrows - (b + 2) * kB));
+      put(down_dots<CPL, kB>(B, hs, lane), b + 1);
+      if (b + 3 >= nb) {
+        put(down_dots<CPL, kB>(A, hs, lane), b + 2);
+        break;
+      }
+      down_load<CPL, kB>(B, span, g, cc, row0 + (b + 3) * kB, min(kB, nrows - (b + 3) * kB));
+    }
+    // Arrival: this wave's y stores are acknowledged at device scope before
+    // the counter moves, so the wave that completes the range reads full rows.
+    wait_mem_complete();
+    int old = 0;
+    if (lane == 0)
+      old = __hip_atomic_fetch_add(cnt + rr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0, kWave);
+    if (old == n - 1) {
+      for (int t = lane; t < nrows; t += kWave) {
+        float acc = 0.0f;
+        for (int e2 = 0; e2 < n; ++e2) {
+          const float v = __hip_atomic_load(y + (size_t)e2 * g.hidden + row0 + t,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          acc += weight_of(rreg, e2) * v;
+        }
+        store_out(out + row0 + t, acc);
+      }
+      if (lane == 0) __hip_atomic_store(cnt + rr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -656,6 +698,13 @@ __global__ void k_activate(const float* __restrict__ gate, const float* __restri
 // ======================================================================
 constexpr int kRouteMaxBank = 4096;
 
+// Inverse of route_key's value half (NaN comes back as -inf, -0 as +0).
+__device__ __forceinline__ float key_value(uint64_t key) {
+  uint32_t u = (uint32_t)(key >> 32);
+  u = (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u;
+  return __uint_as_float(u);
+}
+
 __device__ __forceinline__ uint64_t route_key(float v, int i) {
   uint32_t u = __float_as_uint(v);
   if ((u & 0x7fffffffu) > 0x7f800000u) u = 0xff800000u;  // NaN -> -inf
@@ -664,65 +713,80 @@ __device__ __forceinline__ uint64_t route_key(float v, int i) {
   return ((uint64_t)u << 32) | (uint64_t)(~(uint32_t)i);
 }
 
+// Block-level top-k + softmax.  keys: nseg*64 + round_up(nseg*top_k, 2) uint64
+// of LDS scratch (16-byte aligned); sel/wsel receive the selected ids (rank
+// order) and weights.  All threads of the workgroup call it; it ends with a
+// barrier.  Comparisons read two keys per 128-bit LDS load.
+__device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
+                           uint64_t* keys, int* sel, float* wsel) {
+  const int nseg = (n_bank + 63) >> 6;
+  const int ncand = nseg * top_k;
+  const int ncand2 = (ncand + 1) & ~1;
+  uint64_t* cand = keys + (size_t)nseg * 64;
+  const int T = blockDim.x;
+  for (int i = threadIdx.x; i < nseg * 64; i += T)
+    keys[i] = i < n_bank ? route_key(src[i], i) : 0ull;  // 0 ranks below every real key
+  for (int i = threadIdx.x; i < ncand2; i += T) cand[i] = 0ull;
+  __syncthreads();
+  // stage 1: rank within the 64-key segment
+  for (int i = threadIdx.x; i < n_bank; i += T) {
+    const uint64_t k = keys[i];
+    const ulonglong2* seg = reinterpret_cast<const ulonglong2*>(keys + (i & ~63));
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const ulonglong2 q = seg[j];
+      rank += (q.x > k) + (q.y > k);
+    }
+    if (rank < top_k) cand[(i >> 6) * top_k + rank] = k;
+  }
+  __syncthreads();
+  // stage 2: rank among the candidates is the global rank
+  for (int t = threadIdx.x; t < ncand; t += T) {
+    const uint64_t k = cand[t];
+    if (k == 0ull) continue;
+    const ulonglong2* c2 = reinterpret_cast<const ulonglong2*>(cand);
+    int rank = 0;
+#pragma unroll 8
+    for (int j = 0; j < ncand2 / 2; ++j) {
+      const ulonglong2 q = c2[j];
+      rank += (q.x > k) + (q.y > k);
+    }
+    if (rank < top_k) sel[rank] = (int)(~(uint32_t)k);
+  }
+  __syncthreads();
+  // softmax over the selected logits: one wave, fixed summation order.  The
+  // logit is recovered from its key (no second global load).
+  if (threadIdx.x < 64) {
+    const int j = threadIdx.x;
+    float ex = 0.0f;
+    if (j < top_k) {
+      const float top = key_value(keys[sel[0]]);
+      const float lj = key_value(keys[sel[j]]);
+      ex = expf(lj - top);
+    }
+    const float sum = wave_sum(ex);
+    if (j < top_k) wsel[j] = ex / sum;
+  }
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits, int n_bank,
                                                 int top_k, int32_t* __restrict__ ids_ws,
                                                 float* __restrict__ w_ws,
                                                 int32_t* __restrict__ ids_user,
                                                 float* __restrict__ w_user) {
-  extern __shared__ uint64_t rsm[];  // keys [nseg * 64], then candidates [nseg * top_k]
+  extern __shared__ __attribute__((aligned(16))) uint64_t rsm[];
   __shared__ int sel[K3_HIP_MAX_TOKEN_EXPERTS];
-  __shared__ float ex[K3_HIP_MAX_TOKEN_EXPERTS];
+  __shared__ float wsel[K3_HIP_MAX_TOKEN_EXPERTS];
   const int p = blockIdx.x;
-  const float* src = logits + (size_t)p * n_bank;
-  const int nseg = (n_bank + 63) >> 6;
-  uint64_t* keys = rsm;
-  uint64_t* cand = rsm + (size_t)nseg * 64;
-  const int ncand = nseg * top_k;
-  for (int i = threadIdx.x; i < nseg * 64; i += blockDim.x)
-    keys[i] = i < n_bank ? route_key(src[i], i) : 0ull;  // 0 ranks below every real key
-  for (int i = threadIdx.x; i < ncand; i += blockDim.x) cand[i] = 0ull;
-  __syncthreads();
-  // stage 1
-  for (int i = threadIdx.x; i < nseg * 64; i += blockDim.x) {
-    const uint64_t k = keys[i];
-    const uint64_t* seg = keys + (i & ~63);
-    int rank = 0;
-#pragma unroll 16
-    for (int j = 0; j < 64; ++j) rank += seg[j] > k;
-    if (i < n_bank && rank < top_k) cand[(i >> 6) * top_k + rank] = k;
-  }
-  __syncthreads();
-  // stage 2
-  for (int t = threadIdx.x; t < ncand; t += blockDim.x) {
-    const uint64_t k = cand[t];
-    if (k == 0ull) continue;
-    int rank = 0;
-#pragma unroll 8
-    for (int j = 0; j < ncand; ++j) rank += cand[j] > k;
-    if (rank < top_k) sel[rank] = (int)(~(uint32_t)k);
-  }
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int j = threadIdx.x;
-    if (j < top_k) {
-      const float top = src[sel[0]];
-      float lj = src[sel[j]];
-      if (lj != lj) lj = -INFINITY;
-      ex[j] = expf(lj - top);
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float sum = 0.0f;
-    for (int j = 0; j < top_k; ++j) sum += ex[j];
-    for (int j = 0; j < top_k; ++j) {
-      const float w = ex[j] / sum;
-      const int o = p * top_k + j;
-      ids_ws[o] = sel[j];
-      w_ws[o] = w;
-      if (ids_user) ids_user[o] = sel[j];
-      if (w_user) w_user[o] = w;
-    }
+  block_topk(logits + (size_t)p * n_bank, n_bank, top_k, rsm, sel, wsel);
+  for (int j = threadIdx.x; j < top_k; j += blockDim.x) {
+    const int o = p * top_k + j;
+    ids_ws[o] = sel[j];
+    w_ws[o] = wsel[j];
+    if (ids_user) ids_user[o] = sel[j];
+    if (w_user) w_user[o] = wsel[j];
   }
 }
 
@@ -1033,25 +1097,25 @@ __global__ void k_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed, 
 namespace {
 
 constexpr int kRowsGemv = 8;
-// Rows per wave of the decode gate/up kernel (gate and up each).
-#ifndef K3_GLU_ROWS
-#define K3_GLU_ROWS 8
-#endif
+// Rows per unit of the decode gate/up kernel (gate and up each).
 constexpr int kRowsGlu = K3_GLU_ROWS;
-// Rows per expert load of the decode down kernel with a one-chunk h slice.
-#ifndef K3_DOWN_BATCH
-#define K3_DOWN_BATCH 4
+// Rows per load batch of the decode down kernel.
+#ifndef K3_DOWN_BLOCKS_BATCH
+#define K3_DOWN_BLOCKS_BATCH 4
 #endif
-constexpr int kDownBatch = K3_DOWN_BATCH;
-// Resident workgroups per CU the streaming decode kernels aim for (capped by
-// the kernel's occupancy): enough waves to keep ~64 KB of loads in flight per
-// CU without crowding the memory queues.
-// 2: streaming decode kernels (default); 1: short-wave kernels.
-#ifndef K3_DECODE_SCHEME
-#define K3_DECODE_SCHEME 2
+constexpr int kDownBlocksBatch = K3_DOWN_BLOCKS_BATCH;
+// Rows per batch and target waves per CU of the streaming down kernel.
+#ifndef K3_DOWN_STREAM_BATCH
+#define K3_DOWN_STREAM_BATCH 8
 #endif
-#ifndef K3_GLU_BPC
-#define K3_GLU_BPC 2
+constexpr int kDownStreamBatch = K3_DOWN_STREAM_BATCH;
+#ifndef K3_DOWN_WPC
+#define K3_DOWN_WPC 8
+#endif
+// 1: one workgroup per block of rows (one wave per expert, combine in LDS);
+// 2: streaming units with device-scope arrival counters.
+#ifndef K3_DOWN_SCHEME
+#define K3_DOWN_SCHEME 1
 #endif
 constexpr int kRowsVerifyA = 8;
 constexpr int kRowsVerifyB = 16;
@@ -1155,7 +1219,7 @@ int launch_route(const float* logits, int n_bank, int top_k, int n_positions, in
   if (n_positions <= 0) return fail(K3_HIP_E_INVALID, "router: no positions");
   const int nseg = (n_bank + 63) / 64;
   const int threads = std::min(1024, nseg * 64);
-  const size_t lds = (size_t)nseg * (64 + top_k) * sizeof(uint64_t);
+  const size_t lds = route_scratch_bytes(n_bank, top_k);
   TimedLaunch tl(KC_ROUTE, st);
   hipLaunchKernelGGL(k_route, dim3(n_positions), dim3(threads), (unsigned)lds, st, logits, n_bank,
                      top_k, ids_ws, w_ws, ids_user, w_user);
@@ -1171,78 +1235,16 @@ int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, floa
   const int S = (G + 63) / 64;
   if (S > 4) return fail(K3_HIP_E_INVALID, "decode layer: hidden %d exceeds 8192", g.hidden);
   if (g.inter % kRowsGlu != 0) return fail(K3_HIP_E_INVALID, "decode layer: bad intermediate");
-#if K3_DECODE_SCHEME == 1
-  {
-    TimedLaunch tl(KC_GLU_DECODE, st);
-    hipLaunchKernelGGL((k_glu_short<XT, kRowsGlu>), dim3(route.n * (g.inter / kRowsGlu)),
-                       dim3(64 * S), 0, st, route, g, x, h);
-    return launched("decode gate/up launch");
-  }
-#endif
-  const void* kern = reinterpret_cast<const void*>(&k_glu_stream<XT, kRowsGlu>);
-  const int occ = std::min(K3_GLU_BPC, occupancy_blocks_per_cu(kern, 64 * S, 0));
-  const int slots = std::max(1, device_cu_count() * occ);
-  // The grid must divide the batch count into an even number per workgroup:
-  // take the largest such grid that fits the resident slots.
-  const int nbt = route.n * g.inter / kRowsGlu;
-  int grid = 0;
-  for (int cand = std::min(slots, nbt / 2); cand >= 1; --cand) {
-    if (nbt % (2 * cand) == 0) {
-      grid = cand;
-      break;
-    }
-  }
-  if (grid == 0) return fail(K3_HIP_E_INVALID, "decode layer: batch count %d is odd", nbt);
-  TimedLaunch tl(KC_GLU_DECODE, st);
-  hipLaunchKernelGGL((k_glu_stream<XT, kRowsGlu>), dim3(grid), dim3(64 * S), 0, st, route, g, x,
-                     h, nbt / grid);
-  return launched("decode gate/up launch");
-}
-
-int max_dynamic_lds() {
-  static std::mutex mu;
-  static std::unordered_map<int, int> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 65536;
-  std::lock_guard<std::mutex> lk(mu);
-  auto it = cache.find(dev);
-  if (it != cache.end()) return it->second;
-  int v = 0;
-  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
-      v <= 0) {
-    (void)hipGetLastError();
-    v = 65536;
-  }
-  cache[dev] = v;
-  return v;
-}
-
-template <typename OT, int CPL, int kB>
-int down_rows_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
-                     hipStream_t st) {
-  const size_t lds = (size_t)route.n * g.inter * sizeof(float);
-  const void* kern = reinterpret_cast<const void*>(&k_down_rows<OT, CPL, kB>);
-  if (lds > 65536) {
-    static std::mutex mu;
-    static std::unordered_map<int, size_t> raised;  // per device
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    std::lock_guard<std::mutex> lk(mu);
-    if (raised[dev] < lds) {
-      const hipError_t e =
-          hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return hip_fail("decode down: LDS attribute", e);
-      raised[dev] = lds;
-    }
-  }
+  const size_t lds = route.logits ? route_scratch_bytes(route.n_bank, route.n) : 0;
+  const int n_units = route.n * (g.inter / kRowsGlu);
+  // One workgroup per CU holding up to 16 waves of unit pipelines.
+  const int groups = std::max(1, std::min(kGluMaxThreads / (64 * S), 16 / S));
   const int cus = std::max(1, device_cu_count());
-  const int n_batches = (g.hidden + kB - 1) / kB;
-  const int nw = std::max(1, std::min(8, (n_batches + cus - 1) / cus));
-  const int blocks = std::min(cus, (n_batches + nw - 1) / nw);
-  TimedLaunch tl(KC_DOWN_DECODE, st);
-  hipLaunchKernelGGL((k_down_rows<OT, CPL, kB>), dim3(blocks), dim3(64 * nw), (unsigned)lds, st,
-                     route, g, h, out, n_batches);
-  return launched("decode down/combine launch");
+  const int grid = std::max(1, std::min(cus, (n_units + groups - 1) / groups));
+  TimedLaunch tl(KC_GLU_DECODE, st);
+  hipLaunchKernelGGL((k_glu_decode<XT, kRowsGlu>), dim3(grid), dim3(64 * S * groups),
+                     (unsigned)lds, st, route, g, x, h, n_units, S);
+  return launched("decode gate/up launch");
 }
 
 template <typename OT, int CPL, int kB>
@@ -1260,27 +1262,55 @@ int down_blocks_launch(const Geo& g, const TokenRoute& route, const float* h, OT
   return launched("decode down/combine launch");
 }
 
+// Row ranges (multiples of kB rows) sized so that n x H rows split into about
+// K3_DOWN_WPC waves per CU, one unit each.
+template <typename OT, int CPL, int kB>
+int down_stream_launch(const Geo& g, const TokenRoute& route, const Workspace& ws, OT* out,
+                       hipStream_t st) {
+  const int cus = std::max(1, device_cu_count());
+  const int64_t rows_total = (int64_t)route.n * g.hidden;
+  const int64_t waves_target = (int64_t)cus * K3_DOWN_WPC;
+  int R = (int)((rows_total + waves_target - 1) / waves_target);
+  R = std::max(kB, (R + kB - 1) / kB * kB);
+  const int nrr = (g.hidden + R - 1) / R;
+  if (nrr > kWorkspaceCounters)
+    return fail(K3_HIP_E_INVALID, "decode layer: %d row ranges exceed the workspace counters", nrr);
+  const int units = nrr * route.n;
+  const int blocks = (units + 3) / 4;
+  TimedLaunch tl(KC_DOWN_DECODE, st);
+  hipLaunchKernelGGL((k_down_stream<OT, CPL, kB>), dim3(blocks), dim3(256), 0, st, route, g, ws.h,
+                     ws.y, ws.cnt, out, R, units);
+  return launched("decode down/combine launch");
+}
+
 template <typename OT>
 int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace& ws, OT* out,
                          hipStream_t st) {
   const int GB = g.inter / 32;
-  const int cpl = (GB + 63) / 64;
-  const size_t lds = (size_t)route.n * g.inter * sizeof(float);
-  const bool rows = K3_DECODE_SCHEME != 1 && lds <= (size_t)max_dynamic_lds();
-  switch (cpl) {
-    case 1:
-      return rows ? down_rows_launch<OT, 1, kDownBatch>(g, route, ws.h, out, st)
-                  : down_blocks_launch<OT, 1, 8>(g, route, ws.h, out, st);
-    case 2:
-      return rows ? down_rows_launch<OT, 2, 4>(g, route, ws.h, out, st)
-                  : down_blocks_launch<OT, 2, 4>(g, route, ws.h, out, st);
+#if K3_DOWN_SCHEME == 1
+  switch ((GB + 63) / 64) {
+    case 1: return down_blocks_launch<OT, 1, kDownBlocksBatch>(g, route, ws.h, out, st);
+    case 2: return down_blocks_launch<OT, 2, 2>(g, route, ws.h, out, st);
     case 3: return down_blocks_launch<OT, 3, 2>(g, route, ws.h, out, st);
-    case 4: return down_blocks_launch<OT, 4, 2>(g, route, ws.h, out, st);
+    case 4: return down_blocks_launch<OT, 4, 1>(g, route, ws.h, out, st);
+    default: return fail(K3_HIP_E_INVALID, "decode layer: intermediate %d exceeds 8192", g.inter);
+  }
+#endif
+  switch ((GB + 63) / 64) {
+    case 1: return down_stream_launch<OT, 1, kDownStreamBatch>(g, route, ws, out, st);
+    case 2: return down_stream_launch<OT, 2, 4>(g, route, ws, out, st);
+    case 3: return down_stream_launch<OT, 3, 2>(g, route, ws, out, st);
+    case 4: return down_stream_launch<OT, 4, 2>(g, route, ws, out, st);
     default: return fail(K3_HIP_E_INVALID, "decode layer: intermediate %d exceeds 8192", g.inter);
   }
 }
 
 }  // namespace
+
+size_t route_scratch_bytes(int n_bank, int top_k) {
+  const size_t nseg = (size_t)(n_bank + 63) / 64;
+  return (nseg * 64 + ((nseg * (size_t)top_k + 1) & ~(size_t)1)) * sizeof(uint64_t);
+}
 
 int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x, int x_dtype,
                         void* out, int out_dtype, const Workspace& ws, hipStream_t st) {
@@ -1291,9 +1321,16 @@ int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x, in
                ? glu_decode_dispatch<uint16_t>(g, route, static_cast<const uint16_t*>(x), ws.h, st)
                : glu_decode_dispatch<float>(g, route, static_cast<const float*>(x), ws.h, st);
   if (rc != K3_HIP_OK) return rc;
+  // The down kernel reads the route the gate/up kernel published.
+  TokenRoute down_route = route;
+  if (route.logits) {
+    down_route.logits = nullptr;
+    down_route.ids = ws.ids;
+    down_route.wdev = ws.w;
+  }
   return out_dtype == K3_DTYPE_BF16
-             ? down_decode_dispatch<uint16_t>(g, route, ws, static_cast<uint16_t*>(out), st)
-             : down_decode_dispatch<float>(g, route, ws, static_cast<float*>(out), st);
+             ? down_decode_dispatch<uint16_t>(g, down_route, ws, static_cast<uint16_t*>(out), st)
+             : down_decode_dispatch<float>(g, down_route, ws, static_cast<float*>(out), st);
 }
 
 int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride, int n_positions,
