@@ -136,18 +136,21 @@ enum KernelClass : int {
   KC_COUNT
 };
 
-// Brackets one kernel launch with two hipEvents on its stream while timing is
-// enabled; a no-op otherwise.
+// While timing is enabled, reserves a pair of hipEvents for one kernel launch:
+// the launch hands them to hipExtLaunchKernel, which stamps them with the
+// kernel's own start and end.  Both are null (an untimed launch) otherwise.
+// A launch that fails calls failed() so its unstamped pair is not read.
 class TimedLaunch {
  public:
   TimedLaunch(int kernel_class, hipStream_t stream);
-  ~TimedLaunch();
   TimedLaunch(const TimedLaunch&) = delete;
   TimedLaunch& operator=(const TimedLaunch&) = delete;
+  hipEvent_t start() const;
+  hipEvent_t stop() const;
+  void failed();
 
  private:
   int slot_;
-  hipStream_t stream_;
 };
 
 }  // namespace k3

@@ -24,6 +24,8 @@
 #include <mutex>
 #include <unordered_map>
 
+#include <hip/hip_ext.h>
+
 #include "k3_device.h"
 #include "k3_internal.h"
 
@@ -517,29 +519,35 @@ __device__ __forceinline__ float down_expert(const DownBatch<CPL, kB>& bt, const
   return down_dots<CPL, kB>(bt, hs, lane);
 }
 
-// k_down_blocks: a workgroup owns rows_per_block output rows (one block of
-// rows per CU); wave w takes routed experts w, w + nw, ... with its h slice in
-// registers, loads its rows kB at a time (one butterfly per batch), and the
-// route-ordered weighted sum out = sum over e in route order of w_e * y_e
-// (tools/metal/moe_mxfp4.metal:410-445 order) is formed out of LDS.
+// k_down_blocks: the output rows are cut into batches of kB rows, and
+// workgroup b owns batches b, b + G, b + 2G, ... (G workgroups, one per CU), so
+// at any moment the grid reads one contiguous stretch of every routed expert's
+// down matrix (DRAM rows are opened once and read whole) while each workgroup
+// still owns its output rows outright.  Wave w takes routed experts w, w + nw,
+// ... with its h slice in registers and two batches in flight (one butterfly
+// per batch); the route-ordered weighted sum out = sum over e in route order of
+// w_e * y_e (tools/metal/moe_mxfp4.metal:410-445 order) is formed out of LDS.
 constexpr int kDownMaxRows = 64;
 
+#ifndef K3_DOWN_THREADS
+#define K3_DOWN_THREADS 1024
+#endif
 template <int CPLB>
 constexpr int down_max_threads() {
-  return CPLB <= 1 ? 1024 : 512;
+  return CPLB <= 1 ? K3_DOWN_THREADS : 512;
 }
 
 template <typename OT, int CPLB, int kB>
 __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
-    const TokenRoute route, const Geo g, const float* __restrict__ h, OT* __restrict__ out,
-    int rows_per_block) {
+    const TokenRoute route, const Geo g, const float* __restrict__ h, OT* __restrict__ out) {
   constexpr int L = log2c<kB>();
   __shared__ float ybuf[K3_HIP_MAX_TOKEN_EXPERTS][kDownMaxRows];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  const int row0 = blockIdx.x * rows_per_block;
-  const int nrows = min(rows_per_block, g.hidden - row0);
+  const int G = gridDim.x;
+  const int nbt = (g.hidden + kB - 1) / kB;       // batches in the whole output
+  const int nb = (nbt - (int)blockIdx.x + G - 1) / G;  // this workgroup's batches
   const int GB = g.inter >> 5;
   int cc[CPLB];
   bool valid[CPLB];
@@ -548,8 +556,10 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
     valid[c] = lane + 64 * c < GB;
     cc[c] = min(lane + 64 * c, GB - 1);
   }
+  // First output row of this workgroup's local batch i, and its row count.
+  auto row_of = [&](int i) { return (i * G + (int)blockIdx.x) * kB; };
+  auto rows_in = [&](int i) { return min(kB, g.hidden - row_of(i)); };
   const RouteRegs rreg = route_regs(route, lane);
-  const int nb = (nrows + kB - 1) / kB;
   const int idx = lane >> (6 - L);
   const bool writer = (lane & ((1 << (6 - L)) - 1)) == 0;
   for (int e = wave; e < route.n; e += nw) {
@@ -558,37 +568,39 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
     // reduced.  Loads are unconditional inside the loop (the loop exits
     // instead), so the compiler's wait counts stay partial.
     DownBatch<CPLB, kB> A, B;
-    down_load<CPLB, kB>(A, span, g, cc, row0, min(kB, nrows));
-    const int rb1 = min(1, nb - 1) * kB;
-    down_load<CPLB, kB>(B, span, g, cc, row0 + rb1, min(kB, nrows - rb1));
+    down_load<CPLB, kB>(A, span, g, cc, row_of(0), rows_in(0));
+    const int b1 = min(1, nb - 1);
+    down_load<CPLB, kB>(B, span, g, cc, row_of(b1), rows_in(b1));
     XChunk<float> hs[CPLB];
     load_h_slice<CPLB>(hs, h + (size_t)e * g.inter, cc, valid);
     for (int b = 0;; b += 2) {
       const float va = down_dots<CPLB, kB>(A, hs, lane);
-      if (writer && b * kB + idx < nrows) ybuf[e][b * kB + idx] = va;
+      if (writer && idx < rows_in(b)) ybuf[e][b * kB + idx] = va;
       if (b + 2 >= nb) {
         if (b + 1 < nb) {
           const float vb = down_dots<CPLB, kB>(B, hs, lane);
-          if (writer && (b + 1) * kB + idx < nrows) ybuf[e][(b + 1) * kB + idx] = vb;
+          if (writer && idx < rows_in(b + 1)) ybuf[e][(b + 1) * kB + idx] = vb;
         }
         break;
       }
-      down_load<CPLB, kB>(A, span, g, cc, row0 + (b + 2) * kB, min(kB, nrows - (b + 2) * kB));
+      down_load<CPLB, kB>(A, span, g, cc, row_of(b + 2), rows_in(b + 2));
       const float vb = down_dots<CPLB, kB>(B, hs, lane);
-      if (writer && (b + 1) * kB + idx < nrows) ybuf[e][(b + 1) * kB + idx] = vb;
+      if (writer && idx < rows_in(b + 1)) ybuf[e][(b + 1) * kB + idx] = vb;
       if (b + 3 >= nb) {
         const float va2 = down_dots<CPLB, kB>(A, hs, lane);
-        if (writer && (b + 2) * kB + idx < nrows) ybuf[e][(b + 2) * kB + idx] = va2;
+        if (writer && idx < rows_in(b + 2)) ybuf[e][(b + 2) * kB + idx] = va2;
         break;
       }
-      down_load<CPLB, kB>(B, span, g, cc, row0 + (b + 3) * kB, min(kB, nrows - (b + 3) * kB));
+      down_load<CPLB, kB>(B, span, g, cc, row_of(b + 3), rows_in(b + 3));
     }
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < nrows; t += blockDim.x) {
+  for (int t = threadIdx.x; t < nb * kB; t += blockDim.x) {
+    const int row = row_of(t / kB) + (t % kB);
+    if (row >= g.hidden) continue;
     float acc = 0.0f;
     for (int e = 0; e < route.n; ++e) acc += weight_of(rreg, e) * ybuf[e][t];
-    store_out(out + row0 + t, acc);
+    store_out(out + row, acc);
   }
 }
 
@@ -1122,9 +1134,19 @@ constexpr int kRowsVerifyB = 16;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-int launched(const char* what) {
+// Every launch goes through hipExtLaunchKernel so that an open timing window
+// gets the dispatch's own start/end stamps (null events: an ordinary launch).
+template <typename F, typename... Args>
+void launch_timed(const TimedLaunch& tl, F kernel, const dim3& grid, const dim3& block,
+                  uint32_t lds, hipStream_t st, Args... args) {
+  hipExtLaunchKernelGGL(kernel, grid, block, lds, st, tl.start(), tl.stop(), 0u, args...);
+}
+
+int launched(TimedLaunch& tl, const char* what) {
   const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? K3_HIP_OK : hip_fail(what, e);
+  if (e == hipSuccess) return K3_HIP_OK;
+  tl.failed();
+  return hip_fail(what, e);
 }
 
 template <typename XT, typename OT>
@@ -1137,13 +1159,13 @@ int gemv1_dispatch(const uint8_t* p, const uint8_t* s, const XT* x, OT* y, int r
   if (cpl > 4) return -1;  // caller falls back to the LDS kernel
   TimedLaunch tl(KC_GEMV, st);
   switch (cpl) {
-    case 1: hipLaunchKernelGGL((k_gemv1<XT, OT, 1, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
-    case 2: hipLaunchKernelGGL((k_gemv1<XT, OT, 2, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
-    case 3: hipLaunchKernelGGL((k_gemv1<XT, OT, 3, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
-    case 4: hipLaunchKernelGGL((k_gemv1<XT, OT, 4, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
+    case 1: launch_timed(tl, (k_gemv1<XT, OT, 1, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
+    case 2: launch_timed(tl, (k_gemv1<XT, OT, 2, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
+    case 3: launch_timed(tl, (k_gemv1<XT, OT, 3, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
+    case 4: launch_timed(tl, (k_gemv1<XT, OT, 4, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
     default: return -1;  // caller falls back to the LDS kernel
   }
-  return launched("mxfp4 GEMV launch");
+  return launched(tl, "mxfp4 GEMV launch");
 }
 
 template <typename XT, typename OT>
@@ -1156,9 +1178,9 @@ int gemv_multi_dispatch(const uint8_t* p, const uint8_t* s, const XT* x, OT* y, 
   group = std::min(group, batches);
   const int waves = (rows + kRowsGemv - 1) / kRowsGemv;
   TimedLaunch tl(KC_GEMV, st);
-  hipLaunchKernelGGL((k_gemv_multi<XT, OT, kRowsGemv>), dim3((waves + 3) / 4), dim3(256),
+  launch_timed(tl, (k_gemv_multi<XT, OT, kRowsGemv>), dim3((waves + 3) / 4), dim3(256),
                      (unsigned)(group * per), st, p, s, x, y, rows, cols, batches, group);
-  return launched("mxfp4 GEMV (multi) launch");
+  return launched(tl, "mxfp4 GEMV (multi) launch");
 }
 
 template <typename XT, typename OT>
@@ -1204,8 +1226,8 @@ int launch_activation(const float* gate, const float* up, float* h, int64_t n, i
   const int64_t blocks = (n + 255) / 256;
   if (blocks > INT32_MAX) return fail(K3_HIP_E_INVALID, "activation grid too large");
   TimedLaunch tl(KC_ACTIVATE, st);
-  hipLaunchKernelGGL(k_activate, dim3((unsigned)blocks), dim3(256), 0, st, gate, up, h, n, act);
-  return launched("activation launch");
+  launch_timed(tl, k_activate, dim3((unsigned)blocks), dim3(256), 0, st, gate, up, h, n, act);
+  return launched(tl, "activation launch");
 }
 
 int launch_route(const float* logits, int n_bank, int top_k, int n_positions, int32_t* ids_ws,
@@ -1221,9 +1243,9 @@ int launch_route(const float* logits, int n_bank, int top_k, int n_positions, in
   const int threads = std::min(1024, nseg * 64);
   const size_t lds = route_scratch_bytes(n_bank, top_k);
   TimedLaunch tl(KC_ROUTE, st);
-  hipLaunchKernelGGL(k_route, dim3(n_positions), dim3(threads), (unsigned)lds, st, logits, n_bank,
+  launch_timed(tl, k_route, dim3(n_positions), dim3(threads), (unsigned)lds, st, logits, n_bank,
                      top_k, ids_ws, w_ws, ids_user, w_user);
-  return launched("router launch");
+  return launched(tl, "router launch");
 }
 
 namespace {
@@ -1242,24 +1264,28 @@ int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, floa
   const int cus = std::max(1, device_cu_count());
   const int grid = std::max(1, std::min(cus, (n_units + groups - 1) / groups));
   TimedLaunch tl(KC_GLU_DECODE, st);
-  hipLaunchKernelGGL((k_glu_decode<XT, kRowsGlu>), dim3(grid), dim3(64 * S * groups),
+  launch_timed(tl, (k_glu_decode<XT, kRowsGlu>), dim3(grid), dim3(64 * S * groups),
                      (unsigned)lds, st, route, g, x, h, n_units, S);
-  return launched("decode gate/up launch");
+  return launched(tl, "decode gate/up launch");
 }
 
 template <typename OT, int CPL, int kB>
 int down_blocks_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
                        hipStream_t st) {
+  // One workgroup per CU, more when a workgroup's batches would overflow its
+  // LDS row buffer.
+  const int nbt = (g.hidden + kB - 1) / kB;
   const int cus = std::max(1, device_cu_count());
-  int rpb = (g.hidden + cus - 1) / cus;
-  rpb = std::min(std::max(rpb, 1), kDownMaxRows);
-  const int blocks = (g.hidden + rpb - 1) / rpb;
+  const int per = std::max(1, std::min((nbt + cus - 1) / cus, kDownMaxRows / kB));
+  const int blocks = (nbt + per - 1) / per;
+  if ((nbt + blocks - 1) / blocks * kB > kDownMaxRows)
+    return fail(K3_HIP_E_INVALID, "decode layer: hidden %d too large for the down kernel", g.hidden);
   const int max_waves = down_max_threads<CPL>() / 64;
   const int nw = std::min(route.n, max_waves);
   TimedLaunch tl(KC_DOWN_DECODE, st);
-  hipLaunchKernelGGL((k_down_blocks<OT, CPL, kB>), dim3(blocks), dim3(64 * nw), 0, st, route, g,
-                     h, out, rpb);
-  return launched("decode down/combine launch");
+  launch_timed(tl, (k_down_blocks<OT, CPL, kB>), dim3(blocks), dim3(64 * nw), 0, st, route, g, h,
+               out);
+  return launched(tl, "decode down/combine launch");
 }
 
 // Row ranges (multiples of kB rows) sized so that n x H rows split into about
@@ -1278,9 +1304,9 @@ int down_stream_launch(const Geo& g, const TokenRoute& route, const Workspace& w
   const int units = nrr * route.n;
   const int blocks = (units + 3) / 4;
   TimedLaunch tl(KC_DOWN_DECODE, st);
-  hipLaunchKernelGGL((k_down_stream<OT, CPL, kB>), dim3(blocks), dim3(256), 0, st, route, g, ws.h,
+  launch_timed(tl, (k_down_stream<OT, CPL, kB>), dim3(blocks), dim3(256), 0, st, route, g, ws.h,
                      ws.y, ws.cnt, out, R, units);
-  return launched("decode down/combine launch");
+  return launched(tl, "decode down/combine launch");
 }
 
 template <typename OT>
@@ -1337,15 +1363,15 @@ int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride, 
                             int top_k, const Workspace& ws, hipStream_t st) {
   (void)g;
   TimedLaunch tl(KC_VERIFY_PLAN, st);
-  hipLaunchKernelGGL(k_verify_plan_bank, dim3(1), dim3(256), 0, st, bank, stride, n_positions,
+  launch_timed(tl, k_verify_plan_bank, dim3(1), dim3(256), 0, st, bank, stride, n_positions,
                      top_k, ws);
-  return launched("verify plan launch");
+  return launched(tl, "verify plan launch");
 }
 
 int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws, hipStream_t st) {
   TimedLaunch tl(KC_VERIFY_PLAN, st);
-  hipLaunchKernelGGL(k_verify_plan_table, dim3(1), dim3(256), 0, st, table, ws);
-  return launched("verify plan launch");
+  launch_timed(tl, k_verify_plan_table, dim3(1), dim3(256), 0, st, table, ws);
+  return launched(tl, "verify plan launch");
 }
 
 namespace {
@@ -1358,9 +1384,9 @@ int glu_verify_dispatch(const Geo& g, int n_edges, const XT* x, const Workspace&
   if (lds > 96 * 1024) return fail(K3_HIP_E_INVALID, "verify: hidden %d too wide", g.hidden);
   const int upe = g.inter / (4 * kRowsVerifyA);
   TimedLaunch tl(KC_GLU_VERIFY, st);
-  hipLaunchKernelGGL((k_glu_verify<XT, kRowsVerifyA>), dim3(upe * n_edges), dim3(256),
+  launch_timed(tl, (k_glu_verify<XT, kRowsVerifyA>), dim3(upe * n_edges), dim3(256),
                      (unsigned)lds, st, g, x, ws);
-  return launched("verify gate/up launch");
+  return launched(tl, "verify gate/up launch");
 }
 
 int down_verify_dispatch(const Geo& g, int n_edges, const Workspace& ws, hipStream_t st) {
@@ -1371,13 +1397,13 @@ int down_verify_dispatch(const Geo& g, int n_edges, const Workspace& ws, hipStre
   if (cplb > 4) return fail(K3_HIP_E_INVALID, "verify: intermediate %d exceeds 8192", g.inter);
   TimedLaunch tl(KC_DOWN_VERIFY, st);
   switch (cplb) {
-    case 1: hipLaunchKernelGGL((k_down_verify<1, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
-    case 2: hipLaunchKernelGGL((k_down_verify<2, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
-    case 3: hipLaunchKernelGGL((k_down_verify<3, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
-    case 4: hipLaunchKernelGGL((k_down_verify<4, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
+    case 1: launch_timed(tl, (k_down_verify<1, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
+    case 2: launch_timed(tl, (k_down_verify<2, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
+    case 3: launch_timed(tl, (k_down_verify<3, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
+    case 4: launch_timed(tl, (k_down_verify<4, kRowsVerifyB>), grid, block, 0, st, g, ws); break;
     default: return fail(K3_HIP_E_INVALID, "verify: intermediate %d exceeds 8192", g.inter);
   }
-  return launched("verify down launch");
+  return launched(tl, "verify down launch");
 }
 
 }  // namespace
@@ -1396,12 +1422,12 @@ int launch_verify_layer(const Geo& g, int n_edges, int n_positions, const void* 
   const dim3 grid((unsigned)((n + 255) / 256)), block(256);
   TimedLaunch tl(KC_COMBINE, st);
   if (out_dtype == K3_DTYPE_BF16)
-    hipLaunchKernelGGL(k_combine_positions<uint16_t>, grid, block, 0, st, ws, g.hidden,
+    launch_timed(tl, k_combine_positions<uint16_t>, grid, block, 0, st, ws, g.hidden,
                        n_positions, static_cast<uint16_t*>(out));
   else
-    hipLaunchKernelGGL(k_combine_positions<float>, grid, block, 0, st, ws, g.hidden, n_positions,
+    launch_timed(tl, k_combine_positions<float>, grid, block, 0, st, ws, g.hidden, n_positions,
                        static_cast<float*>(out));
-  return launched("verify combine launch");
+  return launched(tl, "verify combine launch");
 }
 
 int launch_synth_bank(const Geo& g, uint8_t* bank, uint64_t stride, int n_experts,
@@ -1410,9 +1436,9 @@ int launch_synth_bank(const Geo& g, uint8_t* bank, uint64_t stride, int n_expert
       ((uintptr_t)bank & 7u) != 0 || lo < 0 || hi > 255 || lo > hi)
     return fail(K3_HIP_E_INVALID, "synth bank: invalid arguments");
   TimedLaunch tl(KC_SYNTH, st);
-  hipLaunchKernelGGL(k_synth_bank, dim3(1024, n_experts), dim3(256), 0, st, g, bank, stride,
+  launch_timed(tl, k_synth_bank, dim3(1024, n_experts), dim3(256), 0, st, g, bank, stride,
                      first_expert, seed, lo, hi);
-  return launched("synth bank launch");
+  return launched(tl, "synth bank launch");
 }
 
 int launch_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed, uint64_t stream_id,
@@ -1422,9 +1448,9 @@ int launch_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed, uint64_
   if (n == 0) return K3_HIP_OK;
   const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 4096);
   TimedLaunch tl(KC_SYNTH, st);
-  hipLaunchKernelGGL(k_synth_normal, dim3((unsigned)blocks), dim3(256), 0, st, out, dtype, n, seed,
+  launch_timed(tl, k_synth_normal, dim3((unsigned)blocks), dim3(256), 0, st, out, dtype, n, seed,
                      stream_id);
-  return launched("synth normal launch");
+  return launched(tl, "synth normal launch");
 }
 
 }  // namespace k3
