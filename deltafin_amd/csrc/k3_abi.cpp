@@ -80,7 +80,6 @@ uint64_t workspace_bytes(const Geo& g, int max_edges, int max_positions) {
   b += align256(E * 4);             // epos
   b += align256((P + 1) * 4);       // poff
   b += align256(sizeof(VerifyPlanDev));
-  b += align256((uint64_t)kWorkspaceCounters * 4);  // cnt
   return b;
 }
 
@@ -107,7 +106,6 @@ bool carve_workspace(void* base, uint64_t bytes, const Geo& g, int max_edges, in
   ws->epos = reinterpret_cast<int32_t*>(take(E * 4));
   ws->poff = reinterpret_cast<int32_t*>(take((P + 1) * 4));
   ws->plan = reinterpret_cast<VerifyPlanDev*>(take(sizeof(VerifyPlanDev)));
-  ws->cnt = reinterpret_cast<int32_t*>(take((uint64_t)kWorkspaceCounters * 4));
   return true;
 }
 
@@ -127,9 +125,9 @@ int device_cu_count() {
   return cus;
 }
 
-int occupancy_blocks_per_cu(const void* kernel, int block, size_t dynamic_lds) {
+bool lds_fits(const void* kernel, int block, size_t dynamic_lds) {
   static std::mutex mu;
-  static std::unordered_map<std::string, int> cache;
+  static std::unordered_map<std::string, bool> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   char key[96];
@@ -137,14 +135,18 @@ int occupancy_blocks_per_cu(const void* kernel, int block, size_t dynamic_lds) {
   std::lock_guard<std::mutex> lk(mu);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, dynamic_lds) != hipSuccess ||
-      n <= 0) {
+  // Raise the kernel's dynamic-LDS ceiling (a no-op where the runtime needs no
+  // opt-in), then ask whether one workgroup of this shape fits on a CU.
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dynamic_lds) !=
+      hipSuccess)
     (void)hipGetLastError();
-    n = 1;
-  }
-  cache[key] = n;
-  return n;
+  int n = 0;
+  const bool ok =
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, dynamic_lds) == hipSuccess &&
+      n >= 1;
+  if (!ok) (void)hipGetLastError();
+  cache[key] = ok;
+  return ok;
 }
 
 namespace {

@@ -238,6 +238,7 @@ __device__ __forceinline__ float activate(int act, float g, float u) {
 // every LDS wait drain the in-flight weight loads.
 typedef __attribute__((address_space(1))) const u32x4 gu32x4;
 typedef __attribute__((address_space(1))) const uint8_t gu8;
+typedef __attribute__((address_space(1))) const uint32_t gu32;
 
 __device__ __forceinline__ u32x4 load_chunk(const uint8_t* p) {
   return __builtin_nontemporal_load((gu32x4*)(p));
@@ -245,6 +246,10 @@ __device__ __forceinline__ u32x4 load_chunk(const uint8_t* p) {
 
 __device__ __forceinline__ uint32_t load_scale(const uint8_t* p) {
   return *(gu8*)(p);
+}
+
+__device__ __forceinline__ uint32_t load_u32(const uint8_t* p) {  // p 4-byte aligned
+  return *(gu32*)(p);
 }
 
 template <typename T>

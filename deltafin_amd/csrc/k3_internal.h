@@ -60,7 +60,7 @@ struct EdgeTable {
 struct Workspace {
   uint8_t* base;
   uint64_t bytes;
-  float* h;             // [max_edges][I] activations
+  float* h;             // [max_edges][I] activations (decode: lane-major per expert)
   float* y;             // [max_edges][H] per-edge expert outputs (verify)
   int32_t* ids;         // [max_edges] route ids
   float* w;             // [max_edges] route weights
@@ -70,12 +70,7 @@ struct Workspace {
   int32_t* epos;        // [max_edges] edge -> position
   int32_t* poff;        // [max_positions + 1]
   VerifyPlanDev* plan;  // 1
-  int32_t* cnt;         // [kWorkspaceCounters] arrival counters, zero between calls
 };
-
-// Arrival counters in every workspace (one per output row range of the
-// decode down kernel).  Each call returns them to zero.
-constexpr int kWorkspaceCounters = 4096;
 
 uint64_t workspace_bytes(const Geo& g, int max_edges, int max_positions);
 bool carve_workspace(void* base, uint64_t bytes, const Geo& g, int max_edges,
@@ -117,9 +112,10 @@ int launch_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed,
                         uint64_t stream_id, hipStream_t stream);
 
 int device_cu_count();
-// Resident workgroups per CU for `kernel` at `block` threads (cached per
-// kernel and device; 1 when the runtime cannot say).
-int occupancy_blocks_per_cu(const void* kernel, int block, size_t dynamic_lds);
+// Whether one workgroup of `kernel` at `block` threads with `dynamic_lds`
+// bytes of dynamic LDS fits on a CU of the current device, after raising the
+// kernel's dynamic-LDS ceiling (cached per kernel, shape and device).
+bool lds_fits(const void* kernel, int block, size_t dynamic_lds);
 
 // Kernel classes for the optional per-launch timing (k3_hip_timing_begin/end).
 enum KernelClass : int {

@@ -143,15 +143,6 @@ __device__ __forceinline__ float weight_of(const RouteRegs& rr, int e) {
   return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rr.w), e));
 }
 
-// Wait until every memory operation this wave issued has completed (stores
-// acknowledged by the level their scope names).  The signal fences keep the
-// compiler from moving memory operations across the wait.
-__device__ __forceinline__ void wait_mem_complete() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt unconstrained
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 // ======================================================================
 // single-activation GEMV: one wave per kRows rows, x slice in registers
 // ======================================================================
@@ -460,30 +451,45 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
 // ======================================================================
 // decode phase B: down rows of every routed expert + ordered combine
 // ======================================================================
-template <int CPL, int kB>
+// kG (gathered scales): with 64 scale groups per row (one chunk per lane) the
+// kB = 4 rows of a batch have their scale bytes in one contiguous 256 B run,
+// so lane l loads its dword l of the run and each lane's byte of row u
+// (byte 64 u + l, held by lane 16 u + l / 4) is routed to it by a
+// ds_bpermute: one load instead of kB single-byte loads.
+template <int CPL, int kB, bool kG = false>
 struct DownBatch {
+  static_assert(!kG || (CPL == 1 && kB == 4), "gathered scales need CPL 1, kB 4");
   u32x4 w[kB][CPL];
-  uint32_t s[kB][CPL];
+  uint32_t s[kG ? 1 : kB][CPL];
 };
 
-template <int CPL, int kB>
-__device__ __forceinline__ void down_load(DownBatch<CPL, kB>& bt, const uint8_t* span,
+template <int CPL, int kB, bool kG>
+__device__ __forceinline__ void down_load(DownBatch<CPL, kB, kG>& bt, const uint8_t* span,
                                           const Geo& g, const int* cc, int r0, int nrows) {
   const int GB = g.inter >> 5;
   const size_t cpb = (size_t)g.inter >> 1;
   const uint8_t* dp = span + g.w2p;
   const uint8_t* ds = span + g.w2s;
+  if constexpr (kG) {
+    // GB == 64 and cc[0] == lane.  Rows past nrows are not in the matrix:
+    // their lanes re-read the last dword present (those rows' results are
+    // discarded).  Issued first, so waiting for it never waits for the data.
+    const int d = min(cc[0], nrows * 16 - 1);
+    bt.s[0][0] = load_u32(ds + (size_t)r0 * 64 + 4 * d);
+  }
 #pragma unroll
   for (int u = 0; u < kB; ++u) {
     const int r = r0 + min(u, nrows - 1);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       bt.w[u][c] = load_chunk(dp + (size_t)r * cpb + (size_t)cc[c] * 16);
-      bt.s[u][c] = load_scale(ds + (size_t)r * GB + cc[c]);
+      if constexpr (!kG) bt.s[u][c] = load_scale(ds + (size_t)r * GB + cc[c]);
     }
   }
 }
 
+// h_e's chunks cc[c] for this lane straight from memory (zero where the lane
+// has no chunk).  Each of the 8 float4 loads touches 64 lines 128 B apart.
 template <int CPL>
 __device__ __forceinline__ void load_h_slice(XChunk<float>* hs, const float* he, const int* cc,
                                              const bool* valid) {
@@ -495,28 +501,59 @@ __device__ __forceinline__ void load_h_slice(XChunk<float>* hs, const float* he,
   }
 }
 
-template <int CPL, int kB>
-__device__ __forceinline__ float down_dots(const DownBatch<CPL, kB>& bt, const XChunk<float>* hs,
-                                           int lane) {
+// The same for one chunk per lane (64 chunks per row, chunk = lane), through
+// the wave's LDS region: 8 coalesced 1 KB loads of h_e, stored so that lane
+// l's chunk (float4s 8 l .. 8 l + 7) sits at float4 9 l .. 9 l + 7 (one float4
+// of padding per chunk puts the 16 lanes of a ds_read_b128 pass on distinct
+// banks); every access is a base register plus an immediate offset.  A wave's
+// LDS operations complete in order, so no barrier is needed.
+constexpr int kHSliceF4 = 9 * 64;  // float4s of LDS per wave
+
+// Issue the 8 coalesced loads (float4 64 q + lane of h_e into t[q]) ...
+__device__ __forceinline__ void h_slice_issue(float4 (&t)[8], const float* he, int lane) {
+  const float4* src = reinterpret_cast<const float4*>(he) + lane;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) t[q] = src[64 * q];
+}
+
+// ... and, once the weight loads behind them are issued too, route them
+// through LDS: float4 64 q + lane belongs to chunk 8 q + lane / 8 at position
+// lane % 8.
+__device__ __forceinline__ void h_slice_transpose(XChunk<float>& hs, const float4 (&t)[8],
+                                                  float4* hw, int lane) {
+  float4* dst = hw + 9 * (lane >> 3) + (lane & 7);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) dst[72 * q] = t[q];
+  const float4* mine = hw + 9 * lane;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float4 v = mine[q];
+    hs.v[4 * q + 0] = v.x;
+    hs.v[4 * q + 1] = v.y;
+    hs.v[4 * q + 2] = v.z;
+    hs.v[4 * q + 3] = v.w;
+  }
+}
+
+template <int CPL, int kB, bool kG>
+__device__ __forceinline__ float down_dots(const DownBatch<CPL, kB, kG>& bt,
+                                           const XChunk<float>* hs, int lane) {
   float v[kB];
 #pragma unroll
   for (int u = 0; u < kB; ++u) {
-    float a = hs[0].dot(bt.w[u][0]) * e8m0_scale(bt.s[u][0]);
+    if constexpr (kG) {
+      const uint32_t word =
+          (uint32_t)__builtin_amdgcn_ds_bpermute((16 * u + (lane >> 2)) << 2, (int)bt.s[0][0]);
+      v[u] = hs[0].dot(bt.w[u][0]) * e8m0_scale((word >> (8 * (lane & 3))) & 0xffu);
+    } else {
+      float a = hs[0].dot(bt.w[u][0]) * e8m0_scale(bt.s[u][0]);
 #pragma unroll
-    for (int c = 1; c < CPL; ++c) a += hs[c].dot(bt.w[u][c]) * e8m0_scale(bt.s[u][c]);
-    v[u] = a;
+      for (int c = 1; c < CPL; ++c) a += hs[c].dot(bt.w[u][c]) * e8m0_scale(bt.s[u][c]);
+      v[u] = a;
+    }
   }
   wave_reduce_multi<kB>(v, lane);
   return v[0];
-}
-
-template <int CPL, int kB>
-__device__ __forceinline__ float down_expert(const DownBatch<CPL, kB>& bt, const float* hl,
-                                             const Geo& g, const int* cc, const bool* valid,
-                                             int e, int lane) {
-  XChunk<float> hs[CPL];
-  load_h_slice<CPL>(hs, hl + (size_t)e * g.inter, cc, valid);
-  return down_dots<CPL, kB>(bt, hs, lane);
 }
 
 // k_down_blocks: the output rows are cut into batches of kB rows, and
@@ -567,31 +604,31 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
     // Two batches in flight: batch b + 1 is requested before batch b is
     // reduced.  Loads are unconditional inside the loop (the loop exits
     // instead), so the compiler's wait counts stay partial.
-    DownBatch<CPLB, kB> A, B;
-    down_load<CPLB, kB>(A, span, g, cc, row_of(0), rows_in(0));
-    const int b1 = min(1, nb - 1);
-    down_load<CPLB, kB>(B, span, g, cc, row_of(b1), rows_in(b1));
     XChunk<float> hs[CPLB];
     load_h_slice<CPLB>(hs, h + (size_t)e * g.inter, cc, valid);
+    DownBatch<CPLB, kB> A, B;
+    down_load(A, span, g, cc, row_of(0), rows_in(0));
+    const int b1 = min(1, nb - 1);
+    down_load(B, span, g, cc, row_of(b1), rows_in(b1));
     for (int b = 0;; b += 2) {
-      const float va = down_dots<CPLB, kB>(A, hs, lane);
+      const float va = down_dots(A, hs, lane);
       if (writer && idx < rows_in(b)) ybuf[e][b * kB + idx] = va;
       if (b + 2 >= nb) {
         if (b + 1 < nb) {
-          const float vb = down_dots<CPLB, kB>(B, hs, lane);
+          const float vb = down_dots(B, hs, lane);
           if (writer && idx < rows_in(b + 1)) ybuf[e][(b + 1) * kB + idx] = vb;
         }
         break;
       }
-      down_load<CPLB, kB>(A, span, g, cc, row_of(b + 2), rows_in(b + 2));
-      const float vb = down_dots<CPLB, kB>(B, hs, lane);
+      down_load(A, span, g, cc, row_of(b + 2), rows_in(b + 2));
+      const float vb = down_dots(B, hs, lane);
       if (writer && idx < rows_in(b + 1)) ybuf[e][(b + 1) * kB + idx] = vb;
       if (b + 3 >= nb) {
-        const float va2 = down_dots<CPLB, kB>(A, hs, lane);
+        const float va2 = down_dots(A, hs, lane);
         if (writer && idx < rows_in(b + 2)) ybuf[e][(b + 2) * kB + idx] = va2;
         break;
       }
-      down_load<CPLB, kB>(B, span, g, cc, row_of(b + 3), rows_in(b + 3));
+      down_load(B, span, g, cc, row_of(b + 3), rows_in(b + 3));
     }
   }
   __syncthreads();
@@ -604,88 +641,61 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
   }
 }
 
-// k_down_stream: a unit is (row range rr, routed expert e), u = rr * n + e, so
-// the n experts of one row range run side by side; each wave normally owns one
-// unit and streams its R contiguous rows with two kB-row batches in flight,
-// holding h_e's slice in registers.  Row results go to y[e][row] with
-// device-scope stores (written through to the level every XCD reads).  After
-// its last store is acknowledged the wave bumps the row range's arrival
-// counter; the wave that brings it to n forms out[row] = sum over e in route
-// order of w_e * y[e][row] and returns the counter to zero.
-template <typename OT, int CPL, int kB>
-__global__ __launch_bounds__(256) void k_down_stream(const TokenRoute route, const Geo g,
-                                                     const float* __restrict__ h,
-                                                     float* __restrict__ y,
-                                                     int* __restrict__ cnt,
-                                                     OT* __restrict__ out, int R,
-                                                     int n_units) {
-  constexpr int L = log2c<kB>();
+// k_down_g64: the same split for intermediate 2048 (64 scale groups per row:
+// one chunk per lane, batches of 4 rows with gathered scales, h_e's slice
+// transposed through LDS).  Every workgroup runs exactly NB batch slots (a
+// slot past its share re-reads its last batch and stores nothing), fully
+// unrolled, so the double-buffer schedule is straight-line code: while batch
+// b is reduced batch b + 1 is in flight, and batch b + 2 is requested right
+// after b's registers are free.
+constexpr int kDownG64MaxNB = 8;
+
+template <typename OT, int NB>
+__global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route, const Geo g,
+                                                   const float* __restrict__ h,
+                                                   OT* __restrict__ out) {
+  constexpr int kB = 4;
+  __shared__ float ybuf[K3_HIP_MAX_TOKEN_EXPERTS][NB * kB];
+  extern __shared__ float4 hbuf[];  // kHSliceF4 float4 per wave
   const int lane = threadIdx.x & 63;
-  const int gw = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-  const int W = (int)((gridDim.x * blockDim.x) >> 6);
-  const int GB = g.inter >> 5;
-  const int n = route.n;
-  int cc[CPL];
-  bool valid[CPL];
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    valid[c] = lane + 64 * c < GB;
-    cc[c] = min(lane + 64 * c, GB - 1);
-  }
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  const int G = gridDim.x;
+  const int nbt = (g.hidden + kB - 1) / kB;
+  const int nb = (nbt - (int)blockIdx.x + G - 1) / G;  // 1 <= nb <= NB (host)
+  const int cc[1] = {lane};
+  auto row_of = [&](int i) { return (min(i, nb - 1) * G + (int)blockIdx.x) * kB; };
+  auto rows_in = [&](int i) { return min(kB, g.hidden - row_of(i)); };
   const RouteRegs rreg = route_regs(route, lane);
-  const int idx = lane >> (6 - L);
-  const bool writer = (lane & ((1 << (6 - L)) - 1)) == 0;
-  for (int u = gw; u < n_units; u += W) {
-    const int rr = u / n;
-    const int e = u - rr * n;
-    const int row0 = rr * R;
-    const int nrows = min(R, g.hidden - row0);
-    const int nb = (nrows + kB - 1) / kB;
+  const int idx = lane >> 4;
+  const bool writer = (lane & 15) == 0;
+  for (int e = wave; e < route.n; e += nw) {
     const uint8_t* span = span_of(rreg, e);
-    float* ye = y + (size_t)e * g.hidden + row0;
-    auto put = [&](float v, int b) {
-      if (writer && b * kB + idx < nrows)
-        __hip_atomic_store(ye + b * kB + idx, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-    DownBatch<CPL, kB> A, B;
-    down_load<CPL, kB>(A, span, g, cc, row0, min(kB, nrows));
-    const int rb1 = min(1, nb - 1) * kB;
-    down_load<CPL, kB>(B, span, g, cc, row0 + rb1, min(kB, nrows - rb1));
-    XChunk<float> hs[CPL];
-    load_h_slice<CPL>(hs, h + (size_t)e * g.inter, cc, valid);
-    for (int b = 0;; b += 2) {
-      put(down_dots<CPL, kB>(A, hs, lane), b);
-      if (b + 2 >= nb) {
-        if (b + 1 < nb) put(down_dots<CPL, kB>(B, hs, lane), b + 1);
-        break;
-      }
-      down_load<CPL, kB>(A, span, g, cc, row0 + (b + 2) * kB, min(kB, nrows - (b + 2) * kB));
-      put(down_dots<CPL, kB>(B, hs, lane), b + 1);
-      if (b + 3 >= nb) {
-        put(down_dots<CPL, kB>(A, hs, lane), b + 2);
-        break;
-      }
-      down_load<CPL, kB>(B, span, g, cc, row0 + (b + 3) * kB, min(kB, nrows - (b + 3) * kB));
+    // Issue h_e's loads, then batches 0 and 1, before the LDS transpose
+    // waits for h_e (scheduling barriers keep the order).
+    float4 ht[8];
+    h_slice_issue(ht, h + (size_t)e * g.inter, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    DownBatch<1, kB, true> bt[2];
+    down_load(bt[0], span, g, cc, row_of(0), rows_in(0));
+    if constexpr (NB > 1) down_load(bt[1], span, g, cc, row_of(1), rows_in(1));
+    __builtin_amdgcn_sched_barrier(0);
+    XChunk<float> hs;
+    h_slice_transpose(hs, ht, hbuf + wave * kHSliceF4, lane);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float v = down_dots(bt[b & 1], &hs, lane);
+      if (b + 2 < NB) down_load(bt[b & 1], span, g, cc, row_of(b + 2), rows_in(b + 2));
+      if (writer && b < nb && idx < rows_in(b)) ybuf[e][b * kB + idx] = v;
     }
-    // Arrival: this wave's y stores are acknowledged at device scope before
-    // the counter moves, so the wave that completes the range reads full rows.
-    wait_mem_complete();
-    int old = 0;
-    if (lane == 0)
-      old = __hip_atomic_fetch_add(cnt + rr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0, kWave);
-    if (old == n - 1) {
-      for (int t = lane; t < nrows; t += kWave) {
-        float acc = 0.0f;
-        for (int e2 = 0; e2 < n; ++e2) {
-          const float v = __hip_atomic_load(y + (size_t)e2 * g.hidden + row0 + t,
-                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          acc += weight_of(rreg, e2) * v;
-        }
-        store_out(out + row0 + t, acc);
-      }
-      if (lane == 0) __hip_atomic_store(cnt + rr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < nb * kB; t += blockDim.x) {
+    const int row = row_of(t / kB) + (t % kB);
+    if (row >= g.hidden) continue;
+    float acc = 0.0f;
+    for (int e = 0; e < route.n; ++e) acc += weight_of(rreg, e) * ybuf[e][t];
+    store_out(out + row, acc);
   }
 }
 
@@ -1116,19 +1126,6 @@ constexpr int kRowsGlu = K3_GLU_ROWS;
 #define K3_DOWN_BLOCKS_BATCH 4
 #endif
 constexpr int kDownBlocksBatch = K3_DOWN_BLOCKS_BATCH;
-// Rows per batch and target waves per CU of the streaming down kernel.
-#ifndef K3_DOWN_STREAM_BATCH
-#define K3_DOWN_STREAM_BATCH 8
-#endif
-constexpr int kDownStreamBatch = K3_DOWN_STREAM_BATCH;
-#ifndef K3_DOWN_WPC
-#define K3_DOWN_WPC 8
-#endif
-// 1: one workgroup per block of rows (one wave per expert, combine in LDS);
-// 2: streaming units with device-scope arrival counters.
-#ifndef K3_DOWN_SCHEME
-#define K3_DOWN_SCHEME 1
-#endif
 constexpr int kRowsVerifyA = 8;
 constexpr int kRowsVerifyB = 16;
 
@@ -1288,45 +1285,50 @@ int down_blocks_launch(const Geo& g, const TokenRoute& route, const float* h, OT
   return launched(tl, "decode down/combine launch");
 }
 
-// Row ranges (multiples of kB rows) sized so that n x H rows split into about
-// K3_DOWN_WPC waves per CU, one unit each.
-template <typename OT, int CPL, int kB>
-int down_stream_launch(const Geo& g, const TokenRoute& route, const Workspace& ws, OT* out,
-                       hipStream_t st) {
-  const int cus = std::max(1, device_cu_count());
-  const int64_t rows_total = (int64_t)route.n * g.hidden;
-  const int64_t waves_target = (int64_t)cus * K3_DOWN_WPC;
-  int R = (int)((rows_total + waves_target - 1) / waves_target);
-  R = std::max(kB, (R + kB - 1) / kB * kB);
-  const int nrr = (g.hidden + R - 1) / R;
-  if (nrr > kWorkspaceCounters)
-    return fail(K3_HIP_E_INVALID, "decode layer: %d row ranges exceed the workspace counters", nrr);
-  const int units = nrr * route.n;
-  const int blocks = (units + 3) / 4;
+template <typename OT, int NB>
+int down_g64_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out, int blocks,
+                    hipStream_t st) {
+  const int nw = std::min(route.n, 16);
+  const unsigned lds = (unsigned)(nw * kHSliceF4 * sizeof(float4));
+  if (!lds_fits((const void*)k_down_g64<OT, NB>, 64 * nw, lds))
+    return fail(K3_HIP_E_EXEC, "decode layer: %u B of LDS per workgroup not available", lds);
   TimedLaunch tl(KC_DOWN_DECODE, st);
-  launch_timed(tl, (k_down_stream<OT, CPL, kB>), dim3(blocks), dim3(256), 0, st, route, g, ws.h,
-                     ws.y, ws.cnt, out, R, units);
+  launch_timed(tl, (k_down_g64<OT, NB>), dim3(blocks), dim3(64 * nw), lds, st, route, g, h, out);
   return launched(tl, "decode down/combine launch");
+}
+
+// Workgroups for k_down_g64: one per CU, more when a workgroup would own more
+// than kDownG64MaxNB batches; every workgroup owns at least one batch.
+template <typename OT>
+int down_g64_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
+                      hipStream_t st) {
+  const int nbt = (g.hidden + 3) / 4;
+  const int cus = std::max(1, device_cu_count());
+  const int blocks = std::min(nbt, std::max(cus, (nbt + kDownG64MaxNB - 1) / kDownG64MaxNB));
+  const int nb = (nbt + blocks - 1) / blocks;
+  switch (nb) {
+    case 1: return down_g64_launch<OT, 1>(g, route, h, out, blocks, st);
+    case 2: return down_g64_launch<OT, 2>(g, route, h, out, blocks, st);
+    case 3: return down_g64_launch<OT, 3>(g, route, h, out, blocks, st);
+    case 4: return down_g64_launch<OT, 4>(g, route, h, out, blocks, st);
+    case 5: return down_g64_launch<OT, 5>(g, route, h, out, blocks, st);
+    case 6: return down_g64_launch<OT, 6>(g, route, h, out, blocks, st);
+    case 7: return down_g64_launch<OT, 7>(g, route, h, out, blocks, st);
+    case 8: return down_g64_launch<OT, 8>(g, route, h, out, blocks, st);
+    default: return fail(K3_HIP_E_INVALID, "decode layer: %d down batches per workgroup", nb);
+  }
 }
 
 template <typename OT>
 int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace& ws, OT* out,
                          hipStream_t st) {
   const int GB = g.inter / 32;
-#if K3_DOWN_SCHEME == 1
+  if (GB == 64) return down_g64_dispatch<OT>(g, route, ws.h, out, st);
   switch ((GB + 63) / 64) {
     case 1: return down_blocks_launch<OT, 1, kDownBlocksBatch>(g, route, ws.h, out, st);
     case 2: return down_blocks_launch<OT, 2, 2>(g, route, ws.h, out, st);
     case 3: return down_blocks_launch<OT, 3, 2>(g, route, ws.h, out, st);
     case 4: return down_blocks_launch<OT, 4, 1>(g, route, ws.h, out, st);
-    default: return fail(K3_HIP_E_INVALID, "decode layer: intermediate %d exceeds 8192", g.inter);
-  }
-#endif
-  switch ((GB + 63) / 64) {
-    case 1: return down_stream_launch<OT, 1, kDownStreamBatch>(g, route, ws, out, st);
-    case 2: return down_stream_launch<OT, 2, 4>(g, route, ws, out, st);
-    case 3: return down_stream_launch<OT, 3, 2>(g, route, ws, out, st);
-    case 4: return down_stream_launch<OT, 4, 2>(g, route, ws, out, st);
     default: return fail(K3_HIP_E_INVALID, "decode layer: intermediate %d exceeds 8192", g.inter);
   }
 }
