@@ -307,15 +307,41 @@ __device__ __forceinline__ void lds_barrier() {
 // meet in LDS (two slots by unit parity, one barrier per unit); kR lanes of
 // wave 0 sum them in wave order, apply the activation and store h.
 // ======================================================================
-template <typename XT, int kR>
+// kG (gathered scales): a wave's cw = ceil(G / S) groups of a row are cw
+// contiguous scale bytes, so with cw % 4 == 0 and kR * cw <= 256 the kR rows
+// of one matrix in a unit are kR * cw / 4 dwords: lane l loads dword l of
+// them (one load per matrix instead of kR single-byte loads), and the byte of
+// row r for lane l (group c0 + l) is routed to it by a ds_bpermute from lane
+// r * cw / 4 + l / 4.
+template <typename XT, int kR, bool kG = false>
 struct GluBatch {
   u32x4 wg[kR], wu[kR];
-  uint32_t sg[kR], su[kR];
+  uint32_t sg[kG ? 1 : kR], su[kG ? 1 : kR];
 };
 
-template <typename XT, int kR>
-__device__ __forceinline__ void glu_load(GluBatch<XT, kR>& bt, const RouteRegs& rr,
-                                         const Geo& g, int pair0, const ColSplit& cs) {
+// Per-lane constants of the gathered-scale loads: byte offset (from the
+// unit's first row) of the dword this lane loads, and the ds_bpermute address
+// of row 0's source lane (row r adds r * cw).
+struct GluGather {
+  int off;
+  int bp;
+};
+
+__device__ __forceinline__ GluGather glu_gather(int G, int S, int wave, int lane, int kR) {
+  const int cw = (G + S - 1) / S;
+  const int nd = cw >> 2;
+  const int u = min(lane / nd, kR - 1);
+  const int d = lane < kR * nd ? lane % nd : nd - 1;
+  GluGather r;
+  r.off = u * G + min(wave * cw + 4 * d, G - 4);
+  r.bp = (lane >> 2) << 2;
+  return r;
+}
+
+template <typename XT, int kR, bool kG>
+__device__ __forceinline__ void glu_load(GluBatch<XT, kR, kG>& bt, const RouteRegs& rr,
+                                         const Geo& g, int pair0, const ColSplit& cs,
+                                         const GluGather& gg) {
   const int e = pair0 / g.inter;
   const int r0 = pair0 - e * g.inter;
   const int G = g.hidden >> 5;
@@ -323,15 +349,28 @@ __device__ __forceinline__ void glu_load(GluBatch<XT, kR>& bt, const RouteRegs& 
   const uint8_t* span = span_of(rr, e);
   const uint8_t* gp = span + g.w1p + (size_t)r0 * cp + (size_t)cs.cc * 16;
   const uint8_t* up = span + g.w3p + (size_t)r0 * cp + (size_t)cs.cc * 16;
+  if constexpr (kG) {  // scale dwords first: waiting for them never waits for the data
+    bt.sg[0] = load_u32(span + g.w1s + (size_t)r0 * G + gg.off);
+    bt.su[0] = load_u32(span + g.w3s + (size_t)r0 * G + gg.off);
+  }
   const uint8_t* gs = span + g.w1s + (size_t)r0 * G + cs.cc;
   const uint8_t* us = span + g.w3s + (size_t)r0 * G + cs.cc;
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
     bt.wg[r] = load_chunk(gp + (size_t)r * cp);
     bt.wu[r] = load_chunk(up + (size_t)r * cp);
-    bt.sg[r] = load_scale(gs + (size_t)r * G);
-    bt.su[r] = load_scale(us + (size_t)r * G);
+    if constexpr (!kG) {
+      bt.sg[r] = load_scale(gs + (size_t)r * G);
+      bt.su[r] = load_scale(us + (size_t)r * G);
+    }
   }
+}
+
+// Scale byte of row r for this lane from a gathered dword.
+__device__ __forceinline__ uint32_t gathered_scale(uint32_t word, int bp, int row_step, int r,
+                                                   int lane) {
+  const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(bp + r * row_step, (int)word);
+  return (w >> (8 * (lane & 3))) & 0xffu;
 }
 
 __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
@@ -348,7 +387,7 @@ __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
 #endif
 constexpr int kGluMaxThreads = 256 * K3_GLU_GROUPS;
 
-template <typename XT, int kR>
+template <typename XT, int kR, bool kG>
 __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute route, const Geo g,
                                                      const XT* __restrict__ x,
                                                      float* __restrict__ h, int n_units,
@@ -367,6 +406,8 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
   const int grp = wave / S;
   const int gw = wave - grp * S;  // wave within its group
   const ColSplit cs = col_split(g.hidden >> 5, S, gw, lane);
+  const GluGather gg = glu_gather(g.hidden >> 5, S, gw, lane, kR);
+  const int row_step = ((g.hidden >> 5) + S - 1) / S;  // cw: bpermute bytes per row
   XChunk<XT> xc;
   load_x_chunk<XT>(xc, x, cs);
   RouteRegs rr;
@@ -406,14 +447,20 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
     const int u = q0 + it * Q;
     return (u < n_units ? u : 0) * kR;
   };
-  auto finish = [&](const GluBatch<XT, kR>& bt, int it) {
+  auto finish = [&](const GluBatch<XT, kR, kG>& bt, int it) {
     const int u = q0 + it * Q;
     const int parity = it & 1;
     float v[N];
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
-      v[r] = xc.dot(bt.wg[r]) * e8m0_scale(bt.sg[r]);
-      v[kR + r] = xc.dot(bt.wu[r]) * e8m0_scale(bt.su[r]);
+      if constexpr (kG) {
+        v[r] = xc.dot(bt.wg[r]) * e8m0_scale(gathered_scale(bt.sg[0], gg.bp, row_step, r, lane));
+        v[kR + r] =
+            xc.dot(bt.wu[r]) * e8m0_scale(gathered_scale(bt.su[0], gg.bp, row_step, r, lane));
+      } else {
+        v[r] = xc.dot(bt.wg[r]) * e8m0_scale(bt.sg[r]);
+        v[kR + r] = xc.dot(bt.wu[r]) * e8m0_scale(bt.su[r]);
+      }
     }
     wave_reduce_multi<N>(v, lane);
     if ((lane & ((1 << (6 - L)) - 1)) == 0) red[parity][wave][lane >> (6 - L)] = v[0];
@@ -429,22 +476,22 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
     }
   };
   // Two units in flight: unit it + 1 is requested before unit it is reduced.
-  GluBatch<XT, kR> A, B;
-  glu_load<XT, kR>(A, rr, g, unit_pair0(0), cs);
-  glu_load<XT, kR>(B, rr, g, unit_pair0(min(1, iters - 1)), cs);
+  GluBatch<XT, kR, kG> A, B;
+  glu_load(A, rr, g, unit_pair0(0), cs, gg);
+  glu_load(B, rr, g, unit_pair0(min(1, iters - 1)), cs, gg);
   for (int it = 0;; it += 2) {
     finish(A, it);
     if (it + 2 >= iters) {
       if (it + 1 < iters) finish(B, it + 1);
       break;
     }
-    glu_load<XT, kR>(A, rr, g, unit_pair0(it + 2), cs);
+    glu_load(A, rr, g, unit_pair0(it + 2), cs, gg);
     finish(B, it + 1);
     if (it + 3 >= iters) {
       finish(A, it + 2);
       break;
     }
-    glu_load<XT, kR>(B, rr, g, unit_pair0(it + 3), cs);
+    glu_load(B, rr, g, unit_pair0(it + 3), cs, gg);
   }
 }
 
@@ -580,7 +627,7 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
   constexpr int L = log2c<kB>();
   __shared__ float ybuf[K3_HIP_MAX_TOKEN_EXPERTS][kDownMaxRows];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPR
   const int nw = blockDim.x >> 6;
   const int G = gridDim.x;
   const int nbt = (g.hidden + kB - 1) / kB;       // batches in the whole output
@@ -658,7 +705,7 @@ __global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route, const
   __shared__ float ybuf[K3_HIP_MAX_TOKEN_EXPERTS][NB * kB];
   extern __shared__ float4 hbuf[];  // kHSliceF4 float4 per wave
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPR
   const int nw = blockDim.x >> 6;
   const int G = gridDim.x;
   const int nbt = (g.hidden + kB - 1) / kB;
@@ -915,7 +962,7 @@ __global__ __launch_bounds__(256) void k_glu_verify(const Geo g, const XT* __res
   XT* xs = reinterpret_cast<XT*>(smem_va);
   constexpr int kG = VerifyA<XT>::kGroup;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPR
   const int upe = g.inter / (4 * kRows);
   const int u = blockIdx.x / upe;
   if (u >= ws.plan->n_unique) return;
@@ -982,7 +1029,7 @@ template <int CPLB, int kRows>
 __global__ __launch_bounds__(256) void k_down_verify(const Geo g, const Workspace ws) {
   constexpr int kE = (4 / CPLB) > 0 ? (4 / CPLB) : 1;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPR
   const int upe = (g.hidden + 4 * kRows - 1) / (4 * kRows);
   const int u = blockIdx.x / upe;
   if (u >= ws.plan->n_unique) return;
@@ -1260,9 +1307,15 @@ int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, floa
   const int groups = std::max(1, std::min(kGluMaxThreads / (64 * S), 16 / S));
   const int cus = std::max(1, device_cu_count());
   const int grid = std::max(1, std::min(cus, (n_units + groups - 1) / groups));
+  const int cw = (G + S - 1) / S;
+  const bool gather = kRowsGlu == 4 && G % 4 == 0 && cw % 4 == 0 && kRowsGlu * cw <= 256;
   TimedLaunch tl(KC_GLU_DECODE, st);
-  launch_timed(tl, (k_glu_decode<XT, kRowsGlu>), dim3(grid), dim3(64 * S * groups),
-                     (unsigned)lds, st, route, g, x, h, n_units, S);
+  if (gather)
+    launch_timed(tl, (k_glu_decode<XT, kRowsGlu, true>), dim3(grid), dim3(64 * S * groups),
+                 (unsigned)lds, st, route, g, x, h, n_units, S);
+  else
+    launch_timed(tl, (k_glu_decode<XT, kRowsGlu, false>), dim3(grid), dim3(64 * S * groups),
+                 (unsigned)lds, st, route, g, x, h, n_units, S);
   return launched(tl, "decode gate/up launch");
 }
 
