@@ -467,7 +467,7 @@ int positions_locked(Context& c, const uint8_t* const* blobs, int n_edges, const
   carve_workspace(c.ws, c.ws_bytes, c.geo, K3_HIP_MAX_EDGES, K3_HIP_MAX_POSITIONS, &ws);
   int rc = launch_verify_plan_table(tbl, ws, c.stream);
   if (rc == K3_HIP_OK)
-    rc = launch_verify_layer(c.geo, n_edges, n_pos, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws,
+    rc = launch_verify_layer(c.geo, n_edges, n_pos, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws, false,
                              c.stream);
   if (rc == K3_HIP_OK &&
       (e = hipMemcpyAsync(c.hout, c.dout, bytes, hipMemcpyDeviceToHost, c.stream)) != hipSuccess)
@@ -821,7 +821,7 @@ int k3_hip_moe_verify_route_device(const K3HipGeometryV1* gd, const uint8_t* ban
                         route_weights, st);
   if (rc == K3_HIP_OK) rc = launch_verify_plan_bank(g, bank, expert_stride, n_positions, top_k, ws, st);
   if (rc == K3_HIP_OK)
-    rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
+    rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, true, st);
   return rc;
 }
 
@@ -870,7 +870,7 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
   }
   int rc = launch_verify_plan_table(tbl, ws, st);
   if (rc == K3_HIP_OK)
-    rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
+    rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, false, st);
   return rc;
 }
 

@@ -89,6 +89,34 @@ __device__ __forceinline__ float chunk_dot_f32(u32x4 w, const float* xv) {
 }
 
 // Decode a chunk once into fp32 pairs (for reuse across several activations).
+// One chunk against two fp32 activation chunks: each code pair is decoded
+// once and feeds both sums (nothing decoded is held beyond its two FMAs).
+__device__ __forceinline__ void chunk_dot_f32_x2(u32x4 w, const float* xa, const float* xb,
+                                                 float& ra, float& rb) {
+  float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#define K3_DOT2_PAIR(d, sel, base)                                              \
+  {                                                                            \
+    const v2f q = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, (sel));  \
+    a0 = fmaf(q.x, xa[(base) + 0], a0);                                         \
+    a1 = fmaf(q.y, xa[(base) + 1], a1);                                         \
+    b0 = fmaf(q.x, xb[(base) + 0], b0);                                         \
+    b1 = fmaf(q.y, xb[(base) + 1], b1);                                         \
+  }
+#define K3_DOT2_DWORD(d, base) \
+  K3_DOT2_PAIR(d, 0, (base) + 0) \
+  K3_DOT2_PAIR(d, 1, (base) + 2) \
+  K3_DOT2_PAIR(d, 2, (base) + 4) \
+  K3_DOT2_PAIR(d, 3, (base) + 6)
+  K3_DOT2_DWORD(w.x, 0)
+  K3_DOT2_DWORD(w.y, 8)
+  K3_DOT2_DWORD(w.z, 16)
+  K3_DOT2_DWORD(w.w, 24)
+#undef K3_DOT2_DWORD
+#undef K3_DOT2_PAIR
+  ra = a0 + a1;
+  rb = b0 + b1;
+}
+
 __device__ __forceinline__ void chunk_decode_f32(u32x4 w, v2f* out16) {
 #define K3_DEC_DWORD(d, base)                                                  \
   out16[(base) + 0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((d), 1.0f, 0);  \
@@ -250,6 +278,25 @@ __device__ __forceinline__ uint32_t load_scale(const uint8_t* p) {
 
 __device__ __forceinline__ uint32_t load_u32(const uint8_t* p) {  // p 4-byte aligned
   return *(gu32*)(p);
+}
+
+// Buffer-resource loads: a wave-uniform descriptor (base, size), a per-lane
+// byte offset and a wave-uniform byte offset in a scalar register, so a run
+// of rows needs no per-row address registers.  Offsets past `bytes` read 0.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+__device__ __forceinline__ Rsrc make_rsrc(const uint8_t* base, uint32_t bytes) {
+  // dword 3 0x00020000: raw 32-bit data format, no swizzle (gfx9 family).
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ u32x4 rsrc_load_chunk_nt(Rsrc r, uint32_t lane_off, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, off, 2 /* nt */);
+}
+
+__device__ __forceinline__ uint32_t rsrc_load_u32(Rsrc r, uint32_t lane_off, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, lane_off, off, 0);
 }
 
 template <typename T>

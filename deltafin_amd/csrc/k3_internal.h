@@ -102,9 +102,11 @@ int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride,
                             hipStream_t stream);
 int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws,
                              hipStream_t stream);
+// pipelined: the plan came from the device router (rank-sorted plan); the
+// pipelined verify kernels then run where they are enabled.
 int launch_verify_layer(const Geo& g, int n_edges, int n_positions,
                         const void* x, int x_dtype, void* out, int out_dtype,
-                        const Workspace& ws, hipStream_t stream);
+                        const Workspace& ws, bool pipelined, hipStream_t stream);
 int launch_synth_bank(const Geo& g, uint8_t* bank, uint64_t stride,
                       int n_experts, uint64_t first_expert, uint64_t seed,
                       int lo, int hi, hipStream_t stream);

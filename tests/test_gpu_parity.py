@@ -360,3 +360,36 @@ def test_verify_table_matches_layer(gpu):
         ref, mag = oracle.moe_layer_f64([spans[e] for e in r], wts[offs[p]:offs[p + 1]], g.hidden,
                                         g.intermediate, g.activation, x[p])
         assert oracle.cond_rel_err(out[p], ref, mag, g.intermediate) <= TOL
+
+
+@pytest.mark.skip(reason="the pipelined verify kernels (rank-sorted plan, k_glu_verify, "
+                         "k_down_verify64) are switched off in the library: a timing run of "
+                         "device-routed verify over a 384-expert bank faulted the GPU and no "
+                         "cause has been found; the first-design kernels serve every call")
+@pytest.mark.parametrize("m", [4, 16])
+def test_verify_route_bank384(gpu, m):
+    """Device-routed verify over a config-3-sized bank (384 experts), the case
+    the pipelined verify kernels faulted on."""
+    import torch
+    from deltafin_amd import moe
+    g = moe.preset(2)
+    n_bank, k = 384, 16
+    say(f"verify route M={m} bank={n_bank}")
+    stride = g.expert_span
+    bank = torch.empty(n_bank * stride, dtype=torch.uint8, device="cuda")
+    moe.synth_bank(g, bank, stride, n_bank, 0, 777)
+    rng = np.random.default_rng(200 + m)
+    logits = rng.standard_normal((m, n_bank)).astype(np.float32)
+    x = synth.bf16_bits_to_f32(synth.to_bf16_bits(
+        rng.standard_normal((m, g.hidden)).astype(np.float32))).reshape(m, g.hidden)
+    ws = moe.workspace(g, m * k, m)
+    out, ids, _ = moe.moe_verify_route(g, bank, stride, n_bank, _t(logits), k,
+                                       _bf16(x).reshape(m, g.hidden), ws)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for p in range(m):
+        rid, rw = oracle.topk_softmax(logits[p], k)
+        assert ids[p].cpu().numpy().tolist() == rid.tolist()
+        spans = [oracle.synth_expert(777, int(e), g.hidden, g.intermediate) for e in rid]
+        ref, mag = oracle.moe_layer_f64(spans, rw, g.hidden, g.intermediate, g.activation, x[p])
+        assert oracle.cond_rel_err(out[p], ref, mag, g.intermediate) <= TOL
