@@ -733,23 +733,25 @@ __global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route, const
   extern __shared__ float4 hbuf[];  // kHSliceF4 float4 per wave
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPR
-  const int nw = blockDim.x >> 6;
   const int G = gridDim.x;
   const int nbt = (g.hidden + kB - 1) / kB;
   const int nb = (nbt - (int)blockIdx.x + G - 1) / G;  // 1 <= nb <= NB (host)
   const int cc[1] = {lane};
   auto row_of = [&](int i) { return (min(i, nb - 1) * G + (int)blockIdx.x) * kB; };
   auto rows_in = [&](int i) { return min(kB, g.hidden - row_of(i)); };
-  const RouteRegs rreg = route_regs(route, lane);
   const int idx = lane >> 4;
   const bool writer = (lane & 15) == 0;
-  for (int e = wave; e < route.n; e += nw) {
+  // One routed expert per wave (the host launches route.n <= 16 waves).
+  // h_e is indexed by route slot, so its loads go out before the route ids
+  // (and with them the expert's span) come back; then batches 0 and 1, then
+  // the LDS transpose waits for h_e (scheduling barriers keep the order).
+  const int e = wave;
+  float4 ht[8];
+  h_slice_issue(ht, h + (size_t)e * g.inter, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const RouteRegs rreg = route_regs(route, lane);
+  {
     const uint8_t* span = span_of(rreg, e);
-    // Issue h_e's loads, then batches 0 and 1, before the LDS transpose
-    // waits for h_e (scheduling barriers keep the order).
-    float4 ht[8];
-    h_slice_issue(ht, h + (size_t)e * g.inter, lane);
-    __builtin_amdgcn_sched_barrier(0);
     DownBatch<1, kB, true> bt[2];
     down_load(bt[0], span, g, cc, row_of(0), rows_in(0));
     if constexpr (NB > 1) down_load(bt[1], span, g, cc, row_of(1), rows_in(1));
@@ -1676,7 +1678,7 @@ int down_blocks_launch(const Geo& g, const TokenRoute& route, const float* h, OT
 template <typename OT, int NB>
 int down_g64_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out, int blocks,
                     hipStream_t st) {
-  const int nw = std::min(route.n, 16);
+  const int nw = route.n;  // one wave per routed expert (route.n <= 16)
   const unsigned lds = (unsigned)(nw * kHSliceF4 * sizeof(float4));
   if (!lds_fits((const void*)k_down_g64<OT, NB>, 64 * nw, lds))
     return fail(K3_HIP_E_EXEC, "decode layer: %u B of LDS per workgroup not available", lds);
@@ -1711,7 +1713,7 @@ template <typename OT>
 int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace& ws, OT* out,
                          hipStream_t st) {
   const int GB = g.inter / 32;
-  if (GB == 64) return down_g64_dispatch<OT>(g, route, ws.h, out, st);
+  if (GB == 64 && route.n <= 16) return down_g64_dispatch<OT>(g, route, ws.h, out, st);
   switch ((GB + 63) / 64) {
     case 1: return down_blocks_launch<OT, 1, kDownBlocksBatch>(g, route, ws.h, out, st);
     case 2: return down_blocks_launch<OT, 2, 2>(g, route, ws.h, out, st);
