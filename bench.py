@@ -76,6 +76,15 @@ def parse() -> argparse.Namespace:
                     help="CPU work budget for the reference CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--parity-tokens", type=int, default=2)
+    ap.add_argument("--verify-batches", type=int, default=20,
+                    help="verify batches timed per M for the config-3 line (0 skips it)")
+    ap.add_argument("--streamed", action="store_true",
+                    help="run BASELINE configs[4] (8 layers x 384 experts streamed from pinned host "
+                         "memory through a 24 GB HBM cache) instead of the decode bench")
+    ap.add_argument("--streamed-tokens", type=int, default=1000,
+                    help="timed tokens of --streamed (the default bench line carries a "
+                         "300-token run; 0 there skips it)")
+    ap.add_argument("--streamed-line-tokens", type=int, default=300)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 4 plain device copies of 1 GiB (the known-size kernel "
                          "the HBM byte counters are scaled by) and exit")
@@ -189,6 +198,221 @@ def cpu_baseline(bank_host: np.ndarray, logits: np.ndarray, x_f32: np.ndarray,
     return res, np.stack(outs), n
 
 
+STREAM_LAYERS = 8
+STREAM_SLOTS = 1025          # 24e9 B of HBM / 23,396,352 B per expert
+STREAM_ZIPF = 1.1
+STREAM_WARMUP_TOKENS = 200
+
+
+def streamed_config4(n_tokens: int) -> dict:
+    """8 layers x 384 experts (71.87 GB) in pinned host
+    memory (as many 8.98 GB layer banks as the host will pin; the rest alias
+    them), a 1,025-slot (24 GB) HBM LRU cache, 16 distinct experts per layer
+    per token drawn Zipf(1.1) over a per-layer rank permutation (seeded).  Per
+    layer: plan -> fetch the misses (side-stream copies) -> resolve (the
+    compute stream waits per expert) -> layer kernels -> release, with no host
+    synchronisation, x chained layer to layer in bf16.  Reports tokens/s, the
+    PCIe rate of the uploads, the hit rate, and the copy/compute overlap
+    1 - (wall - max(copy, compute)) / min(copy, compute), where compute is the
+    same token sequence over resident experts and copy the same plan/fetch
+    sequence with no kernels."""
+    import torch
+
+    from deltafin_amd import _lib, moe
+
+    torch.cuda.set_device(0)
+    lib = _lib.load()
+    if lib.k3_hip_moe_available(0) != 1:
+        raise _lib.K3HipError(lib.k3_hip_moe_available(0), "k3_hip_moe_available")
+    g = moe.preset(2)
+    L, NB = STREAM_LAYERS, N_BANK
+    # One pinned 8.98 GB bank per layer, as many as the host grants; logical
+    # layers past that read the bytes of pinned layer (layer % pinned) (the
+    # cache still keys every logical layer separately, so misses and uploads
+    # are those of 8 distinct layers).
+    t0 = time.perf_counter()
+    hosts = []
+    for layer in range(L):
+        try:
+            hosts.append(torch.empty(NB * SPAN, dtype=torch.uint8, pin_memory=True))
+        except Exception as e:  # torch raises its accelerator error (a RuntimeError) on OOM
+            log(f"streamed: pinned allocation of layer {layer} refused ({str(e).splitlines()[0]})")
+            break
+    if not hosts:
+        raise RuntimeError("streamed: no pinned host memory for even one layer")
+    t_alloc = time.perf_counter() - t0
+    log(f"streamed: {len(hosts)} x {NB * SPAN / 1e9:.2f} GB pinned host banks in {t_alloc:.1f} s")
+    bank = torch.empty(NB * SPAN, dtype=torch.uint8, device="cuda")
+    for layer, h in enumerate(hosts):
+        moe.synth_bank(g, bank, SPAN, NB, layer * NB, SEED)
+        h.copy_(bank)
+    torch.cuda.synchronize()
+    log(f"streamed: host banks filled ({time.perf_counter() - t0:.1f} s)")
+
+    # Routes: per layer a rank permutation, 16 distinct ranks per token ~ Zipf(1.1).
+    rng = np.random.default_rng(SEED + 4)
+    perms = [rng.permutation(NB) for _ in range(L)]
+    pz = np.arange(1, NB + 1, dtype=np.float64) ** -STREAM_ZIPF
+    pz /= pz.sum()
+    total = STREAM_WARMUP_TOKENS + n_tokens
+    routes = np.empty((total, L, TOP_K), dtype=np.int64)
+    for t in range(total):
+        for layer in range(L):
+            routes[t, layer] = np.sort(perms[layer][rng.choice(NB, TOP_K, replace=False, p=pz)])
+    weights = rng.random((total, L, TOP_K)).astype(np.float32)
+    weights /= weights.sum(axis=2, keepdims=True)
+
+    cache = lib.k3_hip_cache_create(0, SPAN, STREAM_SLOTS, L, 0)
+    if not cache:
+        raise _lib.K3HipError(-3, f"k3_hip_cache_create: {_lib.last_error()}")
+    xs = [moe.synth_normal(HIDDEN, torch.bfloat16, SEED + 5, 0),
+          torch.empty(HIDDEN, dtype=torch.bfloat16, device="cuda")]
+    ws = moe.workspace(g, TOP_K)
+    wsb, wsn = moe._ws_args(ws)
+    st = moe.stream_handle()
+    gref = C.byref(g)
+    host_base = [hosts[layer % len(hosts)].data_ptr() for layer in range(L)]
+    u16 = C.c_uint16 * TOP_K
+    missing = u16()
+    n_missing = C.c_int(0)
+    spans = (C.c_void_p * TOP_K)()
+    srcs = (C.c_void_p * TOP_K)()
+    plan_id = [0]
+
+    def layer_step(t: int, layer: int, cur: int) -> None:
+        ids = u16(*routes[t, layer].tolist())
+        plan_id[0] += 1
+        pid = plan_id[0]
+        rc = lib.k3_hip_cache_plan(cache, pid, layer, ids, TOP_K, missing, C.byref(n_missing))
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_cache_plan")
+        for i in range(n_missing.value):
+            srcs[i] = host_base[layer] + missing[i] * SPAN
+        rc = lib.k3_hip_cache_fetch(cache, pid, srcs, n_missing.value)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_cache_fetch")
+        rc = lib.k3_hip_cache_resolve(cache, pid, ids, TOP_K, spans, st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_cache_resolve")
+        w = (C.c_float * TOP_K)(*weights[t, layer].tolist())
+        rc = lib.k3_hip_moe_layer_device(gref, spans, w, TOP_K, xs[cur].data_ptr(),
+                                         _lib.K3_DTYPE_BF16, xs[1 - cur].data_ptr(),
+                                         _lib.K3_DTYPE_BF16, wsb, wsn, st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_moe_layer_device")
+        lib.k3_hip_cache_release(cache, pid)
+
+    def run(first: int, count: int) -> float:
+        cur = 0
+        torch.cuda.synchronize()
+        t_start = time.perf_counter()
+        for t in range(first, first + count):
+            for layer in range(L):
+                layer_step(t, layer, cur)
+                cur = 1 - cur
+        torch.cuda.synchronize()
+        return time.perf_counter() - t_start
+
+    six = (C.c_longlong * 6)()
+    run(0, STREAM_WARMUP_TOKENS)
+    lib.k3_hip_cache_stats(cache, six)
+    before = list(six)
+    wall = run(STREAM_WARMUP_TOKENS, n_tokens)
+    lib.k3_hip_cache_stats(cache, six)
+    hits, misses = six[0] - before[0], six[1] - before[1]
+    uploaded = six[5] - before[5]
+    lib.k3_hip_cache_destroy(cache)
+
+    # Compute alone: the same routes over experts resident in the device bank.
+    ptrs = [[(C.c_void_p * TOP_K)(*[bank.data_ptr() + int(e) * SPAN for e in routes[t, layer]])
+             for layer in range(L)] for t in range(STREAM_WARMUP_TOKENS, total)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    cur = 0
+    for i, t in enumerate(range(STREAM_WARMUP_TOKENS, total)):
+        for layer in range(L):
+            w = (C.c_float * TOP_K)(*weights[t, layer].tolist())
+            rc = lib.k3_hip_moe_layer_device(gref, ptrs[i][layer], w, TOP_K, xs[cur].data_ptr(),
+                                             _lib.K3_DTYPE_BF16, xs[1 - cur].data_ptr(),
+                                             _lib.K3_DTYPE_BF16, wsb, wsn, st)
+            if rc != 0:
+                raise _lib.K3HipError(rc, "k3_hip_moe_layer_device")
+            cur = 1 - cur
+    torch.cuda.synchronize()
+    compute = time.perf_counter() - t_start
+    # Copy alone: the same plan/fetch/release sequence on a fresh cache with
+    # no layer kernels (the side stream carries exactly the streamed run's
+    # uploads), warm-up tokens included and then timed like the run.
+    cache2 = lib.k3_hip_cache_create(0, SPAN, STREAM_SLOTS, L, 0)
+    if not cache2:
+        raise _lib.K3HipError(-3, f"k3_hip_cache_create: {_lib.last_error()}")
+
+    def fetch_only(first: int, count: int) -> float:
+        torch.cuda.synchronize()
+        t_start = time.perf_counter()
+        for t in range(first, first + count):
+            for layer in range(L):
+                ids = u16(*routes[t, layer].tolist())
+                plan_id[0] += 1
+                pid = plan_id[0]
+                if lib.k3_hip_cache_plan(cache2, pid, layer, ids, TOP_K, missing,
+                                         C.byref(n_missing)) != 0:
+                    raise _lib.K3HipError(-2, "k3_hip_cache_plan")
+                for i in range(n_missing.value):
+                    srcs[i] = host_base[layer] + missing[i] * SPAN
+                if lib.k3_hip_cache_fetch(cache2, pid, srcs, n_missing.value) != 0:
+                    raise _lib.K3HipError(-4, "k3_hip_cache_fetch")
+                if lib.k3_hip_cache_resolve(cache2, pid, ids, TOP_K, spans, st) != 0:
+                    raise _lib.K3HipError(-2, "k3_hip_cache_resolve")
+                lib.k3_hip_cache_release(cache2, pid)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t_start
+
+    fetch_only(0, STREAM_WARMUP_TOKENS)
+    copy = fetch_only(STREAM_WARMUP_TOKENS, n_tokens)
+    lib.k3_hip_cache_destroy(cache2)
+    # Context: pinned H2D rate of one 1.5 GB copy.
+    probe = 64 * SPAN
+    dst = torch.empty(probe, dtype=torch.uint8, device="cuda")
+    src = hosts[0][:probe]
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(3):
+        dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    h2d_gbs = 3 * probe / (time.perf_counter() - t_start) / 1e9
+    overlap = 1.0 - (wall - max(copy, compute)) / min(copy, compute) if min(copy, compute) > 0 else None
+    res = {
+        "metric": "streamed-expert MoE tokens/s (8 layers, 16-of-384 per layer, host -> 24 GB HBM cache)",
+        "value": round(n_tokens / wall, 2),
+        "unit": "tokens/s",
+        "higher_is_better": True,
+        "tokens": n_tokens,
+        "warmup_tokens": STREAM_WARMUP_TOKENS,
+        "ms_per_token": round(wall * 1e3 / n_tokens, 3),
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE configs[4]: 8 layers x 384 MXFP4 experts (71.87 GB) in pinned "
+                        "host memory, 1,025-slot (24 GB) HBM LRU, Zipf(1.1) routes of 16 distinct "
+                        "experts per layer, bf16 x chained through the layers",
+            "layers": L, "experts_per_layer": NB, "top_k": TOP_K, "cache_slots": STREAM_SLOTS,
+            "zipf": STREAM_ZIPF, "pinned_layers": len(hosts),
+            "host_bank_bytes_pinned": len(hosts) * NB * SPAN,
+        },
+        "hit_rate": round(hits / max(hits + misses, 1), 4),
+        "misses_per_token": round(misses / n_tokens, 2),
+        "pcie_gbs": round(uploaded / wall / 1e9, 2),
+        "h2d_probe_gbs": round(h2d_gbs, 2),
+        "compute_only_ms_per_token": round(compute * 1e3 / n_tokens, 3),
+        "copy_only_ms_per_token": round(copy * 1e3 / n_tokens, 3),
+        "overlap": None if overlap is None else round(overlap, 3),
+        "host_alloc_s": round(t_alloc, 1),
+    }
+    del hosts, bank, dst
+    return res
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -203,6 +427,9 @@ def main() -> int:
     args = parse()
     if args.copy_calibration:
         return copy_calibration()
+    if args.streamed:
+        print(json.dumps(streamed_config4(args.streamed_tokens)), flush=True)
+        return 0
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: the routed-expert path is built and measured "
               f"on a single MI355X (asked for --gpus {args.gpus}); multi-GPU sharding is a "
@@ -323,6 +550,14 @@ def main() -> int:
         "timing_dropped": dropped,
         "parity": parity,
     }
+    if args.verify_batches > 0:
+        res["verify"] = _verify_config3(moe, _lib, g, bank, stride, args.verify_batches)
+    if args.streamed_line_tokens > 0:
+        try:
+            res["streamed"] = streamed_config4(args.streamed_line_tokens)
+        except Exception as e:  # reported in the line rather than losing the decode result
+            log(f"streamed run failed: {e}")
+            res["streamed"] = {"error": str(e).splitlines()[0]}
     if not args.no_cpu:
         log("cpu baseline: copying the bank to host DRAM")
         bank_host = bank.cpu().numpy()
@@ -364,6 +599,64 @@ def _traffic_from_profiles(kernel: str):
             except ValueError:
                 return None
     return None
+
+
+MFMA_PEAK_FP4_TFLOPS = 10100.0  # dense MXFP4 on MI355X
+
+
+def _verify_config3(moe, _lib, g, bank, stride, batches: int) -> dict:
+    """batched speculative verify over the same resident
+    bank: M positions, each with its own top-16 of 384 N(0,1) logits and bf16
+    x; each routed expert's bytes are read once per batch (union of the M
+    routes).  Per M: `batches` batches timed back to back (after 3 warm-up
+    batches), bytes = union experts x span + M x (x + logits + out)."""
+    import torch
+
+    out = {}
+    for m in (4, 8, 16):
+        n = batches + 3
+        logits = moe.synth_normal(n * m * N_BANK, torch.float32, SEED + 30 + m, 1).view(n, m, N_BANK)
+        x = moe.synth_normal(n * m * HIDDEN, torch.bfloat16, SEED + 30 + m, 2).view(n, m, HIDDEN)
+        y = torch.empty((n, m, HIDDEN), dtype=torch.bfloat16, device="cuda")
+        ws = moe.workspace(g, m * TOP_K, m)
+        base, nbytes = moe._ws_args(ws)
+        st = moe.stream_handle()
+        lib = _lib.load()
+        ids = torch.empty((n, m, TOP_K), dtype=torch.int32, device="cuda")
+
+        def call(i: int) -> None:
+            rc = lib.k3_hip_moe_verify_route_device(
+                C.byref(g), bank.data_ptr(), stride, N_BANK, logits[i].data_ptr(), m, TOP_K,
+                x[i].data_ptr(), _lib.K3_DTYPE_BF16, y[i].data_ptr(), _lib.K3_DTYPE_BF16,
+                ids[i].data_ptr(), None, base, nbytes, st)
+            if rc != 0:
+                raise _lib.K3HipError(rc, "k3_hip_moe_verify_route_device")
+
+        for i in range(3):
+            call(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(3, n):
+            call(i)
+        torch.cuda.synchronize()
+        sec = (time.perf_counter() - t0) / batches
+        union = float(np.mean([len(set(ids[i].cpu().numpy().ravel().tolist())) for i in range(3, n)]))
+        nbytes_alg = union * SPAN + m * (X_BYTES + LOGIT_BYTES + OUT_BYTES)
+        flops = m * (KERNEL_FLOPS["glu_decode"] + KERNEL_FLOPS["down_decode"])
+        out[f"M{m}"] = {
+            "us_per_batch": round(sec * 1e6, 1),
+            "token_layers_per_s": round(m / sec, 1),
+            "union_experts": round(union, 1),
+            "algorithmic_bytes": int(nbytes_alg),
+            "achieved_gbs": round(nbytes_alg / sec / 1e9, 1),
+            "hbm_frac": round(nbytes_alg / sec / 1e9 / HBM_PEAK_GBS, 4),
+            "mfma_util": flops / sec / (MFMA_PEAK_FP4_TFLOPS * 1e12),
+        }
+        log(f"verify M={m}: {sec * 1e6:.1f} us/batch, union {union:.1f}, "
+            f"{nbytes_alg / sec / 1e9:.0f} GB/s")
+        del ws
+    return {"config": "BASELINE configs[3]: M positions each routing top-16 of 384, "
+                      "bf16 x/out, every routed expert read once per batch", **out}
 
 
 def _parity(moe, oracle, synth, g, bank, stride, logits, x, ws, n_tokens: int) -> dict:

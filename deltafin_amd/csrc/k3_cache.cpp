@@ -13,6 +13,10 @@
 //   copies on the execution stream through two pinned slabs (:757-805); here
 //   pinned sources are copied directly and pageable sources go through a ring
 //   of pinned staging slots.
+// * Because copies run on their own stream, a slot's previous contents may
+//   still be read by kernels the caller queued before release(): release()
+//   records a per-slot event on the stream the plan was resolved on, and a
+//   copy into an evicted slot first makes the side stream wait on it.
 #include <hip/hip_runtime_api.h>
 #include <string.h>
 
@@ -34,9 +38,13 @@ struct K3HipCache {
     int pins = 0;
     hipEvent_t ready = nullptr;
     bool has_event = false;
+    hipEvent_t done = nullptr;  // recorded at release on the plan's stream
+    bool has_done = false;
   };
   struct Plan {
     int layer = 0;
+    hipStream_t stream = nullptr;   // set by resolve()
+    bool resolved = false;
     std::vector<uint16_t> ids;      // canonical ascending
     std::vector<int> hit_slots;     // pinned at plan time
     std::vector<uint16_t> missing;  // ascending
@@ -126,6 +134,7 @@ K3HipCache* k3_hip_cache_create(int device, uint64_t span_bytes, int capacity_ex
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking);
   for (int i = 0; e == hipSuccess && i < capacity_experts; ++i) {
     e = hipEventCreateWithFlags(&c->slots[i].ready, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->slots[i].done, hipEventDisableTiming);
   }
   for (int i = 0; e == hipSuccess && i < staging_slots; ++i) {
     uint8_t* p = nullptr;
@@ -151,8 +160,10 @@ void k3_hip_cache_destroy(K3HipCache* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   if (c->side) (void)hipStreamSynchronize(c->side);
-  for (auto& s : c->slots)
+  for (auto& s : c->slots) {
     if (s.ready) (void)hipEventDestroy(s.ready);
+    if (s.done) (void)hipEventDestroy(s.done);
+  }
   for (size_t i = 0; i < c->staging.size(); ++i) {
     (void)hipEventDestroy(c->staging_ready[i]);
     (void)hipHostFree(c->staging[i]);
@@ -215,7 +226,13 @@ int k3_hip_cache_fetch(K3HipCache* c, uint64_t plan_id, const uint8_t* const* so
     if (slot < 0) return fail(K3_HIP_E_ALLOC, "cache fetch: every slot is pinned by live plans");
     K3HipCache::Slot& s = c->slots[slot];
     uint8_t* dst = c->slab + (uint64_t)slot * c->slot_bytes;
-    hipError_t e;
+    hipError_t e = hipSuccess;
+    // Kernels queued on a caller stream may still read the slot's previous
+    // expert: the copy waits for the release point of its last plan.
+    if (s.has_done) {
+      e = hipStreamWaitEvent(c->side, s.done, 0);
+      if (e != hipSuccess) return hip_fail("cache fetch wait for slot reuse", e);
+    }
     if (pinned_host(sources[i]) || c->staging.empty()) {
       e = hipMemcpyAsync(dst, sources[i], c->span, hipMemcpyHostToDevice, c->side);
     } else {
@@ -266,6 +283,8 @@ int k3_hip_cache_resolve(K3HipCache* c, uint64_t plan_id, const uint16_t* ids, i
   if (pit == c->plans.end()) return fail(K3_HIP_E_INVALID, "cache resolve: stale or unknown plan");
   int rc = set_device(c);
   if (rc != K3_HIP_OK) return rc;
+  pit->second.stream = static_cast<hipStream_t>(stream);
+  pit->second.resolved = true;
   for (int i = 0; i < n; ++i) {
     const int slot = plan_slot(pit->second, ids[i]);
     if (slot == -2) return fail(K3_HIP_E_INVALID, "cache resolve: expert %d outside the plan", ids[i]);
@@ -314,10 +333,23 @@ void k3_hip_cache_release(K3HipCache* c, uint64_t plan_id) {
   std::lock_guard<std::mutex> lk(c->mu);
   auto pit = c->plans.find(plan_id);
   if (pit == c->plans.end()) return;
-  for (int s : pit->second.hit_slots)
-    if (s >= 0 && c->slots[s].pins > 0) --c->slots[s].pins;
-  for (int s : pit->second.miss_slots)
-    if (s >= 0 && c->slots[s].pins > 0) --c->slots[s].pins;
+  K3HipCache::Plan& p = pit->second;
+  (void)set_device(c);
+  auto unpin = [&](int s) {
+    if (s < 0) return;
+    K3HipCache::Slot& slot = c->slots[s];
+    // Everything the caller queued on the plan's stream so far may read the
+    // slot; a later copy into it waits for this point.
+    if (p.resolved) {
+      if (hipEventRecord(slot.done, p.stream) == hipSuccess)
+        slot.has_done = true;
+      else
+        (void)hipGetLastError();
+    }
+    if (slot.pins > 0) --slot.pins;
+  };
+  for (int s : p.hit_slots) unpin(s);
+  for (int s : p.miss_slots) unpin(s);
   c->plans.erase(pit);
 }
 
