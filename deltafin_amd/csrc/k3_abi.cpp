@@ -816,13 +816,33 @@ int k3_hip_moe_verify_route_device(const K3HipGeometryV1* gd, const uint8_t* ban
   Workspace ws;
   if (!carve_workspace(workspace, workspace_bytes, g, n_edges, n_positions, &ws))
     return fail(K3_HIP_E_INVALID, "verify: workspace missing, misaligned or too small");
+  if (n_bank > 4096) return fail(K3_HIP_E_INVALID, "verify: n_bank must be at most 4096");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int rc = launch_route(logits, n_bank, top_k, n_positions, ws.ids, ws.w, route_ids,
-                        route_weights, st);
-  if (rc == K3_HIP_OK) rc = launch_verify_plan_bank(g, bank, expert_stride, n_positions, top_k, ws, st);
-  if (rc == K3_HIP_OK)
-    rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, true, st);
-  return rc;
+  // One routed decode layer per position, in order on the stream: each
+  // position's gate/up kernel ranks its own logits, so the routes equal the
+  // per-position router's.  An expert picked by several positions is read once
+  // per position; with independent routes the union is nearly M * top_k
+  // experts anyway, and these kernels stream about twice as fast as the
+  // union-sharing verify kernels (design notes).
+  const size_t xb = x_dtype == K3_DTYPE_BF16 ? 2 : 4, ob = out_dtype == K3_DTYPE_BF16 ? 2 : 4;
+  for (int p = 0; p < n_positions; ++p) {
+    TokenRoute route;
+    memset(&route, 0, sizeof(route));
+    route.bank = bank;
+    route.stride = expert_stride;
+    route.logits = logits + (size_t)p * n_bank;
+    route.n_bank = n_bank;
+    route.ids_pub = ws.ids;
+    route.w_pub = ws.w;
+    route.ids_user = route_ids ? route_ids + (size_t)p * top_k : nullptr;
+    route.w_user = route_weights ? route_weights + (size_t)p * top_k : nullptr;
+    route.n = top_k;
+    const int rc = launch_decode_layer(g, route, static_cast<const uint8_t*>(x) + p * g.hidden * xb,
+                                       x_dtype, static_cast<uint8_t*>(out) + p * g.hidden * ob,
+                                       out_dtype, ws, st);
+    if (rc != K3_HIP_OK) return rc;
+  }
+  return K3_HIP_OK;
 }
 
 int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* edge_experts,
@@ -868,10 +888,46 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
     tbl.ptr[i] = edge_experts[i];
     tbl.w[i] = edge_weights[i];
   }
-  int rc = launch_verify_plan_table(tbl, ws, st);
-  if (rc == K3_HIP_OK)
-    rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, false, st);
-  return rc;
+  // Positions that share most of their experts: the union kernels read each
+  // shared expert once; otherwise one decode layer per position (about twice
+  // the streaming rate of the union kernels, so they win unless the union is
+  // under half the edges).
+  int n_unique = 0;
+  for (int i = 0; i < n_edges; ++i) {
+    bool seen = false;
+    for (int j = 0; j < i && !seen; ++j) seen = tbl.ptr[j] == tbl.ptr[i];
+    n_unique += !seen;
+  }
+  if (2 * n_unique <= n_edges) {
+    int rc = launch_verify_plan_table(tbl, ws, st);
+    if (rc == K3_HIP_OK)
+      rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, false, st);
+    return rc;
+  }
+  const size_t xb = x_dtype == K3_DTYPE_BF16 ? 2 : 4, ob = out_dtype == K3_DTYPE_BF16 ? 2 : 4;
+  for (int p = 0; p < n_positions; ++p) {
+    const int e0 = position_offsets[p], n = position_offsets[p + 1] - e0;
+    uint8_t* outp = static_cast<uint8_t*>(out) + p * g.hidden * ob;
+    if (n == 0) {  // no routed expert: a zero row
+      const hipError_t e = hipMemsetAsync(outp, 0, g.hidden * ob, st);
+      if (e != hipSuccess) return hip_fail("verify: zero row", e);
+      continue;
+    }
+    if (n > K3_HIP_MAX_TOKEN_EXPERTS)
+      return fail(K3_HIP_E_INVALID, "verify: position %d has %d edges (at most %d)", p, n,
+                  K3_HIP_MAX_TOKEN_EXPERTS);
+    TokenRoute route;
+    memset(&route, 0, sizeof(route));
+    route.n = n;
+    for (int i = 0; i < n; ++i) {
+      route.ptr[i] = tbl.ptr[e0 + i];
+      route.w[i] = tbl.w[e0 + i];
+    }
+    const int rc = launch_decode_layer(g, route, static_cast<const uint8_t*>(x) + p * g.hidden * xb,
+                                       x_dtype, outp, out_dtype, ws, st);
+    if (rc != K3_HIP_OK) return rc;
+  }
+  return K3_HIP_OK;
 }
 
 int k3_hip_synth_bank(const K3HipGeometryV1* gd, uint8_t* bank, uint64_t expert_stride,
