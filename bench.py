@@ -50,14 +50,18 @@ OUT_BYTES = HIDDEN * 2                                    # bf16 output
 LOGIT_BYTES = N_BANK * 4
 H_BYTES = TOP_K * INTER * 4                               # fp32 h handed from gate/up to down
 LAYER_BYTES = TOP_K * SPAN + X_BYTES + LOGIT_BYTES + OUT_BYTES  # 374,371,840
-# Per launch of each decode kernel: gate/up (with the router folded in) reads
+# Per launch of each decode kernel.  The fused kernel (the default path) reads
+# the logits, x and all 48 matrices, writes h and reads it back, and writes the
+# output row.  On the two-launch path gate/up (with the router folded in) reads
 # the logits, x and 32 gate/up matrices and writes h; down reads 16 down
 # matrices and h and writes the output row.
 KERNEL_BYTES = {
+    "decode_fused": 3 * TOP_K * MAT_BYTES + X_BYTES + LOGIT_BYTES + 2 * H_BYTES + OUT_BYTES,
     "glu_decode": 2 * TOP_K * MAT_BYTES + X_BYTES + LOGIT_BYTES + H_BYTES,
     "down_decode": TOP_K * MAT_BYTES + H_BYTES + OUT_BYTES,
 }
 KERNEL_FLOPS = {
+    "decode_fused": 3 * 2 * TOP_K * INTER * HIDDEN,
     "glu_decode": 2 * 2 * TOP_K * INTER * HIDDEN,
     "down_decode": 2 * TOP_K * INTER * HIDDEN,
 }
@@ -517,6 +521,33 @@ def main() -> int:
         "avg_launch_us": round(dom_s * 1e6, 3),
     }
 
+    # ---- the same K steps on the other decode path, for comparison: the
+    # opt-in fused single launch (k_decode_fused) when the default two-launch
+    # path ran, and the reverse
+    fused_ran = "decode_fused" in kern
+    prev = _lib.set_fused_decode(not fused_ran)
+    try:
+        for i in range(20):
+            step(i)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for i in range(args.steps):
+            step(args.warmup + i)
+        torch.cuda.synchronize()
+        wall2 = time.perf_counter() - t1
+        _lib.timing_begin(4 * args.steps + 16)
+        for i in range(args.steps):
+            step(args.warmup + i)
+        kern2, _ = _lib.timing_end()
+    finally:
+        _lib.set_fused_decode(prev)
+    alt = {"path": "two-launch" if fused_ran else "fused single launch",
+           "value": round(args.steps / wall2, 2), "unit": "token-layers/s",
+           "ms_per_step": round(wall2 * 1e3 / args.steps, 5),
+           "kernels_us": {k: round(v["avg_ms"] * 1e3, 3) for k, v in kern2.items()}}
+    log(f"{alt['path']} path: {alt['value']:.1f} tok/s, " +
+        ", ".join(f"{k} {v} us" for k, v in alt["kernels_us"].items()))
+
     # ---- parity of sampled tokens (fp32 output before rounding) against the fp64 oracle
     parity = _parity(moe, oracle, synth, g, bank, stride, logits, x, ws, args.parity_tokens)
 
@@ -548,6 +579,7 @@ def main() -> int:
         "roofline": roofline,
         "kernels_us": {k: round(v["avg_ms"] * 1e3, 3) for k, v in kern.items()},
         "timing_dropped": dropped,
+        "other_decode_path": alt,
         "parity": parity,
     }
     if args.verify_batches > 0:

@@ -130,6 +130,7 @@ SIGNATURES = {
     "k3_hip_timing_begin": (_i32, [_i32]),
     "k3_hip_timing_end": (_i32, [C.POINTER(K3HipKernelTimingV1), _i32, C.POINTER(_i32),
                                  C.POINTER(C.c_longlong)]),
+    "k3_hip_set_fused_decode": (_i32, [_i32]),
     "k3_hip_synth_bank": (_i32, [_GP, _vp, _u64, _i32, _u64, _u64, _i32, _i32, _vp]),
     "k3_hip_synth_normal": (_i32, [_vp, _i32, _u64, _u64, _u64, _vp]),
 }
@@ -207,6 +208,12 @@ def preset(which: int) -> K3HipGeometryV1:
     g = K3HipGeometryV1()
     check(load().k3_hip_geometry_preset(which, C.byref(g)), "k3_hip_geometry_preset")
     return g
+
+
+def set_fused_decode(enabled: bool) -> bool:
+    """Select the fused single-launch decode path or the two-launch path (the
+    default) for later layer calls; returns the previous setting."""
+    return bool(load().k3_hip_set_fused_decode(1 if enabled else 0))
 
 
 def timing_begin(max_launches: int) -> None:

@@ -930,6 +930,8 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
   return K3_HIP_OK;
 }
 
+int k3_hip_set_fused_decode(int enabled) { return set_fused_decode(enabled); }
+
 int k3_hip_synth_bank(const K3HipGeometryV1* gd, uint8_t* bank, uint64_t expert_stride,
                       int n_experts, uint64_t first_expert, uint64_t seed, int scale_lo,
                       int scale_hi, void* stream) {

@@ -95,6 +95,9 @@ int launch_route(const float* logits, int n_bank, int top_k, int n_positions,
 int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x,
                         int x_dtype, void* out, int out_dtype,
                         const Workspace& ws, hipStream_t stream);
+// Process-wide decode path switch (k3_hip_set_fused_decode); returns the
+// previous setting.
+int set_fused_decode(int enabled);
 // LDS bytes the in-kernel router needs for a bank of n_bank logits and top_k.
 size_t route_scratch_bytes(int n_bank, int top_k);
 int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride,
@@ -131,6 +134,7 @@ enum KernelClass : int {
   KC_DOWN_VERIFY,
   KC_COMBINE,
   KC_SYNTH,
+  KC_DECODE_FUSED,
   KC_COUNT
 };
 

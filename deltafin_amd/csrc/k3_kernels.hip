@@ -21,8 +21,10 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include <hip/hip_ext.h>
 
@@ -382,6 +384,107 @@ __device__ __forceinline__ uint32_t gathered_scale(uint32_t word, int bp, int ro
 
 __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
                            uint64_t* keys, int* sel, float* wsel);
+
+// The route as every wave of the workgroup holds it (lane e: expert e's span
+// and weight).  Router mode: the workgroup ranks the logits itself (no
+// separate launch; keys is route_scratch_bytes of LDS) and workgroup 0
+// publishes the route for later kernels and the caller.  All threads call it.
+__device__ __forceinline__ RouteRegs workgroup_route(const TokenRoute& route, uint64_t* keys,
+                                                     int* sel, float* wsel, int lane) {
+  if (!route.logits) return route_regs(route, lane);
+  block_topk(route.logits, route.n_bank, route.n, keys, sel, wsel);
+  if (blockIdx.x == 0) {
+    for (int j = threadIdx.x; j < route.n; j += blockDim.x) {
+      route.ids_pub[j] = sel[j];
+      route.w_pub[j] = wsel[j];
+      if (route.ids_user) route.ids_user[j] = sel[j];
+      if (route.w_user) route.w_user[j] = wsel[j];
+    }
+  }
+  RouteRegs rr;
+  rr.lo = rr.hi = 0u;
+  rr.w = 0.0f;
+  if (lane < route.n) {
+    const uint64_t p = reinterpret_cast<uint64_t>(route.bank) + (uint64_t)sel[lane] * route.stride;
+    rr.lo = (uint32_t)p;
+    rr.hi = (uint32_t)(p >> 32);
+    rr.w = wsel[lane];
+  }
+  return rr;
+}
+
+__device__ __forceinline__ int glu_pair0(int q0, int Q, int n_units, int kR, int it) {
+  const int u = q0 + it * Q;
+  return (u < n_units ? u : 0) * kR;
+}
+
+// The gate/up sweep of one pipeline: pipeline q0 of Q takes units q0, q0 + Q,
+// ... (iters of them) with two units in flight, unit it + 1 requested before
+// unit it is reduced.  A unit past n_units repeats unit 0's loads and stores
+// nothing, so every wave of the workgroup reaches the same iters barriers.
+// The S wave partials of a unit meet in red (two slots by unit parity, one
+// barrier per unit); kR lanes of the pipeline's wave 0 sum them in wave
+// order, apply the activation and store h.
+template <typename XT, int kR, bool kG, bool kDeviceStore = false>
+__device__ __forceinline__ void glu_sweep(const RouteRegs& rr, const Geo& g, const XChunk<XT>& xc,
+                                          const ColSplit& cs, const GluGather& gg, int row_step,
+                                          int S, int grp, int gw, int wave, int lane, int q0,
+                                          int Q, int iters, int n_units, float* __restrict__ h,
+                                          float (*red)[16][2 * kR]) {
+  constexpr int N = 2 * kR;
+  constexpr int L = log2c<N>();
+  auto unit_pair0 = [&](int it) { return glu_pair0(q0, Q, n_units, kR, it); };
+  auto finish = [&](const GluBatch<XT, kR, kG>& bt, int it) {
+    const int u = q0 + it * Q;
+    const int parity = it & 1;
+    float v[N];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      if constexpr (kG) {
+        v[r] = xc.dot(bt.wg[r]) * e8m0_scale(gathered_scale(bt.sg[0], gg.bp, row_step, r, lane));
+        v[kR + r] =
+            xc.dot(bt.wu[r]) * e8m0_scale(gathered_scale(bt.su[0], gg.bp, row_step, r, lane));
+      } else {
+        v[r] = xc.dot(bt.wg[r]) * e8m0_scale(bt.sg[r]);
+        v[kR + r] = xc.dot(bt.wu[r]) * e8m0_scale(bt.su[r]);
+      }
+    }
+    wave_reduce_multi<N>(v, lane);
+    if ((lane & ((1 << (6 - L)) - 1)) == 0) red[parity][wave][lane >> (6 - L)] = v[0];
+    lds_barrier();
+    if (u < n_units && gw == 0 && lane < kR) {
+      const int w0 = grp * S;
+      float gv = red[parity][w0][lane], uv = red[parity][w0][kR + lane];
+      for (int w = 1; w < S; ++w) {
+        gv += red[parity][w0 + w][lane];
+        uv += red[parity][w0 + w][kR + lane];
+      }
+      const float hv = activate(g.act, gv, uv);
+      if constexpr (kDeviceStore)  // written through to the device-coherent level
+        __hip_atomic_store(h + (size_t)u * kR + lane, hv, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      else
+        h[(size_t)u * kR + lane] = hv;
+    }
+  };
+  GluBatch<XT, kR, kG> A, B;
+  glu_load(A, rr, g, unit_pair0(0), cs, gg);
+  glu_load(B, rr, g, unit_pair0(min(1, iters - 1)), cs, gg);
+  for (int it = 0;; it += 2) {
+    finish(A, it);
+    if (it + 2 >= iters) {
+      if (it + 1 < iters) finish(B, it + 1);
+      break;
+    }
+    glu_load(A, rr, g, unit_pair0(it + 2), cs, gg);
+    finish(B, it + 1);
+    if (it + 3 >= iters) {
+      finish(A, it + 2);
+      break;
+    }
+    glu_load(B, rr, g, unit_pair0(it + 3), cs, gg);
+  }
+}
 
 // Unit pipelines per gate/up workgroup (each S column-split waves) and rows
 // per unit; the launch bound follows so the register budget matches the
@@ -772,6 +875,253 @@ __global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route, const
     float acc = 0.0f;
     for (int e = 0; e < route.n; ++e) acc += weight_of(rreg, e) * ybuf[e][t];
     store_out(out + row, acc);
+  }
+}
+
+// ======================================================================
+// fused decode: router, gate/up and down + combine in one launch
+// ======================================================================
+// The work of a token is cut into tickets: n_glu gate/up tickets (ticket v is
+// the sweep share of one k_glu_decode workgroup: pipelines v * groups .. +
+// groups - 1 of Q = n_glu * groups) followed by n_down down tickets (ticket
+// d is the output-row share of k_down_g64 workgroup d of n_down).  A
+// workgroup claims tickets from a counter one at a time, each claim issued
+// while the previous ticket runs, and processes them in claim order.  A down
+// ticket waits until every gate/up ticket has released its h stores.  That
+// wait always ends: the counter hands out every gate/up ticket before the
+// first down ticket, a workgroup holding a gate/up ticket is running and
+// finishes it without waiting for anything, so no workgroup waits on work
+// that is not already held by a running workgroup, however many workgroups
+// are resident.  The wait is still bounded (kFusedSpinLimit polls); a
+// workgroup that gives up writes NaN to its output rows.
+//
+// Cross-workgroup state lives in a slot of g_fused_sync, one slot per caller
+// workspace (calls that share a workspace are ordered, so no two launches use
+// a slot at once).  Slots are zero when the code object loads, and the last
+// workgroup of every launch returns its slot to zero.
+//
+// Opt-in only: on MI355X at config 2 it takes 83 us per token against 67 us
+// for k_glu_decode + k_down_g64.  Per-workgroup phase stamps put the loss in
+// three places: 1024-thread workgroups start over ~4 us (512-thread ones over
+// 0.8 us) and so finish gate/up later; every down ticket waits for the last
+// gate/up ticket plus a poll of the counter; then all workgroups read the
+// whole h at device scope at once.
+struct FusedSync {
+  unsigned ticket;  // tickets claimed
+  unsigned done;    // gate/up tickets whose h stores are released
+  unsigned exited;  // workgroups finished
+  unsigned pad[61];
+};
+constexpr int kFusedSlots = 64;
+constexpr int kFusedSpinLimit = 1 << 20;
+static __device__ __align__(256) FusedSync g_fused_sync[kFusedSlots] = {};
+
+struct FusedPlan {
+  int n_units;  // gate/up units (route.n * inter / kR)
+  int S;        // column-split waves per gate/up pipeline
+  int groups;   // gate/up pipelines per workgroup
+  int n_glu;    // gate/up tickets
+  int n_down;   // down tickets
+  int slot;     // g_fused_sync slot
+};
+
+// Handing h between workgroups.  K3_FUSED_SYNC 1: h is stored and loaded at
+// device scope (written through to, and read from, the level every XCD
+// shares), and a store counts once the wave has seen it acknowledged; no
+// cache-wide maintenance.  0: plain h accesses ordered by agent-scope
+// release / acquire fences (an L2 write-back per storing wave, an L2
+// invalidate per waiting workgroup).
+#ifndef K3_FUSED_SYNC
+#define K3_FUSED_SYNC 1
+#endif
+constexpr bool kFusedDeviceScope = K3_FUSED_SYNC == 1;
+
+// Wait until every memory operation this wave issued has completed (stores
+// and atomics acknowledged); the signal fences keep the compiler from moving
+// memory operations across the wait.
+__device__ __forceinline__ void wait_vm_complete() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt unconstrained
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// h_e's 8 KB for h_slice_transpose, loaded at device scope (sc1).
+__device__ __forceinline__ void h_slice_issue_device(float4 (&t)[8], const float* he, int lane) {
+  const Rsrc r = make_rsrc(reinterpret_cast<const uint8_t*>(he), 8192u);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)lane * 16u,
+                                                          (uint32_t)q * 1024u, 16 /* sc1 */);
+    t[q] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                       __uint_as_float(v[3]));
+  }
+}
+
+__device__ __forceinline__ unsigned agent_add(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Lane 0 of the calling wave polls *c until it reaches target (at most
+// kFusedSpinLimit polls); with fences, the wave then acquires at agent scope
+// (its caches hold nothing older than the releases it observed).  Returns
+// whether the count was reached.
+__device__ __forceinline__ bool wait_count(unsigned* c, unsigned target, int lane) {
+  int ok = 1;
+  if (lane == 0) {
+    int i = 0;
+    while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      if (++i == kFusedSpinLimit) {
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  if constexpr (kFusedDeviceScope)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  else
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return __builtin_amdgcn_readfirstlane(ok) != 0;
+}
+
+template <typename XT, typename OT, int kR, int NB>
+__global__ __launch_bounds__(1024) void k_decode_fused(const TokenRoute route, const Geo g,
+                                                       const XT* __restrict__ x, float* h,
+                                                       OT* __restrict__ out, const FusedPlan fp) {
+  constexpr int kB = 4;
+  // Dynamic LDS: the router's keys at the start, then the waves' h slices.
+  extern __shared__ __attribute__((aligned(16))) float4 fused_lds[];
+  __shared__ float red[2][16][2 * kR];
+  __shared__ float ybuf[K3_HIP_MAX_TOKEN_EXPERTS][NB * kB];
+  __shared__ int sel[K3_HIP_MAX_TOKEN_EXPERTS];
+  __shared__ float wsel[K3_HIP_MAX_TOKEN_EXPERTS];
+  __shared__ unsigned s_ticket[2];
+  __shared__ int s_ok;
+  FusedSync* sy = &g_fused_sync[fp.slot];
+  const int S = fp.S;
+  const int G = g.hidden >> 5;
+  const int row_step = (G + S - 1) / S;
+  const unsigned n_glu = (unsigned)fp.n_glu;
+  const unsigned n_total = n_glu + (unsigned)fp.n_down;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  unsigned claim = 0;
+  if (threadIdx.x == 0) claim = agent_add(&sy->ticket, 1u);
+  const RouteRegs rr =
+      workgroup_route(route, reinterpret_cast<uint64_t*>(fused_lds), sel, wsel, lane);
+  if (threadIdx.x == 0) s_ticket[0] = claim;
+  __syncthreads();
+  unsigned t = s_ticket[0];
+  int i = 1;
+  // Tickets come in increasing order, so a workgroup's gate/up tickets all
+  // precede its down tickets: two loops, each with only its own phase's
+  // values live.
+  if (t < n_glu) {
+    const int grp = wave / S;
+    const int gw = wave - grp * S;
+    const int Q = fp.n_glu * fp.groups;
+    const int iters = (fp.n_units + Q - 1) / Q;
+    const ColSplit cs = col_split(G, S, gw, lane);
+    const GluGather gg = glu_gather(G, S, gw, lane, kR);
+    XChunk<XT> xc;
+    load_x_chunk<XT>(xc, x, cs);
+    for (; t < n_glu; ++i) {
+      if (threadIdx.x == 0) claim = agent_add(&sy->ticket, 1u);
+      if (grp < fp.groups) {
+        glu_sweep<XT, kR, true, kFusedDeviceScope>(rr, g, xc, cs, gg, row_step, S, grp, gw,
+                                                   wave, lane, (int)t * fp.groups + grp, Q,
+                                                   iters, fp.n_units, h, red);
+        // This wave's h stores are visible device-wide before the ticket
+        // counts as done.
+        if (gw == 0) {
+          if constexpr (kFusedDeviceScope)
+            wait_vm_complete();
+          else
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        }
+      } else {
+        for (int it = 0; it < iters; ++it) lds_barrier();  // the sweep's barriers
+      }
+      if (threadIdx.x == 0) s_ticket[i & 1] = claim;
+      __syncthreads();
+      if (threadIdx.x == 0) agent_add(&sy->done, 1u);
+      t = s_ticket[i & 1];
+    }
+  }
+  {
+    // Down ticket d: output-row batches d, d + n_down, ... (nb <= NB of
+    // them), one routed expert per wave.  The expert's first two weight
+    // batches are requested before the wait for h.
+    const int cc[1] = {lane};
+    const int idx = lane >> 4;
+    const bool writer = (lane & 15) == 0;
+    const int e = wave;
+    const bool active = e < route.n;
+    const uint8_t* span = span_of(rr, active ? e : 0);
+    const int nbt = (g.hidden + kB - 1) / kB;
+    for (; t < n_total; ++i) {
+      if (threadIdx.x == 0) claim = agent_add(&sy->ticket, 1u);
+      const int d = (int)(t - n_glu);
+      const int nb = (nbt - d + fp.n_down - 1) / fp.n_down;
+      auto row_of = [&](int b) { return (min(b, nb - 1) * fp.n_down + d) * kB; };
+      auto rows_in = [&](int b) { return min(kB, g.hidden - row_of(b)); };
+      DownBatch<1, kB, true> bt[2];
+      if (active) {
+        down_load(bt[0], span, g, cc, row_of(0), rows_in(0));
+        if constexpr (NB > 1) down_load(bt[1], span, g, cc, row_of(1), rows_in(1));
+      }
+      if (wave == 0) {
+        const bool ok = wait_count(&sy->done, n_glu, lane);
+        if (lane == 0) s_ok = ok ? 1 : 0;
+      }
+      __syncthreads();
+      if (active) {
+        float4 ht[8];
+        if constexpr (kFusedDeviceScope)
+          h_slice_issue_device(ht, h + (size_t)e * g.inter, lane);
+        else
+          h_slice_issue(ht, h + (size_t)e * g.inter, lane);
+        XChunk<float> hs;
+        h_slice_transpose(hs, ht, fused_lds + wave * kHSliceF4, lane);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const float v = down_dots(bt[b & 1], &hs, lane);
+          if (b + 2 < NB) down_load(bt[b & 1], span, g, cc, row_of(b + 2), rows_in(b + 2));
+          if (writer && b < nb && idx < rows_in(b)) ybuf[e][b * kB + idx] = v;
+        }
+      }
+      __syncthreads();
+      const bool ok = s_ok != 0;
+      for (int r = threadIdx.x; r < nb * kB; r += blockDim.x) {
+        const int row = row_of(r / kB) + (r % kB);
+        if (row >= g.hidden) continue;
+        float acc = 0.0f;
+        for (int k = 0; k < route.n; ++k) acc += weight_of(rr, k) * ybuf[k][r];
+        store_out(out + row, ok ? acc : __builtin_nanf(""));
+      }
+      if (threadIdx.x == 0) s_ticket[i & 1] = claim;
+      __syncthreads();
+      t = s_ticket[i & 1];
+    }
+  }
+  // Exit: every claim this workgroup made has returned (its value decided the
+  // loop), and thread 0's done increments are acknowledged before its exit
+  // increment (a workgroup that held no down ticket never waited for them).
+  // The last workgroup out returns the slot to zero.
+  if (threadIdx.x == 0) {
+    unsigned old;
+    if constexpr (kFusedDeviceScope) {
+      wait_vm_complete();
+      old = agent_add(&sy->exited, 1u);
+    } else {
+      old = __hip_atomic_fetch_add(&sy->exited, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (old == gridDim.x - 1) {
+      __hip_atomic_store(&sy->ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&sy->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&sy->exited, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -1723,7 +2073,102 @@ int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace&
   }
 }
 
+// Fused decode (k_decode_fused) when selected (k3_hip_set_fused_decode; off
+// by default: it measures slower than the two launches, see the kernel's
+// comment) and its shape holds: intermediate 2048 (64 scale groups per down
+// row), at most 16 routed experts, gathered gate/up scales, and a free
+// g_fused_sync slot for the workspace.  *ran tells the caller whether it
+// launched; otherwise the two-launch path runs.
+#ifndef K3_FUSED_DECODE
+#define K3_FUSED_DECODE 0
+#endif
+#ifndef K3_FUSED_GLU_GROUPS
+#define K3_FUSED_GLU_GROUPS 2
+#endif
+
+std::atomic<int> g_fused_enabled{K3_FUSED_DECODE};
+
+// Slot of g_fused_sync for a workspace on the current device, -1 once every
+// slot is taken.  A workspace keeps its slot for the life of the process.
+int fused_slot(const void* ws_base) {
+  static std::mutex mu;
+  static std::unordered_map<int, std::vector<const void*>> table;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  std::lock_guard<std::mutex> lock(mu);
+  std::vector<const void*>& v = table[dev];
+  for (size_t i = 0; i < v.size(); ++i)
+    if (v[i] == ws_base) return (int)i;
+  if ((int)v.size() >= kFusedSlots) return -1;
+  v.push_back(ws_base);
+  return (int)v.size() - 1;
+}
+
+// Launched for bf16 activations only (fused_decode): an fp32 x slice (32
+// registers) does not fit the 1024-thread register budget next to the
+// gate/up batches.
+template <typename OT, int NB>
+int fused_launch(const Geo& g, const TokenRoute& route, const uint16_t* x, float* h, OT* out,
+                 const FusedPlan& fp, int grid, hipStream_t st, bool* ran) {
+  const size_t keys = route.logits ? route_scratch_bytes(route.n_bank, route.n) : 0;
+  const size_t lds = std::max(keys, (size_t)16 * kHSliceF4 * sizeof(float4));
+  const void* kernel = (const void*)k_decode_fused<uint16_t, OT, kRowsGlu, NB>;
+  if (!lds_fits(kernel, 1024, lds)) return K3_HIP_OK;  // two-launch path
+  *ran = true;
+  TimedLaunch tl(KC_DECODE_FUSED, st);
+  launch_timed(tl, (k_decode_fused<uint16_t, OT, kRowsGlu, NB>), dim3(grid), dim3(1024),
+               (unsigned)lds, st, route, g, x, h, out, fp);
+  return launched(tl, "fused decode launch");
+}
+
+template <typename OT>
+int fused_decode(const Geo& g, const TokenRoute& route, const float* x, OT* out,
+                 const Workspace& ws, hipStream_t st, bool* ran) {
+  *ran = false;  // fp32 activations: two-launch path
+  return K3_HIP_OK;
+}
+
+template <typename OT>
+int fused_decode(const Geo& g, const TokenRoute& route, const uint16_t* x, OT* out,
+                 const Workspace& ws, hipStream_t st, bool* ran) {
+  *ran = false;
+  if (!g_fused_enabled.load(std::memory_order_relaxed)) return K3_HIP_OK;
+  const int G = g.hidden / 32;
+  const int S = (G + 63) / 64;
+  const int cw = (G + S - 1) / S;
+  const bool gather = kRowsGlu == 4 && G % 4 == 0 && cw % 4 == 0 && kRowsGlu * cw <= 256;
+  if (S > 4 || !gather || g.inter != 64 * 32 || route.n > 16) return K3_HIP_OK;
+  const int slot = fused_slot(ws.base);
+  if (slot < 0) return K3_HIP_OK;
+  const int cus = std::max(1, device_cu_count());
+  FusedPlan fp;
+  fp.S = S;
+  fp.groups = std::max(1, std::min(K3_FUSED_GLU_GROUPS, 16 / S));
+  fp.n_units = route.n * (g.inter / kRowsGlu);
+  fp.n_glu = std::max(1, std::min(cus, (fp.n_units + fp.groups - 1) / fp.groups));
+  const int nbt = (g.hidden + 3) / 4;
+  fp.n_down = std::min(nbt, std::max(cus, (nbt + kDownG64MaxNB - 1) / kDownG64MaxNB));
+  fp.slot = slot;
+  const int nb = (nbt + fp.n_down - 1) / fp.n_down;
+  const int grid = std::min(cus, std::max(fp.n_glu, fp.n_down));
+  switch (nb) {
+    case 1: return fused_launch<OT, 1>(g, route, x, ws.h, out, fp, grid, st, ran);
+    case 2: return fused_launch<OT, 2>(g, route, x, ws.h, out, fp, grid, st, ran);
+    case 3: return fused_launch<OT, 3>(g, route, x, ws.h, out, fp, grid, st, ran);
+    case 4: return fused_launch<OT, 4>(g, route, x, ws.h, out, fp, grid, st, ran);
+    case 5: return fused_launch<OT, 5>(g, route, x, ws.h, out, fp, grid, st, ran);
+    case 6: return fused_launch<OT, 6>(g, route, x, ws.h, out, fp, grid, st, ran);
+    case 7: return fused_launch<OT, 7>(g, route, x, ws.h, out, fp, grid, st, ran);
+    case 8: return fused_launch<OT, 8>(g, route, x, ws.h, out, fp, grid, st, ran);
+    default: return K3_HIP_OK;
+  }
+}
+
 }  // namespace
+
+int set_fused_decode(int enabled) {
+  return g_fused_enabled.exchange(enabled ? 1 : 0);
+}
 
 size_t route_scratch_bytes(int n_bank, int top_k) {
   const size_t nseg = (size_t)(n_bank + 63) / 64;
@@ -1735,6 +2180,20 @@ int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x, in
   if (route.n <= 0 || route.n > K3_HIP_MAX_TOKEN_EXPERTS)
     return fail(K3_HIP_E_INVALID, "decode layer: expert count %d outside [1, %d]", route.n,
                 K3_HIP_MAX_TOKEN_EXPERTS);
+  bool ran = false;
+  const int frc =
+      x_dtype == K3_DTYPE_BF16
+          ? (out_dtype == K3_DTYPE_BF16
+                 ? fused_decode(g, route, static_cast<const uint16_t*>(x),
+                                static_cast<uint16_t*>(out), ws, st, &ran)
+                 : fused_decode(g, route, static_cast<const uint16_t*>(x),
+                                static_cast<float*>(out), ws, st, &ran))
+          : (out_dtype == K3_DTYPE_BF16
+                 ? fused_decode(g, route, static_cast<const float*>(x),
+                                static_cast<uint16_t*>(out), ws, st, &ran)
+                 : fused_decode(g, route, static_cast<const float*>(x), static_cast<float*>(out),
+                                ws, st, &ran));
+  if (frc != K3_HIP_OK || ran) return frc;
   int rc = x_dtype == K3_DTYPE_BF16
                ? glu_decode_dispatch<uint16_t>(g, route, static_cast<const uint16_t*>(x), ws.h, st)
                : glu_decode_dispatch<float>(g, route, static_cast<const float*>(x), ws.h, st);

@@ -25,6 +25,7 @@ namespace {
 const char* const kClassNames[KC_COUNT] = {
     "gemv",        "activate",    "route",       "glu_decode", "down_decode",
     "verify_plan", "glu_verify",  "down_verify", "combine",    "synth",
+    "decode_fused",
 };
 
 struct TimingState {

@@ -194,9 +194,8 @@ int k3_hip_moe_launch(const K3HipGeometryV1* g, const uint8_t* expert_span,
                       float* expert_output, void* stream);
 
 /* Device workspace bytes needed by the layer / verify calls below for up to
- * max_edges routed edges over max_positions positions.  The workspace must be
- * zero-filled once before first use; every call leaves it reusable.  Calls
- * that share one workspace must not overlap. */
+ * max_edges routed edges over max_positions positions.  Its contents need no
+ * initialisation.  Calls that share one workspace must not overlap. */
 uint64_t k3_hip_moe_workspace_bytes(const K3HipGeometryV1* g, int max_edges,
                                     int max_positions);
 
@@ -318,6 +317,16 @@ typedef struct K3HipKernelTimingV1 {
 int k3_hip_timing_begin(int max_launches);
 int k3_hip_timing_end(K3HipKernelTimingV1* out, int capacity, int* n_out,
                       long long* dropped);
+
+/* ============================== decode kernel selection */
+/* No reference counterpart.  A single-token layer call above runs as a
+ * gate/up launch and a down launch (the default).  enabled = 1 makes every
+ * later call in the process run as one fused launch (router, gate/up, down
+ * and ordered combine) where its shape allows it (bf16 x, intermediate 2048,
+ * at most 16 experts, one of 64 workspaces per device); 0 restores the
+ * default.  Both paths compute bit-identical outputs; the fused one is
+ * slower on MI355X.  Returns the previous setting. */
+int k3_hip_set_fused_decode(int enabled);
 
 /* ============================== synthetic inputs (benchmark support) */
 /* No reference counterpart.  Fill device memory with the counter-based

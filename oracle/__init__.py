@@ -24,7 +24,9 @@ Pins for each oracle function (tests/test_oracle.py):
   expert_f64 (SiTU)   the reference's mxfp4_moe_expert_set within 2e-4 relative
   moe_layer_f64       numpy ordered weighted sum of expert_f64 outputs; the
                       reference mxfp4_moe_expert_set (SiTU) for the full set
-  topk_softmax        numpy stable argsort / exp-normalise
+  topk_softmax        numpy stable argsort / exp-normalise; NaN ranked as -inf
+                      and -0 equal to +0 wherever they sit (the order the
+                      reference leaves open for NaN, whose route it rejects)
   synth               numpy restatement in deltafin_amd/synth.py (bit-exact)
 """
 from __future__ import annotations

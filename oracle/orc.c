@@ -164,6 +164,15 @@ void orc_moe_layer_f64(const uint8_t *const *spans, int n_experts,
     free(m);
 }
 
+/* The order the router ranks logits in: NaN as -inf and -0 as +0, so that the
+ * order is total (ties then go to the lower index).  The reference does not
+ * fix it for NaN: its router takes torch.topk and then rejects a route with a
+ * non-finite weight (provider_moe.cpp:570-586, :1673-1683). */
+static double rank_value(float v) {
+    if (v != v) return -INFINITY;
+    return v == 0.0f ? 0.0 : (double)v;
+}
+
 int orc_topk_softmax(const float *logits, int n, int k, int *ids,
                      double *weights) {
     if (n <= 0 || k <= 0 || k > n) return -1;
@@ -174,16 +183,16 @@ int orc_topk_softmax(const float *logits, int n, int k, int *ids,
         int best = -1;
         for (int i = 0; i < n; i++) {
             if (taken[i]) continue;
-            if (best < 0 || logits[i] > logits[best]) best = i;
+            if (best < 0 || rank_value(logits[i]) > rank_value(logits[best])) best = i;
         }
         taken[best] = 1;
         ids[j] = best;
     }
     free(taken);
-    const double top = (double)logits[ids[0]];
+    const double top = rank_value(logits[ids[0]]);
     double sum = 0.0;
     for (int j = 0; j < k; j++) {
-        weights[j] = exp((double)logits[ids[j]] - top);
+        weights[j] = exp(rank_value(logits[ids[j]]) - top);
         sum += weights[j];
     }
     for (int j = 0; j < k; j++) weights[j] /= sum;

@@ -296,6 +296,25 @@ def test_topk_ties_prefer_lower_index():
     assert w[0] == w[1] and w[2] == w[3]
 
 
+@pytest.mark.parametrize("pos", [0, 3, 7])
+def test_topk_nan_ranks_as_minus_inf(pos):
+    """A NaN logit ranks with -inf (lower index first on the tie) wherever it
+    sits, and its weight is exp(-inf) = 0."""
+    lg = np.array([0.1, -0.2, 0.3, -np.inf, 0.0, -0.0, 1.5, -3.0], np.float32)
+    lg[pos] = np.nan
+    ids, w = oracle.topk_softmax(lg, 8)
+    vals = np.where(np.isnan(lg), -np.inf, lg).astype(np.float64)
+    order = sorted(range(8), key=lambda i: (-vals[i], i))  # -0 == +0, ties to the lower index
+    assert ids.tolist() == order
+    assert w[ids.tolist().index(pos)] == 0.0
+    np.testing.assert_allclose(w.sum(), 1.0, rtol=1e-15)
+
+
+def test_topk_signed_zero_ties():
+    ids, _ = oracle.topk_softmax(np.array([-0.0, 0.0, -0.0], np.float32), 3)
+    assert ids.tolist() == [0, 1, 2]
+
+
 # ------------------------------------------------------------------ synthetic generator
 def test_synth_c_equals_numpy_restatement():
     for stream in (0, 5, 1151):
