@@ -131,6 +131,7 @@ SIGNATURES = {
     "k3_hip_timing_end": (_i32, [C.POINTER(K3HipKernelTimingV1), _i32, C.POINTER(_i32),
                                  C.POINTER(C.c_longlong)]),
     "k3_hip_set_fused_decode": (_i32, [_i32]),
+    "k3_hip_scale4_check_header": (_i32, [_vp, _u64]),
     "k3_hip_synth_bank": (_i32, [_GP, _vp, _u64, _i32, _u64, _u64, _i32, _i32, _vp]),
     "k3_hip_synth_normal": (_i32, [_vp, _i32, _u64, _u64, _u64, _vp]),
 }

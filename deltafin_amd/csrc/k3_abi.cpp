@@ -58,9 +58,85 @@ bool make_geo(const K3HipGeometryV1* d, Geo* out) {
   g.w3p = g.w2s + w2s;
   g.w3s = g.w3p + w13p;
   g.span = g.w3s + w13s;
+  g.layout = K3_LAYOUT_RAW_V1;
   if (d->expert_span != g.span) return false;
   *out = g;
   return true;
+}
+
+// ---------------------------------------------------------------- scale4-v2
+namespace {
+constexpr uint32_t kS4Header = 8192;
+
+uint32_t le32(const uint8_t* p) {
+  return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
+}
+uint64_t le64(const uint8_t* p) { return (uint64_t)le32(p) | (uint64_t)le32(p + 4) << 32; }
+bool all_zero(const uint8_t* p, size_t begin, size_t end) {
+  for (size_t i = begin; i < end; ++i)
+    if (p[i]) return false;
+  return true;
+}
+}  // namespace
+
+bool make_geo_scale4(const Geo& raw, Geo* out) {
+  if (raw.hidden != 3584 || raw.inter != 3072) return false;
+  const uint64_t packed = (uint64_t)raw.hidden * raw.inter / 2;
+  const uint64_t s4 = (uint64_t)raw.hidden * (raw.inter / 32) / 2;  // same for all three
+  Geo g = raw;
+  g.w1p = kS4Header;
+  g.w1s = g.w1p + packed;
+  g.w2p = g.w1s + s4;
+  g.w2s = g.w2p + packed;
+  g.w3p = g.w2s + s4;
+  g.w3s = g.w3p + packed;
+  g.span = g.w3s + s4;
+  g.layout = K3_LAYOUT_SCALE4_V2;
+  if (g.span != K3_SCALE4_V2_EXPERT_SPAN) return false;
+  *out = g;
+  return true;
+}
+
+// The format fixes every field for the K3 geometry: identity and lengths,
+// the in-memory payload table (offset, bytes of w1p, w1s, w2p, w2s, w3p,
+// w3s), the on-disk sidecar table (offset, bytes of the three index planes),
+// zero padding, and per matrix a base <= 240 with the 16-entry table of E8M0
+// float bits (base + d) << 23.  Bytes 32-63 (the source digest) are free.
+const char* scale4_header_error(const uint8_t* p) {
+  static const uint8_t magic[8] = {'K', '3', 'S', 'C', '4', 'V', '2', 0};
+  Geo raw, g;
+  K3HipGeometryV1 d;
+  memset(&d, 0, sizeof(d));
+  d.abi_version = 1;
+  d.struct_bytes = sizeof(d);
+  d.hidden = 3584;
+  d.intermediate = 3072;
+  d.activation = K3_ACT_SITU;
+  d.expert_span = K3_RAW_V1_EXPERT_SPAN;
+  if (!make_geo(&d, &raw) || !make_geo_scale4(raw, &g)) return "scale4-v2 geometry";
+  if (!p) return "null scale4-v2 header";
+  if (memcmp(p, magic, sizeof(magic)) != 0 || le32(p + 8) != 2 || le32(p + 12) != kS4Header ||
+      le64(p + 16) != g.span || le64(p + 24) != raw.span)
+    return "invalid scale4-v2 header identity or length";
+  const uint32_t packed = (uint32_t)(g.w1s - g.w1p), s4 = (uint32_t)(g.w2p - g.w1s);
+  const uint32_t payload[12] = {(uint32_t)g.w1p, packed, (uint32_t)g.w1s, s4,
+                                (uint32_t)g.w2p, packed, (uint32_t)g.w2s, s4,
+                                (uint32_t)g.w3p, packed, (uint32_t)g.w3s, s4};
+  for (int i = 0; i < 12; ++i)
+    if (le32(p + 72 + 4 * i) != payload[i]) return "invalid scale4-v2 payload table";
+  const uint32_t sidecar[6] = {kS4Header, s4, kS4Header + s4, s4, kS4Header + 2 * s4, s4};
+  for (int i = 0; i < 6; ++i)
+    if (le32(p + 320 + 4 * i) != sidecar[i]) return "invalid scale4-v2 sidecar payload table";
+  if (!all_zero(p, 67, 72) || !all_zero(p, 120, 128) || !all_zero(p, 344, kS4Header))
+    return "scale4-v2 reserved header bytes are nonzero";
+  for (int m = 0; m < 3; ++m) {
+    const uint32_t base = p[64 + m];
+    if (base > 240) return "scale4-v2 base exceeds the exact uint8 range";
+    for (uint32_t delta = 0; delta < 16; ++delta)
+      if (le32(p + 128 + 64 * m + 4 * delta) != (base + delta) << 23)
+        return "scale4-v2 exponent table does not match its base";
+  }
+  return nullptr;
 }
 
 namespace {
@@ -304,8 +380,9 @@ void evict_one_locked(Context& c, const std::vector<const uint8_t*>& keep) {
 
 // Device address for one blob; uploads host blobs into the HBM cache.
 // `temps` collects uncached uploads to free after the call.
-int resolve_blob_locked(Context& c, const uint8_t* blob, const std::vector<const uint8_t*>& call,
-                        const uint8_t** out, std::vector<uint8_t*>* temps) {
+int resolve_blob_locked(Context& c, const Geo& lg, const uint8_t* blob,
+                        const std::vector<const uint8_t*>& call, const uint8_t** out,
+                        std::vector<uint8_t*>* temps) {
   const int kind = classify(blob);
   if (kind == 2) {
     ++c.device_uses;
@@ -313,7 +390,7 @@ int resolve_blob_locked(Context& c, const uint8_t* blob, const std::vector<const
     return K3_HIP_OK;
   }
   auto it = c.blobs.find(blob);
-  if (it != c.blobs.end() && it->second.span == c.geo.span && c.cache_mode == 1) {
+  if (it != c.blobs.end() && it->second.span == lg.span && c.cache_mode == 1) {
     it->second.last_use = ++c.clock;
     *out = it->second.dev;
     return K3_HIP_OK;
@@ -331,13 +408,13 @@ int resolve_blob_locked(Context& c, const uint8_t* blob, const std::vector<const
     }
   }
   uint8_t* dev = nullptr;
-  hipError_t e = hipMalloc(reinterpret_cast<void**>(&dev), c.geo.span);
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&dev), lg.span);
   if (e != hipSuccess) {
     (void)hipGetLastError();
     return fail(K3_HIP_E_ALLOC, "expert upload allocation: %s", hipGetErrorString(e));
   }
-  e = kind == 1 ? hipMemcpyAsync(dev, blob, c.geo.span, hipMemcpyHostToDevice, c.stream)
-                : hipMemcpy(dev, blob, c.geo.span, hipMemcpyHostToDevice);
+  e = kind == 1 ? hipMemcpyAsync(dev, blob, lg.span, hipMemcpyHostToDevice, c.stream)
+                : hipMemcpy(dev, blob, lg.span, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     (void)hipFree(dev);
     return fail(K3_HIP_E_COPY, "expert upload: %s", hipGetErrorString(e));
@@ -346,7 +423,7 @@ int resolve_blob_locked(Context& c, const uint8_t* blob, const std::vector<const
   if (keep) {
     BlobEntry be;
     be.dev = dev;
-    be.span = c.geo.span;
+    be.span = lg.span;
     be.last_use = ++c.clock;
     c.blobs[blob] = be;
   } else {
@@ -364,28 +441,57 @@ int finish_call_locked(Context& c, std::vector<uint8_t*>& temps, int rc) {
   return K3_HIP_OK;
 }
 
-// Descriptor validation (tools/metal_moe.mm:407-450).
+// Descriptor validation (tools/metal_moe.mm:407-450): every descriptor of a
+// call has the same layout, its byte length is that layout's span, and a
+// scale4-v2 blob's header passes scale4_header_error (read from device memory
+// when the blob is there).  *lg receives the call's layout geometry.
 int check_descriptors(const Context& c, const K3HipExpertDescriptorV1* d, int count,
-                      std::vector<const uint8_t*>* blobs) {
+                      std::vector<const uint8_t*>* blobs, Geo* lg) {
   if (count < 0 || (count > 0 && !d))
     return fail(K3_HIP_E_DESCRIPTOR, "invalid expert descriptor array");
   blobs->clear();
+  *lg = c.geo;
+  uint32_t selected = 0;
+  std::vector<uint8_t> header;
   for (int i = 0; i < count; ++i) {
     if (d[i].abi_version != K3_DESCRIPTOR_ABI_V1 ||
         d[i].struct_bytes != sizeof(K3HipExpertDescriptorV1) || d[i].reserved != 0 ||
         !d[i].blob)
       return fail(K3_HIP_E_DESCRIPTOR, "invalid expert descriptor fields (index %d)", i);
-    if (d[i].layout_id == K3_LAYOUT_SCALE4_V2)
-      return fail(K3_HIP_E_CAPABILITY, "scale4-v2 layout is not supported by this build");
-    if (d[i].layout_id != K3_LAYOUT_RAW_V1 || d[i].blob_bytes != c.geo.span)
-      return fail(K3_HIP_E_DESCRIPTOR, "unknown expert layout or byte length (index %d)", i);
+    Geo cand = c.geo;
+    if (d[i].layout_id == K3_LAYOUT_SCALE4_V2) {
+      if (!make_geo_scale4(c.geo, &cand))
+        return fail(K3_HIP_E_CAPABILITY,
+                    "scale4-v2 needs the K3 geometry (hidden 3584, intermediate 3072)");
+    } else if (d[i].layout_id != K3_LAYOUT_RAW_V1) {
+      return fail(K3_HIP_E_DESCRIPTOR, "unknown expert layout (index %d)", i);
+    }
+    if (d[i].blob_bytes != cand.span)
+      return fail(K3_HIP_E_DESCRIPTOR, "expert byte length does not match its layout (index %d)", i);
+    if (i == 0) {
+      selected = d[i].layout_id;
+      *lg = cand;
+    } else if (d[i].layout_id != selected) {
+      return fail(K3_HIP_E_DESCRIPTOR, "mixed expert layouts are not allowed in one call");
+    }
+    if (d[i].layout_id == K3_LAYOUT_SCALE4_V2) {
+      const uint8_t* hp = d[i].blob;
+      if (classify(d[i].blob) == 2) {
+        header.resize(8192);
+        const hipError_t e = hipMemcpy(header.data(), d[i].blob, 8192, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_fail("scale4-v2 header read", e);
+        hp = header.data();
+      }
+      if (const char* why = scale4_header_error(hp))
+        return fail(K3_HIP_E_DESCRIPTOR, "%s (index %d)", why, i);
+    }
     blobs->push_back(d[i].blob);
   }
   return K3_HIP_OK;
 }
 
-int layer_locked(Context& c, const uint8_t* const* blobs, int n, const float* weights,
-                 const float* x, float* out) {
+int layer_locked(Context& c, const Geo& lg, const uint8_t* const* blobs, int n,
+                 const float* weights, const float* x, float* out) {
   if (!x || !out || n < 0) return fail(K3_HIP_E_INVALID, "layer: null input/output or n < 0");
   const size_t hb = (size_t)c.geo.hidden * 4;
   if (n == 0) {
@@ -404,7 +510,7 @@ int layer_locked(Context& c, const uint8_t* const* blobs, int n, const float* we
   route.n = n;
   for (int i = 0; i < n; ++i) {
     if (!blobs[i]) return fail(K3_HIP_E_INVALID, "layer: null blob %d", i);
-    const int rc = resolve_blob_locked(c, blobs[i], call, &route.ptr[i], &temps);
+    const int rc = resolve_blob_locked(c, lg, blobs[i], call, &route.ptr[i], &temps);
     if (rc != K3_HIP_OK) return finish_call_locked(c, temps, rc);
     route.w[i] = weights[i];
   }
@@ -413,7 +519,7 @@ int layer_locked(Context& c, const uint8_t* const* blobs, int n, const float* we
     return finish_call_locked(c, temps, fail(K3_HIP_E_COPY, "layer input copy: %s", hipGetErrorString(e)));
   Workspace ws;
   carve_workspace(c.ws, c.ws_bytes, c.geo, K3_HIP_MAX_EDGES, K3_HIP_MAX_POSITIONS, &ws);
-  int rc = launch_decode_layer(c.geo, route, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws, c.stream);
+  int rc = launch_decode_layer(lg, route, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws, c.stream);
   if (rc == K3_HIP_OK &&
       (e = hipMemcpyAsync(c.hout, c.dout, hb, hipMemcpyDeviceToHost, c.stream)) != hipSuccess)
     rc = fail(K3_HIP_E_COPY, "layer output copy: %s", hipGetErrorString(e));
@@ -424,8 +530,9 @@ int layer_locked(Context& c, const uint8_t* const* blobs, int n, const float* we
   return K3_HIP_OK;
 }
 
-int positions_locked(Context& c, const uint8_t* const* blobs, int n_edges, const int* offs,
-                     int n_pos, const float* weights, const float* x, float* out) {
+int positions_locked(Context& c, const Geo& lg, const uint8_t* const* blobs, int n_edges,
+                     const int* offs, int n_pos, const float* weights, const float* x,
+                     float* out) {
   // Offset validation mirrors tools/metal_moe.mm:852-871.
   if (n_edges < 0 || n_pos < 0) return fail(K3_HIP_E_INVALID, "positions: negative counts");
   if (n_pos == 0) return n_edges == 0 ? K3_HIP_OK : fail(K3_HIP_E_INVALID, "positions: edges without positions");
@@ -456,7 +563,7 @@ int positions_locked(Context& c, const uint8_t* const* blobs, int n_edges, const
   for (int i = 0; i < n_edges; ++i) {
     if (!blobs[i]) return fail(K3_HIP_E_INVALID, "positions: null blob %d", i);
     // Repeated blobs resolve to the same device address, so the plan groups them.
-    const int rc = resolve_blob_locked(c, blobs[i], call, &tbl.ptr[i], &temps);
+    const int rc = resolve_blob_locked(c, lg, blobs[i], call, &tbl.ptr[i], &temps);
     if (rc != K3_HIP_OK) return finish_call_locked(c, temps, rc);
     tbl.w[i] = weights[i];
   }
@@ -465,10 +572,34 @@ int positions_locked(Context& c, const uint8_t* const* blobs, int n_edges, const
     return finish_call_locked(c, temps, fail(K3_HIP_E_COPY, "positions input copy: %s", hipGetErrorString(e)));
   Workspace ws;
   carve_workspace(c.ws, c.ws_bytes, c.geo, K3_HIP_MAX_EDGES, K3_HIP_MAX_POSITIONS, &ws);
-  int rc = launch_verify_plan_table(tbl, ws, c.stream);
-  if (rc == K3_HIP_OK)
-    rc = launch_verify_layer(c.geo, n_edges, n_pos, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws, false,
-                             c.stream);
+  int rc = K3_HIP_OK;
+  if (lg.layout == K3_LAYOUT_SCALE4_V2) {
+    // scale4-v2 runs through the decode kernels: one layer per position (a
+    // position with no edges gets a zero row).
+    for (int p = 0; p < n_pos && rc == K3_HIP_OK; ++p) {
+      float* op = c.dout + (size_t)p * c.geo.hidden;
+      const int n = offs[p + 1] - offs[p];
+      if (n == 0) {
+        e = hipMemsetAsync(op, 0, (size_t)c.geo.hidden * 4, c.stream);
+        if (e != hipSuccess) rc = hip_fail("positions zero row", e);
+        continue;
+      }
+      TokenRoute route;
+      memset(&route, 0, sizeof(route));
+      route.n = n;
+      for (int j = 0; j < n; ++j) {
+        route.ptr[j] = tbl.ptr[offs[p] + j];
+        route.w[j] = tbl.w[offs[p] + j];
+      }
+      rc = launch_decode_layer(lg, route, c.dx + (size_t)p * c.geo.hidden, K3_DTYPE_F32, op,
+                               K3_DTYPE_F32, ws, c.stream);
+    }
+  } else {
+    rc = launch_verify_plan_table(tbl, ws, c.stream);
+    if (rc == K3_HIP_OK)
+      rc = launch_verify_layer(c.geo, n_edges, n_pos, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws,
+                               false, c.stream);
+  }
   if (rc == K3_HIP_OK &&
       (e = hipMemcpyAsync(c.hout, c.dout, bytes, hipMemcpyDeviceToHost, c.stream)) != hipSuccess)
     rc = fail(K3_HIP_E_COPY, "positions output copy: %s", hipGetErrorString(e));
@@ -537,7 +668,14 @@ uint64_t k3_hip_layout_capabilities(void) {
   Context& c = ctx();
   std::lock_guard<std::mutex> lk(c.mu);
   if (!init_locked(c, nullptr)) return 0;
-  return K3_CAP_RAW_V1;
+  Geo g4;
+  return K3_CAP_RAW_V1 | (make_geo_scale4(c.geo, &g4) ? K3_CAP_SCALE4_V2 : 0);
+}
+
+int k3_hip_scale4_check_header(const uint8_t* header, uint64_t bytes) {
+  if (!header || bytes < 8192) return fail(K3_HIP_E_INVALID, "scale4-v2 header needs 8192 bytes");
+  if (const char* why = scale4_header_error(header)) return fail(K3_HIP_E_DESCRIPTOR, "%s", why);
+  return K3_HIP_OK;
 }
 
 int k3_hip_configure_v1(const K3HipGeometryV1* geometry) {
@@ -615,9 +753,10 @@ int k3_hip_moe_layer_desc_v1(const K3HipExpertDescriptorV1* experts, int expert_
   std::lock_guard<std::mutex> lk(c.mu);
   if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
   std::vector<const uint8_t*> blobs;
-  const int rc = check_descriptors(c, experts, expert_count, &blobs);
+  Geo lg;
+  const int rc = check_descriptors(c, experts, expert_count, &blobs, &lg);
   if (rc != K3_HIP_OK) return rc;
-  return layer_locked(c, blobs.empty() ? nullptr : blobs.data(), expert_count, weights, input,
+  return layer_locked(c, lg, blobs.empty() ? nullptr : blobs.data(), expert_count, weights, input,
                       output);
 }
 
@@ -628,9 +767,10 @@ int k3_hip_moe_positions_desc_v1(const K3HipExpertDescriptorV1* experts, int edg
   std::lock_guard<std::mutex> lk(c.mu);
   if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
   std::vector<const uint8_t*> blobs;
-  const int rc = check_descriptors(c, experts, edge_count, &blobs);
+  Geo lg;
+  const int rc = check_descriptors(c, experts, edge_count, &blobs, &lg);
   if (rc != K3_HIP_OK) return rc;
-  return positions_locked(c, blobs.empty() ? nullptr : blobs.data(), edge_count,
+  return positions_locked(c, lg, blobs.empty() ? nullptr : blobs.data(), edge_count,
                           position_offsets, position_count, weights, input, output);
 }
 
@@ -639,7 +779,7 @@ int k3_hip_moe_layer(const uint8_t* const* expert_blobs, int n_experts, const fl
   Context& c = ctx();
   std::lock_guard<std::mutex> lk(c.mu);
   if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
-  return layer_locked(c, expert_blobs, n_experts, weights, x, out);
+  return layer_locked(c, c.geo, expert_blobs, n_experts, weights, x, out);
 }
 
 int k3_hip_moe_positions(const uint8_t* const* expert_blobs, int n_edges,
@@ -648,8 +788,8 @@ int k3_hip_moe_positions(const uint8_t* const* expert_blobs, int n_edges,
   Context& c = ctx();
   std::lock_guard<std::mutex> lk(c.mu);
   if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
-  return positions_locked(c, expert_blobs, n_edges, position_offsets, n_positions, weights, x,
-                          out);
+  return positions_locked(c, c.geo, expert_blobs, n_edges, position_offsets, n_positions, weights,
+                          x, out);
 }
 
 // ------------------------------------------------------------ surface 2

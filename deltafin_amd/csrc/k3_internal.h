@@ -8,15 +8,26 @@
 
 namespace k3 {
 
-// Byte offsets of one raw-v1 expert span (provider_moe.cpp:217-243).
+// Byte offsets of one expert span: raw-v1 (provider_moe.cpp:217-243), or
+// scale4-v2 (tools/metal_moe.mm:127-155), where w1s / w2s / w3s are planes of
+// 4-bit scale indices (two per byte, low nibble first, over the flattened
+// [rows][groups] scale order) and the E8M0 scale of index d is base + d, the
+// three bases being bytes 64, 65, 66 of the span (w1, w2, w3).
 struct Geo {
   int hidden;        // H: gate/up columns, down rows, x/out length
   int inter;         // I: gate/up rows, down columns, h length
   int act;           // K3_ACT_*
   uint64_t w1p, w1s, w2p, w2s, w3p, w3s, span;
+  int layout;        // K3_LAYOUT_RAW_V1 or K3_LAYOUT_SCALE4_V2
 };
 
 bool make_geo(const K3HipGeometryV1* g, Geo* out);
+// The scale4-v2 layout of a raw geometry: the reference fixes it for K3 only
+// (hidden 3584, intermediate 3072, span 17,039,360); false otherwise.
+bool make_geo_scale4(const Geo& raw, Geo* out);
+// Header checks of a scale4-v2 span (tools/metal_moe.mm:353-405); p holds the
+// span's first 8192 bytes in host memory.  nullptr when valid, else the reason.
+const char* scale4_header_error(const uint8_t* p);
 
 // Expert addressing for one token (decode) or one edge set: either a resident
 // bank indexed by device-side ids, or explicit span pointers passed by value.

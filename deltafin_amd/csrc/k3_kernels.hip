@@ -23,6 +23,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 #include <vector>
 
@@ -315,8 +316,16 @@ __device__ __forceinline__ void lds_barrier() {
 // them (one load per matrix instead of kR single-byte loads), and the byte of
 // row r for lane l (group c0 + l) is routed to it by a ds_bpermute from lane
 // r * cw / 4 + l / 4.
-template <typename XT, int kR, bool kG = false>
-struct GluBatch {
+// kS4 (scale4-v2 spans, gathered scales only): sg / su hold gathered index
+// dwords and b4 the unit's expert bases (bytes 64-66 of its span).
+struct NoBases {};
+struct SpanBases {
+  uint32_t b4;
+};
+
+template <typename XT, int kR, bool kG = false, bool kS4 = false>
+struct GluBatch : std::conditional_t<kS4, SpanBases, NoBases> {
+  static_assert(!kS4 || kG, "scale4-v2 gate/up loads need gathered scales");
   u32x4 wg[kR], wu[kR];
   uint32_t sg[kG ? 1 : kR], su[kG ? 1 : kR];
 };
@@ -340,16 +349,34 @@ __device__ __forceinline__ GluGather glu_gather(int G, int S, int wave, int lane
   return r;
 }
 
+// scale4-v2 form of glu_gather: a row's cw groups are cw / 2 index bytes, so
+// with G % 8 == 0, cw % 8 == 0 and kR * cw / 8 <= 64 lane l loads dword l of
+// the unit's kR * cw / 8 (row u = l / (cw / 8)), and the nibble of group
+// c0 + L of row r sits in lane r * cw / 8 + L / 8 at bits 4 (L % 8).
+__device__ __forceinline__ GluGather glu_gather4(int G, int S, int wave, int lane, int kR) {
+  const int cw = (G + S - 1) / S;
+  const int nd = cw >> 3;
+  const int u = min(lane / nd, kR - 1);
+  const int d = lane < kR * nd ? lane % nd : nd - 1;
+  GluGather r;
+  r.off = u * (G >> 1) + min(((wave * cw) >> 1) + 4 * d, (G >> 1) - 4);
+  r.bp = (lane >> 3) << 2;
+  return r;
+}
+
 // Rows r0 .. r0 + kR - 1 of the gate and up matrices of the span at `span`.
-template <typename XT, int kR, bool kG>
-__device__ __forceinline__ void glu_load_rows(GluBatch<XT, kR, kG>& bt, const uint8_t* span,
+template <typename XT, int kR, bool kG, bool kS4>
+__device__ __forceinline__ void glu_load_rows(GluBatch<XT, kR, kG, kS4>& bt, const uint8_t* span,
                                               const Geo& g, int r0, const ColSplit& cs,
                                               const GluGather& gg) {
   const int G = g.hidden >> 5;
   const size_t cp = (size_t)g.hidden >> 1;
   const uint8_t* gp = span + g.w1p + (size_t)r0 * cp + (size_t)cs.cc * 16;
   const uint8_t* up = span + g.w3p + (size_t)r0 * cp + (size_t)cs.cc * 16;
-  if constexpr (kG) {  // scale dwords first: waiting for them never waits for the data
+  if constexpr (kS4) {  // index dwords first, as below
+    bt.sg[0] = load_u32(span + g.w1s + (size_t)r0 * (G >> 1) + gg.off);
+    bt.su[0] = load_u32(span + g.w3s + (size_t)r0 * (G >> 1) + gg.off);
+  } else if constexpr (kG) {  // scale dwords first: waiting for them never waits for the data
     bt.sg[0] = load_u32(span + g.w1s + (size_t)r0 * G + gg.off);
     bt.su[0] = load_u32(span + g.w3s + (size_t)r0 * G + gg.off);
   }
@@ -366,13 +393,15 @@ __device__ __forceinline__ void glu_load_rows(GluBatch<XT, kR, kG>& bt, const ui
   }
 }
 
-// Pair index pair0 = e * inter + r0 of routed expert e (route registers).
-template <typename XT, int kR, bool kG>
-__device__ __forceinline__ void glu_load(GluBatch<XT, kR, kG>& bt, const RouteRegs& rr,
+// Pair index pair0 = e * inter + r0 of routed expert e (route registers;
+// kS4: rb4 holds lane e's span bases).
+template <typename XT, int kR, bool kG, bool kS4>
+__device__ __forceinline__ void glu_load(GluBatch<XT, kR, kG, kS4>& bt, const RouteRegs& rr,
                                          const Geo& g, int pair0, const ColSplit& cs,
-                                         const GluGather& gg) {
+                                         const GluGather& gg, uint32_t rb4 = 0u) {
   const int e = pair0 / g.inter;
   glu_load_rows(bt, span_of(rr, e), g, pair0 - e * g.inter, cs, gg);
+  if constexpr (kS4) bt.b4 = __builtin_amdgcn_readlane(rb4, e);
 }
 
 // Scale byte of row r for this lane from a gathered dword.
@@ -380,6 +409,23 @@ __device__ __forceinline__ uint32_t gathered_scale(uint32_t word, int bp, int ro
                                                    int lane) {
   const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(bp + r * row_step, (int)word);
   return (w >> (8 * (lane & 3))) & 0xffu;
+}
+
+// scale4-v2: the scale byte base + index of row r for this lane from a
+// gathered index dword (row_step4 = cw / 2 bytes of bpermute address per row).
+__device__ __forceinline__ uint32_t gathered_scale4(uint32_t word, uint32_t base, int bp,
+                                                    int row_step4, int r, int lane) {
+  const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(bp + r * row_step4, (int)word);
+  return base + ((w >> (4 * (lane & 7))) & 0xfu);
+}
+
+// scale4-v2: lane e (< n) gets the bases dword of its expert's span (bytes
+// 64, 65, 66 = w1, w2, w3 bases; byte 67 is zero).
+__device__ __forceinline__ uint32_t route_bases(const RouteRegs& rr, int n, int lane) {
+  if (lane >= n) return 0u;
+  const uint8_t* sp =
+      reinterpret_cast<const uint8_t*>(((uint64_t)rr.hi << 32) | (uint64_t)rr.lo);
+  return load_u32(sp + 64);
 }
 
 __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
@@ -497,7 +543,7 @@ __device__ __forceinline__ void glu_sweep(const RouteRegs& rr, const Geo& g, con
 #endif
 constexpr int kGluMaxThreads = 256 * K3_GLU_GROUPS;
 
-template <typename XT, int kR, bool kG>
+template <typename XT, int kR, bool kG, bool kS4 = false>
 __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute route, const Geo g,
                                                      const XT* __restrict__ x,
                                                      float* __restrict__ h, int n_units,
@@ -516,8 +562,10 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
   const int grp = wave / S;
   const int gw = wave - grp * S;  // wave within its group
   const ColSplit cs = col_split(g.hidden >> 5, S, gw, lane);
-  const GluGather gg = glu_gather(g.hidden >> 5, S, gw, lane, kR);
-  const int row_step = ((g.hidden >> 5) + S - 1) / S;  // cw: bpermute bytes per row
+  const GluGather gg = kS4 ? glu_gather4(g.hidden >> 5, S, gw, lane, kR)
+                           : glu_gather(g.hidden >> 5, S, gw, lane, kR);
+  // cw (scale4-v2: cw / 2): bpermute bytes per row
+  const int row_step = (((g.hidden >> 5) + S - 1) / S) >> (kS4 ? 1 : 0);
   XChunk<XT> xc;
   load_x_chunk<XT>(xc, x, cs);
   RouteRegs rr;
@@ -544,6 +592,7 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
   } else {
     rr = route_regs(route, lane);
   }
+  const uint32_t rb4 = kS4 ? route_bases(rr, route.n, lane) : 0u;
   // Unit pipelines: global pipeline index q = blockIdx.x * groups + grp takes
   // units q, q + Q, q + 2Q, ... (Q = pipelines in the grid).  Every pipeline
   // of the grid runs the same number of iterations (the host sizes the grid
@@ -557,13 +606,18 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
     const int u = q0 + it * Q;
     return (u < n_units ? u : 0) * kR;
   };
-  auto finish = [&](const GluBatch<XT, kR, kG>& bt, int it) {
+  auto finish = [&](const GluBatch<XT, kR, kG, kS4>& bt, int it) {
     const int u = q0 + it * Q;
     const int parity = it & 1;
     float v[N];
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
-      if constexpr (kG) {
+      if constexpr (kS4) {  // w1 base in byte 0 of the bases, w3 base in byte 2
+        v[r] = xc.dot(bt.wg[r]) *
+               e8m0_scale(gathered_scale4(bt.sg[0], bt.b4 & 0xffu, gg.bp, row_step, r, lane));
+        v[kR + r] = xc.dot(bt.wu[r]) * e8m0_scale(gathered_scale4(bt.su[0], (bt.b4 >> 16) & 0xffu,
+                                                                  gg.bp, row_step, r, lane));
+      } else if constexpr (kG) {
         v[r] = xc.dot(bt.wg[r]) * e8m0_scale(gathered_scale(bt.sg[0], gg.bp, row_step, r, lane));
         v[kR + r] =
             xc.dot(bt.wu[r]) * e8m0_scale(gathered_scale(bt.su[0], gg.bp, row_step, r, lane));
@@ -586,22 +640,22 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
     }
   };
   // Two units in flight: unit it + 1 is requested before unit it is reduced.
-  GluBatch<XT, kR, kG> A, B;
-  glu_load(A, rr, g, unit_pair0(0), cs, gg);
-  glu_load(B, rr, g, unit_pair0(min(1, iters - 1)), cs, gg);
+  GluBatch<XT, kR, kG, kS4> A, B;
+  glu_load(A, rr, g, unit_pair0(0), cs, gg, rb4);
+  glu_load(B, rr, g, unit_pair0(min(1, iters - 1)), cs, gg, rb4);
   for (int it = 0;; it += 2) {
     finish(A, it);
     if (it + 2 >= iters) {
       if (it + 1 < iters) finish(B, it + 1);
       break;
     }
-    glu_load(A, rr, g, unit_pair0(it + 2), cs, gg);
+    glu_load(A, rr, g, unit_pair0(it + 2), cs, gg, rb4);
     finish(B, it + 1);
     if (it + 3 >= iters) {
       finish(A, it + 2);
       break;
     }
-    glu_load(B, rr, g, unit_pair0(it + 3), cs, gg);
+    glu_load(B, rr, g, unit_pair0(it + 3), cs, gg, rb4);
   }
 }
 
@@ -620,9 +674,14 @@ struct DownBatch {
   uint32_t s[kG ? 1 : kB][CPL];
 };
 
-template <int CPL, int kB, bool kG, bool kRs = false>
+// kS4 (scale4-v2, byte-scale path only): s[u][c] receives the index byte that
+// holds the nibble of group cc[c] of row r (flattened index r * GB + cc[c];
+// GB is even, so the nibble is the high one exactly when cc[c] is odd), and
+// down_dots turns it into base + index.
+template <int CPL, int kB, bool kG, bool kRs = false, bool kS4 = false>
 __device__ __forceinline__ void down_load(DownBatch<CPL, kB, kG>& bt, const uint8_t* span,
                                           const Geo& g, const int* cc, int r0, int nrows) {
+  static_assert(!kS4 || !kG, "scale4-v2 down loads use the byte-scale path");
   const int GB = g.inter >> 5;
   const size_t cpb = (size_t)g.inter >> 1;
   const uint8_t* dp = span + g.w2p;
@@ -659,7 +718,10 @@ __device__ __forceinline__ void down_load(DownBatch<CPL, kB, kG>& bt, const uint
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {
         bt.w[u][c] = load_chunk(dp + (size_t)r * cpb + (size_t)cc[c] * 16);
-        bt.s[u][c] = load_scale(ds + (size_t)r * GB + cc[c]);
+        if constexpr (kS4)
+          bt.s[u][c] = load_scale(ds + (((size_t)r * GB + cc[c]) >> 1));
+        else
+          bt.s[u][c] = load_scale(ds + (size_t)r * GB + cc[c]);
       }
     }
   }
@@ -712,13 +774,25 @@ __device__ __forceinline__ void h_slice_transpose(XChunk<float>& hs, const float
   }
 }
 
-template <int CPL, int kB, bool kG>
+// kS4: base is the expert's w2 base and shift4[c] the nibble position of
+// chunk cc[c] (4 when cc[c] is odd).
+template <int CPL, int kB, bool kG, bool kS4 = false>
 __device__ __forceinline__ float down_dots(const DownBatch<CPL, kB, kG>& bt,
-                                           const XChunk<float>* hs, int lane) {
+                                           const XChunk<float>* hs, int lane,
+                                           uint32_t base = 0u, const int* shift4 = nullptr) {
   float v[kB];
 #pragma unroll
   for (int u = 0; u < kB; ++u) {
-    if constexpr (kG) {
+    if constexpr (kS4) {
+      float a = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const uint32_t sc = base + ((bt.s[u][c] >> shift4[c]) & 0xfu);
+        a = c == 0 ? hs[0].dot(bt.w[u][0]) * e8m0_scale(sc)
+                   : a + hs[c].dot(bt.w[u][c]) * e8m0_scale(sc);
+      }
+      v[u] = a;
+    } else if constexpr (kG) {
       const uint32_t word =
           (uint32_t)__builtin_amdgcn_ds_bpermute((16 * u + (lane >> 2)) << 2, (int)bt.s[0][0]);
       v[u] = hs[0].dot(bt.w[u][0]) * e8m0_scale((word >> (8 * (lane & 3))) & 0xffu);
@@ -751,7 +825,7 @@ constexpr int down_max_threads() {
   return CPLB <= 1 ? K3_DOWN_THREADS : 512;
 }
 
-template <typename OT, int CPLB, int kB>
+template <typename OT, int CPLB, int kB, bool kS4 = false>
 __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
     const TokenRoute route, const Geo g, const float* __restrict__ h, OT* __restrict__ out) {
   constexpr int L = log2c<kB>();
@@ -765,47 +839,51 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
   const int GB = g.inter >> 5;
   int cc[CPLB];
   bool valid[CPLB];
+  int shift4[CPLB];  // scale4-v2: nibble position of chunk cc[c]
 #pragma unroll
   for (int c = 0; c < CPLB; ++c) {
     valid[c] = lane + 64 * c < GB;
     cc[c] = min(lane + 64 * c, GB - 1);
+    shift4[c] = (cc[c] & 1) * 4;
   }
   // First output row of this workgroup's local batch i, and its row count.
   auto row_of = [&](int i) { return (i * G + (int)blockIdx.x) * kB; };
   auto rows_in = [&](int i) { return min(kB, g.hidden - row_of(i)); };
   const RouteRegs rreg = route_regs(route, lane);
+  const uint32_t rb4 = kS4 ? route_bases(rreg, route.n, lane) : 0u;
   const int idx = lane >> (6 - L);
   const bool writer = (lane & ((1 << (6 - L)) - 1)) == 0;
   for (int e = wave; e < route.n; e += nw) {
     const uint8_t* span = span_of(rreg, e);
+    const uint32_t base = kS4 ? (__builtin_amdgcn_readlane(rb4, e) >> 8) & 0xffu : 0u;
     // Two batches in flight: batch b + 1 is requested before batch b is
     // reduced.  Loads are unconditional inside the loop (the loop exits
     // instead), so the compiler's wait counts stay partial.
     XChunk<float> hs[CPLB];
     load_h_slice<CPLB>(hs, h + (size_t)e * g.inter, cc, valid);
     DownBatch<CPLB, kB> A, B;
-    down_load(A, span, g, cc, row_of(0), rows_in(0));
+    down_load<CPLB, kB, false, false, kS4>(A, span, g, cc, row_of(0), rows_in(0));
     const int b1 = min(1, nb - 1);
-    down_load(B, span, g, cc, row_of(b1), rows_in(b1));
+    down_load<CPLB, kB, false, false, kS4>(B, span, g, cc, row_of(b1), rows_in(b1));
     for (int b = 0;; b += 2) {
-      const float va = down_dots(A, hs, lane);
+      const float va = down_dots<CPLB, kB, false, kS4>(A, hs, lane, base, shift4);
       if (writer && idx < rows_in(b)) ybuf[e][b * kB + idx] = va;
       if (b + 2 >= nb) {
         if (b + 1 < nb) {
-          const float vb = down_dots(B, hs, lane);
+          const float vb = down_dots<CPLB, kB, false, kS4>(B, hs, lane, base, shift4);
           if (writer && idx < rows_in(b + 1)) ybuf[e][(b + 1) * kB + idx] = vb;
         }
         break;
       }
-      down_load(A, span, g, cc, row_of(b + 2), rows_in(b + 2));
-      const float vb = down_dots(B, hs, lane);
+      down_load<CPLB, kB, false, false, kS4>(A, span, g, cc, row_of(b + 2), rows_in(b + 2));
+      const float vb = down_dots<CPLB, kB, false, kS4>(B, hs, lane, base, shift4);
       if (writer && idx < rows_in(b + 1)) ybuf[e][(b + 1) * kB + idx] = vb;
       if (b + 3 >= nb) {
-        const float va2 = down_dots(A, hs, lane);
+        const float va2 = down_dots<CPLB, kB, false, kS4>(A, hs, lane, base, shift4);
         if (writer && idx < rows_in(b + 2)) ybuf[e][(b + 2) * kB + idx] = va2;
         break;
       }
-      down_load(B, span, g, cc, row_of(b + 3), rows_in(b + 3));
+      down_load<CPLB, kB, false, false, kS4>(B, span, g, cc, row_of(b + 3), rows_in(b + 3));
     }
   }
   __syncthreads();
@@ -1996,6 +2074,16 @@ int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, floa
   const int grid = std::max(1, std::min(cus, (n_units + groups - 1) / groups));
   const int cw = (G + S - 1) / S;
   const bool gather = kRowsGlu == 4 && G % 4 == 0 && cw % 4 == 0 && kRowsGlu * cw <= 256;
+  if (g.layout == K3_LAYOUT_SCALE4_V2) {
+    // Index dwords gathered per unit: whole bytes per wave and row, dword
+    // aligned, at most one dword per lane.
+    if (!(kRowsGlu == 4 && G % 8 == 0 && cw % 8 == 0 && kRowsGlu * (cw / 8) <= 64))
+      return fail(K3_HIP_E_CAPABILITY, "scale4-v2: hidden %d is not supported", g.hidden);
+    TimedLaunch tl(KC_GLU_DECODE, st);
+    launch_timed(tl, (k_glu_decode<XT, kRowsGlu, true, true>), dim3(grid), dim3(64 * S * groups),
+                 (unsigned)lds, st, route, g, x, h, n_units, S);
+    return launched(tl, "decode gate/up launch");
+  }
   TimedLaunch tl(KC_GLU_DECODE, st);
   if (gather)
     launch_timed(tl, (k_glu_decode<XT, kRowsGlu, true>), dim3(grid), dim3(64 * S * groups),
@@ -2006,7 +2094,7 @@ int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, floa
   return launched(tl, "decode gate/up launch");
 }
 
-template <typename OT, int CPL, int kB>
+template <typename OT, int CPL, int kB, bool kS4 = false>
 int down_blocks_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
                        hipStream_t st) {
   // One workgroup per CU, more when a workgroup's batches would overflow its
@@ -2020,8 +2108,8 @@ int down_blocks_launch(const Geo& g, const TokenRoute& route, const float* h, OT
   const int max_waves = down_max_threads<CPL>() / 64;
   const int nw = std::min(route.n, max_waves);
   TimedLaunch tl(KC_DOWN_DECODE, st);
-  launch_timed(tl, (k_down_blocks<OT, CPL, kB>), dim3(blocks), dim3(64 * nw), 0, st, route, g, h,
-               out);
+  launch_timed(tl, (k_down_blocks<OT, CPL, kB, kS4>), dim3(blocks), dim3(64 * nw), 0, st, route, g,
+               h, out);
   return launched(tl, "decode down/combine launch");
 }
 
@@ -2063,6 +2151,11 @@ template <typename OT>
 int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace& ws, OT* out,
                          hipStream_t st) {
   const int GB = g.inter / 32;
+  if (g.layout == K3_LAYOUT_SCALE4_V2) {
+    // The format is defined for K3 only (96 groups per down row).
+    if (GB != 96) return fail(K3_HIP_E_CAPABILITY, "scale4-v2: intermediate %d is not supported", g.inter);
+    return down_blocks_launch<OT, 2, 2, true>(g, route, ws.h, out, st);
+  }
   if (GB == 64 && route.n <= 16) return down_g64_dispatch<OT>(g, route, ws.h, out, st);
   switch ((GB + 63) / 64) {
     case 1: return down_blocks_launch<OT, 1, kDownBlocksBatch>(g, route, ws.h, out, st);

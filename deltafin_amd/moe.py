@@ -192,13 +192,14 @@ def moe_verify(g: K3HipGeometryV1, edge_experts: Sequence[int | torch.Tensor],
 
 
 # ----------------------------------------------------------------- surface 1
-def _descs(blobs: Sequence[np.ndarray | torch.Tensor | int], span: int):
+def _descs(blobs: Sequence[np.ndarray | torch.Tensor | int], span: int,
+           layout: int = _lib.K3_LAYOUT_RAW_V1):
     arr = (K3HipExpertDescriptorV1 * max(len(blobs), 1))()
     for i, b in enumerate(blobs):
         d = arr[i]
         d.abi_version = _lib.K3_DESCRIPTOR_ABI_V1
         d.struct_bytes = C.sizeof(K3HipExpertDescriptorV1)
-        d.layout_id = _lib.K3_LAYOUT_RAW_V1
+        d.layout_id = layout
         d.reserved = 0
         d.blob_bytes = span
         if isinstance(b, np.ndarray):
@@ -210,22 +211,29 @@ def _descs(blobs: Sequence[np.ndarray | torch.Tensor | int], span: int):
     return arr
 
 
-def moe_layer_desc(blobs: Sequence, weights: Sequence[float], x: np.ndarray) -> np.ndarray:
-    """Host-synchronous descriptor call (surface 1); x fp32 [hidden] on host."""
+def _layout_span(layout: int, raw_span: int) -> int:
+    return _lib.K3_SCALE4_V2_EXPERT_SPAN if layout == _lib.K3_LAYOUT_SCALE4_V2 else raw_span
+
+
+def moe_layer_desc(blobs: Sequence, weights: Sequence[float], x: np.ndarray,
+                   layout: int = _lib.K3_LAYOUT_RAW_V1) -> np.ndarray:
+    """Host-synchronous descriptor call (surface 1); x fp32 [hidden] on host;
+    every blob in `layout` (raw-v1, or scale4-v2 at the K3 geometry)."""
     lib = load()
     h, i, span = C.c_int(), C.c_int(), C.c_longlong()
     lib.k3_hip_shapes(C.byref(h), C.byref(i), C.byref(span))
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty(h.value, dtype=np.float32)
     w = np.ascontiguousarray(weights, dtype=np.float32)
-    rc = lib.k3_hip_moe_layer_desc_v1(_descs(blobs, span.value), len(blobs), w.ctypes.data,
-                                      x.ctypes.data, out.ctypes.data)
+    rc = lib.k3_hip_moe_layer_desc_v1(_descs(blobs, _layout_span(layout, span.value), layout),
+                                      len(blobs), w.ctypes.data, x.ctypes.data, out.ctypes.data)
     check(rc, "k3_hip_moe_layer_desc_v1")
     return out
 
 
 def moe_positions_desc(blobs: Sequence, position_offsets: Sequence[int],
-                       weights: Sequence[float], x: np.ndarray) -> np.ndarray:
+                       weights: Sequence[float], x: np.ndarray,
+                       layout: int = _lib.K3_LAYOUT_RAW_V1) -> np.ndarray:
     lib = load()
     h, i, span = C.c_int(), C.c_int(), C.c_longlong()
     lib.k3_hip_shapes(C.byref(h), C.byref(i), C.byref(span))
@@ -234,8 +242,9 @@ def moe_positions_desc(blobs: Sequence, position_offsets: Sequence[int],
     out = np.empty((m, h.value), dtype=np.float32)
     w = np.ascontiguousarray(weights, dtype=np.float32)
     offs = np.ascontiguousarray(position_offsets, dtype=np.int32)
-    rc = lib.k3_hip_moe_positions_desc_v1(_descs(blobs, span.value), len(blobs), offs.ctypes.data,
-                                          m, w.ctypes.data, x.ctypes.data, out.ctypes.data)
+    rc = lib.k3_hip_moe_positions_desc_v1(_descs(blobs, _layout_span(layout, span.value), layout),
+                                          len(blobs), offs.ctypes.data, m, w.ctypes.data,
+                                          x.ctypes.data, out.ctypes.data)
     check(rc, "k3_hip_moe_positions_desc_v1")
     return out
 

@@ -71,11 +71,15 @@ enum { K3_DTYPE_F32 = 0, K3_DTYPE_BF16 = 1 };
 
 /* Expert descriptor: byte-for-byte the layout of K3MetalExpertDescriptorV1
  * (tools/metal_moe_abi.h:35-50), so a caller's descriptor arrays pass through
- * unchanged.  blob_bytes must equal the configured geometry's span. */
+ * unchanged.  blob_bytes must equal the span of the descriptor's layout at
+ * the configured geometry (raw-v1: k3_hip_geometry_span; scale4-v2:
+ * K3_SCALE4_V2_EXPERT_SPAN, an 8192-byte header then w1 packed, w1 4-bit
+ * scale indices, w2 packed, w2 indices, w3 packed, w3 indices). */
 typedef struct K3HipExpertDescriptorV1 {
   uint32_t abi_version;  /* K3_DESCRIPTOR_ABI_V1 */
   uint32_t struct_bytes; /* sizeof(K3HipExpertDescriptorV1) == 32 */
-  uint32_t layout_id;    /* K3_LAYOUT_RAW_V1 */
+  uint32_t layout_id;    /* K3_LAYOUT_RAW_V1, or K3_LAYOUT_SCALE4_V2 (K3 only;
+                            every descriptor of a call has the same layout) */
   uint32_t reserved;     /* 0 */
   uint64_t blob_bytes;
   const uint8_t* blob;   /* host or device pointer */
@@ -121,8 +125,16 @@ int k3_hip_init(const char* selector);
 int k3_hip_available(void);
 /* Replaces k3_metal_descriptor_abi_version (tools/metal_moe_abi.h:56). */
 uint32_t k3_hip_descriptor_abi_version(void);
-/* Replaces k3_metal_layout_capabilities (tools/metal_moe_abi.h:57). */
+/* Replaces k3_metal_layout_capabilities (tools/metal_moe_abi.h:57):
+ * K3_CAP_RAW_V1, plus K3_CAP_SCALE4_V2 while the surface-1 geometry is K3
+ * (the scale4-v2 format is defined for K3 only, tools/metal_moe.mm:127-155). */
 uint64_t k3_hip_layout_capabilities(void);
+/* The header checks surface 1 applies to every scale4-v2 descriptor
+ * (validate_scale4_header, tools/metal_moe.mm:353-405) on a header in host
+ * memory: 0, K3_HIP_E_INVALID (fewer than 8192 bytes) or K3_HIP_E_DESCRIPTOR
+ * with the reason in k3_hip_last_error().  No separate reference entry point:
+ * the reference runs these checks inside its descriptor calls. */
+int k3_hip_scale4_check_header(const uint8_t* header, uint64_t bytes);
 /* Sets the geometry used by surface 1 (default preset 1, K3).  Drops every
  * cached blob.  No reference counterpart: the Metal bridge fixes K3. */
 int k3_hip_configure_v1(const K3HipGeometryV1* geometry);

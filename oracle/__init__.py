@@ -49,6 +49,7 @@ _ref = None
 _u8p = C.POINTER(C.c_uint8)
 _f32p = C.POINTER(C.c_float)
 _f64p = C.POINTER(C.c_double)
+_u32p = C.POINTER(C.c_uint32)
 _i32p = C.POINTER(C.c_int)
 
 
@@ -78,6 +79,11 @@ def orc() -> C.CDLL:
                                           C.c_int, _f64p, _f64p, _f64p]
         lib.orc_topk_softmax.restype = C.c_int
         lib.orc_topk_softmax.argtypes = [_f32p, C.c_int, C.c_int, _i32p, _f64p]
+        for name in ("orc_scale4_pack", "orc_scale4_unpack"):
+            getattr(lib, name).restype = C.c_int
+            getattr(lib, name).argtypes = [_u8p, C.c_uint64, C.c_int, _u8p]
+        lib.orc_scale4_header.restype = C.c_int
+        lib.orc_scale4_header.argtypes = [_u8p, _u8p, _u8p]
         lib.orc_rand_u64.restype = C.c_uint64
         lib.orc_rand_u64.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64]
         lib.orc_synth_mxfp4.argtypes = [C.c_uint64, C.c_uint64, _u8p, C.c_uint64, _u8p,
@@ -104,6 +110,8 @@ def ref() -> C.CDLL:
             getattr(lib, name).argtypes = [_u8p, _u8p, _f32p, _f32p, C.c_int, C.c_int]
         for name in ("mxfp4_gemv_mt", "mxfp4_gemv_mt_compat"):
             getattr(lib, name).argtypes = [_u8p, _u8p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        lib.mxfp4_gemv_mt_scale4.argtypes = [_u8p, _u8p, _u32p, _f32p, _f32p, C.c_int, C.c_int,
+                                             C.c_int]
         lib.mxfp4_have_avx2.restype = C.c_int
         lib.mxfp4_cpu_compatible.restype = C.c_int
         lib.mxfp4_pool_init.restype = C.c_int
@@ -283,3 +291,87 @@ def plain_max_rel(y, ref_y, floor: float = 1e-6) -> float:
     y = np.asarray(y, dtype=np.float64)
     r = np.asarray(ref_y, dtype=np.float64)
     return float(np.max(np.abs(y - r) / np.maximum(np.abs(r), floor)))
+
+
+# ------------------------------------------------------------------ scale4-v2
+# K3 geometry constants of the format (native/deltafin/src/expert_scale4.rs:17-63).
+SCALE4_HEADER_BYTES = 8192
+SCALE4_SPAN = 17_039_360
+SCALE4_K3 = (3584, 3072)
+
+
+def scale4_pack(values, base: int | None = None) -> tuple[int, np.ndarray]:
+    """(base, packed) of a scale plane; base defaults to the plane's minimum
+    (expert_scale4.rs:114-148).  Raises ValueError when it does not fit."""
+    v = _u8(values)
+    b = int(v.min()) if base is None else int(base)
+    out = np.empty((v.size + 1) // 2, dtype=np.uint8)
+    if orc().orc_scale4_pack(_p(v, _u8p), v.size, b, _p(out, _u8p)) != 0:
+        raise ValueError(f"scale plane does not fit base {b} plus a 4-bit index")
+    return b, out
+
+
+def scale4_unpack(packed, base: int, n: int) -> np.ndarray:
+    pk = _u8(packed)
+    if pk.size != (n + 1) // 2:
+        raise ValueError("packed length does not match the value count")
+    out = np.empty(n, dtype=np.uint8)
+    if orc().orc_scale4_unpack(_p(pk, _u8p), n, int(base), _p(out, _u8p)) != 0:
+        raise ValueError(f"base {base} exceeds 240")
+    return out
+
+
+def scale4_header(digest: bytes, bases) -> np.ndarray:
+    d = _u8(np.frombuffer(bytes(digest), dtype=np.uint8))
+    b = _u8(bases)
+    if d.size != 32 or b.size != 3:
+        raise ValueError("digest is 32 bytes and bases 3")
+    out = np.empty(SCALE4_HEADER_BYTES, dtype=np.uint8)
+    if orc().orc_scale4_header(_p(d, _u8p), _p(b, _u8p), _p(out, _u8p)) != 0:
+        raise ValueError("a base exceeds 240")
+    return out
+
+
+def scale4_span(raw_span, digest: bytes = bytes(32)) -> np.ndarray:
+    """The assembled scale4-v2 span of a raw-v1 K3 span: header, then w1
+    packed, w1 indices, w2 packed, w2 indices, w3 packed, w3 indices, each
+    matrix's base the minimum of its scale plane (tools/metal_moe.mm:127-155)."""
+    raw = _u8(raw_span)
+    off = expert_offsets(*SCALE4_K3)
+    if raw.size != off[6]:
+        raise ValueError("not a raw-v1 K3 span")
+    bases, parts = [], []
+    for m in range(3):
+        p0, s0, s1 = off[2 * m], off[2 * m + 1], off[2 * m + 2]
+        b, pk = scale4_pack(raw[s0:s1])
+        bases.append(b)
+        parts += [raw[p0:s0], pk]
+    return np.concatenate([scale4_header(digest, bases)] + parts)
+
+
+def scale4_to_raw(span4) -> np.ndarray:
+    """Inverse of scale4_span (the indices expanded to E8M0 bytes)."""
+    s4 = _u8(span4)
+    off = expert_offsets(*SCALE4_K3)
+    bases = [int(s4[64 + m]) for m in range(3)]
+    parts, pos = [], SCALE4_HEADER_BYTES
+    for m in range(3):
+        n_packed = off[2 * m + 1] - off[2 * m]
+        n_scales = off[2 * m + 2] - off[2 * m + 1]
+        parts.append(s4[pos:pos + n_packed])
+        pos += n_packed
+        parts.append(scale4_unpack(s4[pos:pos + (n_scales + 1) // 2], bases[m], n_scales))
+        pos += (n_scales + 1) // 2
+    return np.concatenate(parts)
+
+
+def ref_gemv_scale4(packed, scales4, base: int, x, rows: int, cols: int, threads: int = 1):
+    """The reference's mxfp4_gemv_mt_scale4 (tools/fused_gemv.c:1059-1071) with
+    the 16-entry table of E8M0 float bits (base + d) << 23."""
+    lib = ref()
+    table = np.array([(base + d) << 23 for d in range(16)], dtype=np.uint32)
+    xs = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    lib.mxfp4_gemv_mt_scale4(_p(_u8(packed), _u8p), _p(_u8(scales4), _u8p), _p(table, _u32p),
+                             _p(xs, _f32p), _p(y, _f32p), rows, cols, threads)
+    return y

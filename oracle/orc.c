@@ -241,3 +241,59 @@ void orc_synth_expert(uint64_t seed, uint64_t expert, int hidden, int inter,
     orc_synth_mxfp4(seed, 3 * expert + 2, span + off[4], w13p, span + off[5], w13s,
                     scale_lo, scale_hi);
 }
+
+/* ------------------------------------------------------------ scale4-v2 */
+int orc_scale4_pack(const uint8_t *values, uint64_t n, int base, uint8_t *packed) {
+    if (base < 0 || base > 240) return -1;
+    for (uint64_t i = 0; i < (n + 1) / 2; i++) packed[i] = 0;
+    for (uint64_t i = 0; i < n; i++) {
+        const int d = (int)values[i] - base;
+        if (d < 0 || d > 15) return -1;
+        packed[i / 2] |= (uint8_t)(d << ((i & 1) * 4));
+    }
+    return 0;
+}
+
+int orc_scale4_unpack(const uint8_t *packed, uint64_t n, int base, uint8_t *values) {
+    if (base < 0 || base > 240) return -1;
+    for (uint64_t i = 0; i < n; i++)
+        values[i] = (uint8_t)(base + ((packed[i / 2] >> ((i & 1) * 4)) & 0x0F));
+    return 0;
+}
+
+static void put32(uint8_t *p, uint32_t v) {
+    for (int i = 0; i < 4; i++) p[i] = (uint8_t)(v >> (8 * i));
+}
+
+int orc_scale4_header(const uint8_t *digest32, const uint8_t *bases3, uint8_t *header) {
+    /* K3: packed planes 3072 x 3584 / 2 bytes, index planes half a byte per
+     * 32-element group. */
+    const uint32_t hdr = 8192, packed = 5505024, s4 = 344064 / 2;
+    for (int m = 0; m < 3; m++)
+        if (bases3[m] > 240) return -1;
+    for (int i = 0; i < 8192; i++) header[i] = 0;
+    memcpy(header, "K3SC4V2", 8);  /* the terminating zero is the 8th byte */
+    put32(header + 8, 2);
+    put32(header + 12, hdr);
+    put32(header + 16, hdr + 3 * (packed + s4));
+    put32(header + 24, 3 * (packed + 344064));
+    memcpy(header + 32, digest32, 32);
+    memcpy(header + 64, bases3, 3);
+    uint32_t off = hdr;
+    for (int m = 0; m < 3; m++) {
+        put32(header + 72 + 16 * m, off);
+        put32(header + 76 + 16 * m, packed);
+        off += packed;
+        put32(header + 80 + 16 * m, off);
+        put32(header + 84 + 16 * m, s4);
+        off += s4;
+    }
+    for (int m = 0; m < 3; m++)
+        for (uint32_t d = 0; d < 16; d++)
+            put32(header + 128 + 64 * m + 4 * d, ((uint32_t)bases3[m] + d) << 23);
+    for (int m = 0; m < 3; m++) {
+        put32(header + 320 + 8 * m, hdr + m * s4);
+        put32(header + 324 + 8 * m, s4);
+    }
+    return 0;
+}

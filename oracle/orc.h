@@ -79,6 +79,18 @@ void orc_synth_mxfp4(uint64_t seed, uint64_t stream, uint8_t *packed,
 void orc_synth_expert(uint64_t seed, uint64_t expert, int hidden, int inter,
                       uint8_t *span, int scale_lo, int scale_hi);
 
+/* scale4-v2 codec (native/deltafin/src/expert_scale4.rs:114-171): entry i of
+ * a scale plane is the 4-bit index value - base, in byte i/2, low nibble for
+ * even i.  pack returns -1 when base > 240 or a value lies outside
+ * [base, base + 15]; unpack returns -1 when base > 240. */
+int orc_scale4_pack(const uint8_t *values, uint64_t n, int base, uint8_t *packed);
+int orc_scale4_unpack(const uint8_t *packed, uint64_t n, int base, uint8_t *values);
+/* The 8192-byte scale4-v2 header for the K3 geometry (expert_scale4.rs:173-208):
+ * identity and lengths, the 32-byte source digest, the three bases, the
+ * in-memory payload table, the exponent tables (base + d) << 23 at 128 / 192 /
+ * 256 and the on-disk sidecar table at 320.  -1 when a base exceeds 240. */
+int orc_scale4_header(const uint8_t *digest32, const uint8_t *bases3, uint8_t *header);
+
 #ifdef __cplusplus
 }
 #endif
