@@ -127,6 +127,8 @@ SIGNATURES = {
     "k3_hip_cache_release": (None, [_vp, _u64]),
     "k3_hip_cache_stats": (None, [_vp, C.POINTER(C.c_longlong)]),
     "k3_hip_cache_read_back": (_i32, [_vp, _i32, C.c_uint16, _vp, _u64]),
+    "k3_hip_cache_state": (_i32, [_vp, C.c_char_p, _u64]),
+    "k3_hip_cache_poison": (None, [_vp, C.c_char_p]),
     "k3_hip_timing_begin": (_i32, [_i32]),
     "k3_hip_timing_end": (_i32, [C.POINTER(K3HipKernelTimingV1), _i32, C.POINTER(_i32),
                                  C.POINTER(C.c_longlong)]),

@@ -17,12 +17,20 @@
 //   still be read by kernels the caller queued before release(): release()
 //   records a per-slot event on the stream the plan was resolved on, and a
 //   copy into an evicted slot first makes the side stream wait on it.
+// * Qualification and fail-closed state (provider_cuda_moe.cpp:889-953,
+//   :517-533): the first plan runs the reference's device known-answer tests
+//   (:291-420) on the cache's stream.  A mismatch disables the cache
+//   (K3_HIP_E_CAPABILITY: the caller takes its CPU path); a HIP error, or a
+//   caller's k3_hip_cache_poison, makes it terminal (K3_HIP_E_EXEC).  Either
+//   way every resident entry is dropped and later calls fail with the reason.
 #include <hip/hip_runtime_api.h>
+#include <math.h>
 #include <string.h>
 
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <string>
 #include <unordered_map>
 #include <vector>
 
@@ -67,6 +75,9 @@ struct K3HipCache {
   std::vector<bool> staging_used;
   int staging_cursor = 0;
   long long hits = 0, misses = 0, evictions = 0, uploaded = 0;
+  enum State { kUnqualified = 0, kEnabled = 1, kDisabled = 2, kTerminal = 3 };
+  int state = kUnqualified;
+  std::string reason = "not yet qualified";
 
   int resident() const {
     int n = 0;
@@ -97,6 +108,159 @@ int take_slot(K3HipCache* c) {
     ++c->evictions;
   }
   return victim;
+}
+
+// ------------------------------------------------------------ qualification
+float e2m1_value(uint8_t code) {
+  static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  return (code & 8) ? -mag[code & 7] : mag[code & 7];
+}
+
+// The reference's two device known-answer tests (provider_cuda_moe.cpp:291-420)
+// through this library's own entry points, on `st`: every E2M1 code across two
+// generated GEMV rows at two batches (within 2e-4 of a sequential fma sum),
+// and a K3 expert with one nonzero per matrix through the single-expert
+// launch (out[0] = SiTU(x0, 2 x0), within 2e-5).  Each runs twice and the two
+// outputs must match bit for bit.  0 = pass, 1 = mismatch, -1 = HIP error;
+// *why names the failure.
+int known_answer_tests(hipStream_t st, std::string* why) {
+  uint8_t packed[32];
+  for (int i = 0; i < 16; ++i) {
+    const int ph = (2 * i) % 16;
+    packed[i] = (uint8_t)(ph | (((ph + 1) % 16) << 4));
+    packed[16 + i] = (uint8_t)((15 - ph) | ((14 - ph) << 4));
+  }
+  const uint8_t scales[2] = {127, 126};
+  float x[64];
+  for (int c = 0; c < 32; ++c) {
+    x[c] = (float)c / 32.0f;
+    x[32 + c] = ((float)c - 15.0f) / 17.0f;
+  }
+  float want[4];
+  for (int b = 0; b < 2; ++b)
+    for (int r = 0; r < 2; ++r) {
+      float t = 0.0f;
+      for (int c = 0; c < 32; ++c) {
+        const uint8_t byte = packed[r * 16 + c / 2];
+        const uint8_t code = (c & 1) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 15);
+        t = fmaf(ldexpf(e2m1_value(code), (int)scales[r] - 127), x[b * 32 + c], t);
+      }
+      want[b * 2 + r] = t;
+    }
+  K3HipGeometryV1 gd;
+  k3_hip_geometry_preset(1, &gd);  // K3: hidden 3584, intermediate 3072, SiTU
+  const int H = (int)gd.hidden, I = (int)gd.intermediate;
+  const uint64_t P = (uint64_t)H * I / 2, S = (uint64_t)I * (H / 32);
+  uint8_t *dp = nullptr, *ds = nullptr, *span = nullptr;
+  float *dx = nullptr, *o1 = nullptr, *o2 = nullptr, *mx = nullptr, *gate = nullptr,
+        *up = nullptr, *m1 = nullptr, *m2 = nullptr;
+  std::vector<float> h1(2 * (size_t)H), h2(2 * (size_t)H), mxh(2 * (size_t)H, 0.0f);
+  float g1[4], g2[4];
+  int result = 0;
+  hipError_t e = hipSuccess;
+  auto ok = [&](hipError_t v) { return (e = v) == hipSuccess; };
+  if (ok(hipMalloc(reinterpret_cast<void**>(&dp), 32)) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&ds), 2)) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&dx), sizeof(x))) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&o1), 16)) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&o2), 16)) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&span), gd.expert_span)) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&mx), 2 * (size_t)H * 4)) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&gate), 2 * (size_t)I * 4)) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&up), 2 * (size_t)I * 4)) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&m1), 2 * (size_t)H * 4)) &&
+      ok(hipMalloc(reinterpret_cast<void**>(&m2), 2 * (size_t)H * 4)) &&
+      ok(hipMemcpyAsync(dp, packed, 32, hipMemcpyHostToDevice, st)) &&
+      ok(hipMemcpyAsync(ds, scales, 2, hipMemcpyHostToDevice, st)) &&
+      ok(hipMemcpyAsync(dx, x, sizeof(x), hipMemcpyHostToDevice, st))) {
+    // The one-hot expert: code 2 (1.0) at w1 and w2 element 0, code 4 (2.0)
+    // at w3 element 0, scale 127 (1.0) for their first groups.
+    const uint8_t one = 0x02, two = 0x04, unit = 127;
+    mxh[0] = 1.0f;
+    mxh[(size_t)H] = -0.5f;
+    if (ok(hipMemsetAsync(span, 0, gd.expert_span, st)) &&
+        ok(hipMemcpyAsync(span, &one, 1, hipMemcpyHostToDevice, st)) &&
+        ok(hipMemcpyAsync(span + P, &unit, 1, hipMemcpyHostToDevice, st)) &&
+        ok(hipMemcpyAsync(span + P + S, &one, 1, hipMemcpyHostToDevice, st)) &&
+        ok(hipMemcpyAsync(span + 2 * P + S, &unit, 1, hipMemcpyHostToDevice, st)) &&
+        ok(hipMemcpyAsync(span + 2 * (P + S), &two, 1, hipMemcpyHostToDevice, st)) &&
+        ok(hipMemcpyAsync(span + 3 * P + 2 * S, &unit, 1, hipMemcpyHostToDevice, st)) &&
+        ok(hipMemcpyAsync(mx, mxh.data(), 2 * (size_t)H * 4, hipMemcpyHostToDevice, st))) {
+      int rc = k3_hip_mxfp4_gemv(dp, ds, dx, o1, 2, 32, 2, st);
+      if (rc == K3_HIP_OK) rc = k3_hip_mxfp4_gemv(dp, ds, dx, o2, 2, 32, 2, st);
+      if (rc == K3_HIP_OK) rc = k3_hip_moe_launch(&gd, span, mx, 2, gate, up, m1, st);
+      if (rc == K3_HIP_OK) rc = k3_hip_moe_launch(&gd, span, mx, 2, gate, up, m2, st);
+      if (rc != K3_HIP_OK) {
+        *why = std::string("known-answer launch failed: ") + k3_hip_last_error();
+        result = -1;
+      } else if (ok(hipMemcpyAsync(g1, o1, 16, hipMemcpyDeviceToHost, st)) &&
+                 ok(hipMemcpyAsync(g2, o2, 16, hipMemcpyDeviceToHost, st)) &&
+                 ok(hipMemcpyAsync(h1.data(), m1, 2 * (size_t)H * 4, hipMemcpyDeviceToHost, st)) &&
+                 ok(hipMemcpyAsync(h2.data(), m2, 2 * (size_t)H * 4, hipMemcpyDeviceToHost, st)) &&
+                 ok(hipStreamSynchronize(st))) {
+        float d1 = 0.0f;
+        for (int i = 0; i < 4; ++i) d1 = fmaxf(d1, fabsf(g1[i] - want[i]));
+        float d2 = 0.0f;
+        for (int b = 0; b < 2; ++b) {
+          const float in = b == 0 ? 1.0f : -0.5f, g = in, u = 2.0f * in;
+          const float sit = 4.0f * tanhf(g / 4.0f) / (1.0f + expf(-g)) * (25.0f * tanhf(u / 25.0f));
+          for (int i = 0; i < H; ++i)
+            d2 = fmaxf(d2, fabsf(h1[(size_t)b * H + i] - (i == 0 ? sit : 0.0f)));
+        }
+        if (memcmp(g1, g2, sizeof(g1)) != 0 || !(d1 <= 2.0e-4f)) {
+          *why = "MXFP4 generated-weight known-answer test failed";
+          result = 1;
+        } else if (memcmp(h1.data(), h2.data(), h1.size() * 4) != 0 || !(d2 <= 2.0e-5f)) {
+          *why = "full-expert generated-weight known-answer test failed";
+          result = 1;
+        }
+      }
+    }
+  }
+  if (e != hipSuccess && result == 0) {
+    (void)hipGetLastError();
+    *why = std::string("known-answer test: ") + hipGetErrorString(e);
+    result = -1;
+  }
+  (void)hipStreamSynchronize(st);
+  for (void* q : {(void*)dp, (void*)ds, (void*)dx, (void*)o1, (void*)o2, (void*)span, (void*)mx,
+                  (void*)gate, (void*)up, (void*)m1, (void*)m2})
+    if (q) (void)hipFree(q);
+  return result;
+}
+
+// Fail closed: drop every resident entry and keep the reason.
+void poison_locked(K3HipCache* c, const std::string& why, bool terminal) {
+  c->state = terminal || c->state == K3HipCache::kTerminal ? K3HipCache::kTerminal
+                                                          : K3HipCache::kDisabled;
+  c->reason = why;
+  for (auto& s : c->slots) s.layer = s.id = -1;
+  for (auto& m : c->strata) m.clear();
+}
+
+// The gate every plan / fetch / resolve call passes (qualifies on first use).
+int gate_locked(K3HipCache* c) {
+  if (c->state == K3HipCache::kUnqualified) {
+    std::string why;
+    const int r = known_answer_tests(c->side, &why);
+    if (r == 0) {
+      c->state = K3HipCache::kEnabled;
+      c->reason = "known-answer tests passed";
+    } else {
+      poison_locked(c, why, r < 0);
+    }
+  }
+  if (c->state == K3HipCache::kEnabled) return K3_HIP_OK;
+  return fail(c->state == K3HipCache::kDisabled ? K3_HIP_E_CAPABILITY : K3_HIP_E_EXEC,
+              "expert cache disabled: %s", c->reason.c_str());
+}
+
+// A HIP failure inside a cache call: terminal.
+int runtime_fail_locked(K3HipCache* c, const char* what, hipError_t e) {
+  (void)hipGetLastError();
+  poison_locked(c, std::string(what) + ": " + hipGetErrorString(e), true);
+  return fail(K3_HIP_E_EXEC, "expert cache disabled after runtime failure: %s",
+              c->reason.c_str());
 }
 
 bool pinned_host(const void* p) {
@@ -184,6 +348,9 @@ int k3_hip_cache_plan(K3HipCache* c, uint64_t plan_id, int layer, const uint16_t
       return fail(K3_HIP_E_INVALID, "cache plan: ids must be canonical ascending IDs");
   std::lock_guard<std::mutex> lk(c->mu);
   if (c->plans.count(plan_id)) return fail(K3_HIP_E_INVALID, "cache plan: plan id already live");
+  int rc = set_device(c);
+  if (rc == K3_HIP_OK) rc = gate_locked(c);
+  if (rc != K3_HIP_OK) return rc;
   K3HipCache::Plan p;
   p.layer = layer;
   p.ids.assign(ids, ids + n);
@@ -219,6 +386,7 @@ int k3_hip_cache_fetch(K3HipCache* c, uint64_t plan_id, const uint8_t* const* so
     return fail(K3_HIP_E_INVALID, "cache fetch: %d sources for %zu misses", n_sources,
                 p.missing.size());
   int rc = set_device(c);
+  if (rc == K3_HIP_OK) rc = gate_locked(c);
   if (rc != K3_HIP_OK) return rc;
   for (int i = 0; i < n_sources; ++i) {
     if (!sources[i]) return fail(K3_HIP_E_INVALID, "cache fetch: null source %d", i);
@@ -231,7 +399,7 @@ int k3_hip_cache_fetch(K3HipCache* c, uint64_t plan_id, const uint8_t* const* so
     // expert: the copy waits for the release point of its last plan.
     if (s.has_done) {
       e = hipStreamWaitEvent(c->side, s.done, 0);
-      if (e != hipSuccess) return hip_fail("cache fetch wait for slot reuse", e);
+      if (e != hipSuccess) return runtime_fail_locked(c, "cache fetch wait for slot reuse", e);
     }
     if (pinned_host(sources[i]) || c->staging.empty()) {
       e = hipMemcpyAsync(dst, sources[i], c->span, hipMemcpyHostToDevice, c->side);
@@ -240,7 +408,7 @@ int k3_hip_cache_fetch(K3HipCache* c, uint64_t plan_id, const uint8_t* const* so
       c->staging_cursor = (k + 1) % (int)c->staging.size();
       if (c->staging_used[k]) {
         e = hipEventSynchronize(c->staging_ready[k]);
-        if (e != hipSuccess) return hip_fail("cache staging wait", e);
+        if (e != hipSuccess) return runtime_fail_locked(c, "cache staging wait", e);
       }
       memcpy(c->staging[k], sources[i], c->span);
       e = hipMemcpyAsync(dst, c->staging[k], c->span, hipMemcpyHostToDevice, c->side);
@@ -250,7 +418,7 @@ int k3_hip_cache_fetch(K3HipCache* c, uint64_t plan_id, const uint8_t* const* so
     if (e == hipSuccess) e = hipEventRecord(s.ready, c->side);
     if (e != hipSuccess) {
       (void)hipStreamSynchronize(c->side);
-      return fail(K3_HIP_E_COPY, "cache fetch copy: %s", hipGetErrorString(e));
+      return runtime_fail_locked(c, "cache fetch copy", e);
     }
     s.has_event = true;
     s.layer = p.layer;
@@ -282,6 +450,7 @@ int k3_hip_cache_resolve(K3HipCache* c, uint64_t plan_id, const uint16_t* ids, i
   auto pit = c->plans.find(plan_id);
   if (pit == c->plans.end()) return fail(K3_HIP_E_INVALID, "cache resolve: stale or unknown plan");
   int rc = set_device(c);
+  if (rc == K3_HIP_OK) rc = gate_locked(c);
   if (rc != K3_HIP_OK) return rc;
   pit->second.stream = static_cast<hipStream_t>(stream);
   pit->second.resolved = true;
@@ -292,7 +461,7 @@ int k3_hip_cache_resolve(K3HipCache* c, uint64_t plan_id, const uint16_t* ids, i
     K3HipCache::Slot& s = c->slots[slot];
     if (s.has_event) {
       const hipError_t e = hipStreamWaitEvent(static_cast<hipStream_t>(stream), s.ready, 0);
-      if (e != hipSuccess) return hip_fail("cache resolve wait", e);
+      if (e != hipSuccess) return runtime_fail_locked(c, "cache resolve wait", e);
     }
     device_spans[i] = c->slab + (uint64_t)slot * c->slot_bytes;
   }
@@ -307,6 +476,7 @@ int k3_hip_cache_ready_subset(K3HipCache* c, uint64_t plan_id, const uint16_t* i
   auto pit = c->plans.find(plan_id);
   if (pit == c->plans.end()) return fail(K3_HIP_E_INVALID, "cache ready: stale or unknown plan");
   int rc = set_device(c);
+  if (rc == K3_HIP_OK) rc = gate_locked(c);
   if (rc != K3_HIP_OK) return rc;
   int ready = 0;
   for (int i = 0; i < n; ++i) {
@@ -320,7 +490,7 @@ int k3_hip_cache_ready_subset(K3HipCache* c, uint64_t plan_id, const uint16_t* i
         (void)hipGetLastError();
         continue;
       }
-      if (q != hipSuccess) return hip_fail("cache ready query", q);
+      if (q != hipSuccess) return runtime_fail_locked(c, "cache ready query", q);
     }
     device_spans[i] = c->slab + (uint64_t)slot * c->slot_bytes;
     ++ready;
@@ -351,6 +521,29 @@ void k3_hip_cache_release(K3HipCache* c, uint64_t plan_id) {
   for (int s : p.hit_slots) unpin(s);
   for (int s : p.miss_slots) unpin(s);
   c->plans.erase(pit);
+}
+
+int k3_hip_cache_state(const K3HipCache* c, char* reason, uint64_t reason_capacity) {
+  if (!c) return fail(K3_HIP_E_INVALID, "cache state: null cache");
+  K3HipCache* m = const_cast<K3HipCache*>(c);
+  std::lock_guard<std::mutex> lk(m->mu);
+  if (reason && reason_capacity > 0) {
+    const size_t n = std::min<size_t>(c->reason.size(), (size_t)reason_capacity - 1);
+    memcpy(reason, c->reason.data(), n);
+    reason[n] = 0;
+  }
+  switch (c->state) {
+    case K3HipCache::kEnabled: return 1;
+    case K3HipCache::kUnqualified: return 0;
+    case K3HipCache::kDisabled: return K3_HIP_E_CAPABILITY;
+    default: return K3_HIP_E_EXEC;
+  }
+}
+
+void k3_hip_cache_poison(K3HipCache* c, const char* failure) {
+  if (!c) return;
+  std::lock_guard<std::mutex> lk(c->mu);
+  poison_locked(c, std::string("poisoned by caller: ") + (failure ? failure : "no detail"), true);
 }
 
 void k3_hip_cache_stats(const K3HipCache* c, long long* six) {

@@ -305,6 +305,19 @@ int k3_hip_cache_ready_subset(K3HipCache* cache, uint64_t plan_id,
 void k3_hip_cache_release(K3HipCache* cache, uint64_t plan_id);
 /* [hits, misses, evictions, resident, capacity, bytes_uploaded]. */
 void k3_hip_cache_stats(const K3HipCache* cache, long long* six);
+/* Qualification and fail-closed state (CudaMoeExpertCache::available / detail,
+ * provider_cuda_moe.cpp:889-961).  The first plan runs the reference's device
+ * known-answer tests (:291-420) on the cache's stream.  Returns 1 enabled,
+ * 0 not yet qualified, K3_HIP_E_CAPABILITY disabled by a known-answer
+ * mismatch (the caller takes its CPU path), K3_HIP_E_EXEC terminal (a HIP
+ * failure inside a cache call, or k3_hip_cache_poison); once not enabled,
+ * plan / fetch / resolve / ready_subset return that status and every resident
+ * entry is dropped.  reason (nullable) receives the detail. */
+int k3_hip_cache_state(const K3HipCache* cache, char* reason,
+                       uint64_t reason_capacity);
+/* Mark the cache terminally failed (CudaMoeExpertCache::poison_external,
+ * provider_cuda_moe.cpp:1199-1201). */
+void k3_hip_cache_poison(K3HipCache* cache, const char* failure);
 /* Copy the resident span of (layer, id) to host (bounded D2H, the CPU fallback
  * materialisation of provider_cuda_moe.cpp:1170-1201).  0 or -2 if absent. */
 int k3_hip_cache_read_back(K3HipCache* cache, int layer, uint16_t id,

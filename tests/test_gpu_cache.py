@@ -11,6 +11,10 @@ CudaMoeExpertCache (native/provider_gate/provider_cuda_moe.{h,cpp}).
   exactly one of them, with no host synchronisation between calls, so every
   upload overwrites slots that kernels queued on the compute stream may still
   be reading; outputs must equal direct layer calls on the same bytes.
+* Qualification: the reference's device known-answer tests run before the
+  first plan (provider_cuda_moe.cpp:291-420, :889-953).
+* Fail-closed: a poisoned cache drops its entries and refuses later calls with
+  the reason (:517-533, :1199-1201).
 """
 import ctypes as C
 
@@ -190,5 +194,61 @@ def test_cache_streaming_reuse(gpu):
                                 x[c:c + 1], moe.workspace(g, n))
             torch.cuda.synchronize()
             assert torch.equal(outs[c], ref), f"call {c}"
+    finally:
+        lib.k3_hip_cache_destroy(cache)
+
+
+def _state(lib, cache):
+    buf = C.create_string_buffer(256)
+    return lib.k3_hip_cache_state(cache, buf, 256), buf.value.decode()
+
+
+def test_cache_qualifies_on_first_plan(gpu):
+    """CudaMoeExpertCache::available (provider_cuda_moe.cpp:889-953): the
+    device known-answer tests run before the first use, and pass here."""
+    from deltafin_amd import _lib
+    lib = gpu
+    say("cache qualification (device known-answer tests)")
+    cache = lib.k3_hip_cache_create(0, 1 << 20, 2, 1, 0)
+    assert cache, _lib.last_error()
+    try:
+        assert _state(lib, cache)[0] == 0
+        assert _plan(lib, cache, 1, 0, [3]) == [3]
+        st, why = _state(lib, cache)
+        assert st == 1 and "known-answer" in why, why
+        lib.k3_hip_cache_release(cache, 1)
+    finally:
+        lib.k3_hip_cache_destroy(cache)
+
+
+def test_cache_poison_fails_closed(gpu):
+    """poison_external / poison (provider_cuda_moe.cpp:517-533, :1199-1201):
+    every resident entry is dropped and later calls fail with the reason."""
+    import torch
+    from deltafin_amd import _lib
+    lib = gpu
+    span = 1 << 20
+    say("cache poison")
+    host = _pinned(span)
+    host.numpy()[:] = 7
+    cache = lib.k3_hip_cache_create(0, span, 2, 1, 0)
+    assert cache, _lib.last_error()
+    try:
+        assert _plan(lib, cache, 1, 0, [5]) == [5]
+        srcs = (C.c_void_p * 1)(host.data_ptr())
+        assert lib.k3_hip_cache_fetch(cache, 1, srcs, 1) == 0
+        torch.cuda.synchronize()
+        lib.k3_hip_cache_release(cache, 1)
+        assert _stats(lib, cache)[3] == 1
+        lib.k3_hip_cache_poison(cache, b"spine failure")
+        st, why = _state(lib, cache)
+        assert st == _lib.K3_HIP_E_EXEC and "spine failure" in why
+        assert _stats(lib, cache)[3] == 0
+        missing = (C.c_uint16 * 1)()
+        n_missing = C.c_int(-1)
+        rc = lib.k3_hip_cache_plan(cache, 2, 0, _ids([5]), 1, missing, C.byref(n_missing))
+        assert rc == _lib.K3_HIP_E_EXEC and "spine failure" in _lib.last_error()
+        back = np.empty(span, dtype=np.uint8)
+        assert lib.k3_hip_cache_read_back(cache, 0, 5, back.ctypes.data, span) != 0
     finally:
         lib.k3_hip_cache_destroy(cache)

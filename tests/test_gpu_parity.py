@@ -393,3 +393,38 @@ def test_verify_route_bank384(gpu, m):
         spans = [oracle.synth_expert(777, int(e), g.hidden, g.intermediate) for e in rid]
         ref, mag = oracle.moe_layer_f64(spans, rw, g.hidden, g.intermediate, g.activation, x[p])
         assert oracle.cond_rel_err(out[p], ref, mag, g.intermediate) <= TOL
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="reference CPU library not built")
+def test_k3_layer_vs_reference_expert_set(gpu):
+    """K3 at full shape (hidden 3584, intermediate 3072, SiTU, 16 experts)
+    against the reference's own whole-set call mxfp4_moe_expert_set
+    (tools/fused_gemv_batch.c:465-518, built from the reference sources into
+    oracle/_ref), within 2e-4 of the output's condition scale, the bound the
+    reference's full-layer parity test uses (provider_moe_test.cpp:268-296).
+    Checked through the device surface and through the descriptor surface with
+    raw-v1 and scale4-v2 spans."""
+    import torch
+    from deltafin_amd import _lib, moe
+    g = moe.preset(1)
+    assert gpu.k3_hip_configure_v1(C.byref(g)) == 0
+    n = 16
+    say(f"K3 layer vs reference mxfp4_moe_expert_set, {n} experts")
+    spans = _experts(n, g.hidden, g.intermediate, 808)
+    rng = np.random.default_rng(909)
+    w = rng.random(n).astype(np.float32)
+    w /= w.sum()
+    x = rng.standard_normal(g.hidden).astype(np.float32)
+    want = oracle.ref_expert_set(spans, w, x, g.hidden, g.intermediate, threads=8)
+    _, mag = oracle.moe_layer_f64(spans, w.astype(np.float64), g.hidden, g.intermediate,
+                                  g.activation, x)
+    outs = {}
+    dspans = [_t(sp) for sp in spans]
+    outs["device"] = moe.moe_layer(g, dspans, w, _t(x), moe.workspace(g, n)).cpu().numpy()
+    outs["descriptor raw-v1"] = moe.moe_layer_desc(spans, w, x)
+    s4 = [oracle.scale4_span(sp) for sp in spans]
+    outs["descriptor scale4-v2"] = moe.moe_layer_desc(s4, w, x, layout=_lib.K3_LAYOUT_SCALE4_V2)
+    torch.cuda.synchronize()
+    for name, got in outs.items():
+        err = oracle.cond_rel_err(got, want, mag, g.intermediate)
+        assert err <= 2e-4, f"{name}: {err:.3e}"
