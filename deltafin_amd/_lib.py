@@ -133,6 +133,7 @@ SIGNATURES = {
     "k3_hip_timing_end": (_i32, [C.POINTER(K3HipKernelTimingV1), _i32, C.POINTER(_i32),
                                  C.POINTER(C.c_longlong)]),
     "k3_hip_set_fused_decode": (_i32, [_i32]),
+    "k3_hip_set_verify_mode": (_i32, [_i32]),
     "k3_hip_scale4_check_header": (_i32, [_vp, _u64]),
     "k3_hip_synth_bank": (_i32, [_GP, _vp, _u64, _i32, _u64, _u64, _i32, _i32, _vp]),
     "k3_hip_synth_normal": (_i32, [_vp, _i32, _u64, _u64, _u64, _vp]),
@@ -217,6 +218,16 @@ def set_fused_decode(enabled: bool) -> bool:
     """Select the fused single-launch decode path or the two-launch path (the
     default) for later layer calls; returns the previous setting."""
     return bool(load().k3_hip_set_fused_decode(1 if enabled else 0))
+
+
+VERIFY_AUTO, VERIFY_POSITIONS, VERIFY_UNION_MFMA, VERIFY_UNION_VALU = 0, 1, 2, 3
+
+
+def set_verify_mode(mode: int) -> int:
+    """Select the verify path process-wide (K3_VERIFY_*); returns the previous mode."""
+    prev = load().k3_hip_set_verify_mode(int(mode))
+    check(min(prev, 0), "k3_hip_set_verify_mode")
+    return prev
 
 
 def timing_begin(max_launches: int) -> None:

@@ -49,7 +49,7 @@ CXX_FLAGS = [
     "-Wextra",
     "-Wno-unused-parameter",
 ]
-KERNEL_SOURCES = ["k3_kernels.hip"]
+KERNEL_SOURCES = ["k3_kernels.hip", "k3_verify_mfma.hip"]
 HOST_SOURCES = ["k3_abi.cpp", "k3_cache.cpp", "k3_timing.cpp"]
 
 

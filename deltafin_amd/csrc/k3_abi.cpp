@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -156,6 +157,10 @@ uint64_t workspace_bytes(const Geo& g, int max_edges, int max_positions) {
   b += align256(E * 4);             // epos
   b += align256((P + 1) * 4);       // poff
   b += align256(sizeof(VerifyPlanDev));
+  b += align256(P * kMaxTerms * g.hidden);         // xq
+  b += align256(P * kMaxTerms * (g.hidden / 32));  // xqs
+  b += align256(E * kMaxTerms * g.inter);          // hq
+  b += align256(E * kMaxTerms * (g.inter / 32));   // hqs
   return b;
 }
 
@@ -182,6 +187,10 @@ bool carve_workspace(void* base, uint64_t bytes, const Geo& g, int max_edges, in
   ws->epos = reinterpret_cast<int32_t*>(take(E * 4));
   ws->poff = reinterpret_cast<int32_t*>(take((P + 1) * 4));
   ws->plan = reinterpret_cast<VerifyPlanDev*>(take(sizeof(VerifyPlanDev)));
+  ws->xq = take(P * kMaxTerms * g.hidden);
+  ws->xqs = take(P * kMaxTerms * (g.hidden / 32));
+  ws->hq = take(E * kMaxTerms * g.inter);
+  ws->hqs = take(E * kMaxTerms * (g.inter / 32));
   return true;
 }
 
@@ -621,6 +630,9 @@ bool geometry_from(const K3HipGeometryV1* g, Geo* out) {
 
 int check_dtype(int d) { return d == K3_DTYPE_F32 || d == K3_DTYPE_BF16; }
 
+// Process-wide verify path (k3_hip_set_verify_mode).
+std::atomic<int> g_verify_mode{K3_VERIFY_AUTO};
+
 }  // namespace
 }  // namespace k3
 
@@ -958,12 +970,29 @@ int k3_hip_moe_verify_route_device(const K3HipGeometryV1* gd, const uint8_t* ban
     return fail(K3_HIP_E_INVALID, "verify: workspace missing, misaligned or too small");
   if (n_bank > 4096) return fail(K3_HIP_E_INVALID, "verify: n_bank must be at most 4096");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int mode = g_verify_mode.load();
+  if (mode == K3_VERIFY_UNION_MFMA && !verify_mfma_supported(g))
+    return fail(K3_HIP_E_CAPABILITY, "verify: this geometry/layout has no matrix-core path");
+  // Union paths: route every position (one workgroup each), group the edges
+  // by expert, then read each routed expert once for all of its positions.
+  // A position's top_k experts are distinct, so no expert has more than
+  // n_positions <= 16 edges.
+  const bool mfma = mode == K3_VERIFY_UNION_MFMA ||
+                    (mode == K3_VERIFY_AUTO && n_positions >= 2 && verify_mfma_supported(g));
+  if (mfma || mode == K3_VERIFY_UNION_VALU) {
+    int rc = launch_route(logits, n_bank, top_k, n_positions, ws.ids, ws.w, route_ids,
+                          route_weights, st);
+    if (rc == K3_HIP_OK)
+      rc = launch_verify_plan_bank(g, bank, expert_stride, n_positions, top_k, ws, st);
+    if (rc != K3_HIP_OK) return rc;
+    return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
+                : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws,
+                                      true, st);
+  }
   // One routed decode layer per position, in order on the stream: each
   // position's gate/up kernel ranks its own logits, so the routes equal the
   // per-position router's.  An expert picked by several positions is read once
-  // per position; with independent routes the union is nearly M * top_k
-  // experts anyway, and these kernels stream about twice as fast as the
-  // union-sharing verify kernels (design notes).
+  // per position.
   const size_t xb = x_dtype == K3_DTYPE_BF16 ? 2 : 4, ob = out_dtype == K3_DTYPE_BF16 ? 2 : 4;
   for (int p = 0; p < n_positions; ++p) {
     TokenRoute route;
@@ -1028,21 +1057,38 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
     tbl.ptr[i] = edge_experts[i];
     tbl.w[i] = edge_weights[i];
   }
-  // Positions that share most of their experts: the union kernels read each
-  // shared expert once; otherwise one decode layer per position (about twice
-  // the streaming rate of the union kernels, so they win unless the union is
-  // under half the edges).
-  int n_unique = 0;
+  // Distinct experts and the most edges any one of them carries (the
+  // matrix-core path takes up to 16 edges, one token column each).
+  int n_unique = 0, max_edges_per_expert = 0;
   for (int i = 0; i < n_edges; ++i) {
     bool seen = false;
     for (int j = 0; j < i && !seen; ++j) seen = tbl.ptr[j] == tbl.ptr[i];
-    n_unique += !seen;
+    if (seen) continue;
+    ++n_unique;
+    int c = 0;
+    for (int j = i; j < n_edges; ++j) c += tbl.ptr[j] == tbl.ptr[i];
+    max_edges_per_expert = std::max(max_edges_per_expert, c);
   }
-  if (2 * n_unique <= n_edges) {
+  const int mode = g_verify_mode.load();
+  const bool mfma_ok = verify_mfma_supported(g) && max_edges_per_expert <= 16;
+  if (mode == K3_VERIFY_UNION_MFMA && !mfma_ok)
+    return fail(K3_HIP_E_CAPABILITY,
+                "verify: no matrix-core path (geometry/layout, or an expert with %d > 16 edges)",
+                max_edges_per_expert);
+  const bool mfma = mode == K3_VERIFY_UNION_MFMA ||
+                    (mode == K3_VERIFY_AUTO && n_positions >= 2 && mfma_ok);
+  // Without the matrix-core path, positions that share most of their experts
+  // take the VALU union kernels (each shared expert read once); otherwise one
+  // decode layer per position (about twice the streaming rate of the VALU
+  // union kernels, so they win unless the union is under half the edges).
+  const bool valu = mode == K3_VERIFY_UNION_VALU ||
+                    (mode == K3_VERIFY_AUTO && !mfma && 2 * n_unique <= n_edges);
+  if (mfma || valu) {
     int rc = launch_verify_plan_table(tbl, ws, st);
-    if (rc == K3_HIP_OK)
-      rc = launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, false, st);
-    return rc;
+    if (rc != K3_HIP_OK) return rc;
+    return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
+                : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws,
+                                      false, st);
   }
   const size_t xb = x_dtype == K3_DTYPE_BF16 ? 2 : 4, ob = out_dtype == K3_DTYPE_BF16 ? 2 : 4;
   for (int p = 0; p < n_positions; ++p) {
@@ -1071,6 +1117,12 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
 }
 
 int k3_hip_set_fused_decode(int enabled) { return set_fused_decode(enabled); }
+
+int k3_hip_set_verify_mode(int mode) {
+  if (mode < K3_VERIFY_AUTO || mode > K3_VERIFY_UNION_VALU)
+    return fail(K3_HIP_E_INVALID, "verify mode %d unknown", mode);
+  return g_verify_mode.exchange(mode);
+}
 
 int k3_hip_synth_bank(const K3HipGeometryV1* gd, uint8_t* bank, uint64_t expert_stride,
                       int n_experts, uint64_t first_expert, uint64_t seed, int scale_lo,

@@ -299,6 +299,25 @@ __device__ __forceinline__ uint32_t rsrc_load_u32(Rsrc r, uint32_t lane_off, uin
   return __builtin_amdgcn_raw_buffer_load_b32(r, lane_off, off, 0);
 }
 
+// The wave-uniform copy of a pointer, in scalar registers (lane 0's value).
+// __builtin_amdgcn_readfirstlane returns a signed int, so each half passes
+// through uint32_t before widening: a low word >= 2^31 widened from int would
+// sign-extend into the high word and form a wild address.
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | (uint64_t)lo);
+}
+
+// Workgroup barrier ordering only LDS: outstanding global loads (prefetched
+// weight batches) and global stores stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <typename T>
 __device__ __forceinline__ T ld(const T* p) {
   return *p;

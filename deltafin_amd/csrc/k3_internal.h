@@ -81,7 +81,17 @@ struct Workspace {
   int32_t* epos;        // [max_edges] edge -> position
   int32_t* poff;        // [max_positions + 1]
   VerifyPlanDev* plan;  // 1
+  // MFMA verify operands: activations split into fp8 (E4M3) terms with one
+  // E8M0 scale per 32 elements and term, row-major [row][term][K] bytes and
+  // [row][term][K / 32] scale bytes (kMaxTerms terms per row).
+  uint8_t* xq;          // [max_positions][kMaxTerms][H]
+  uint8_t* xqs;         // [max_positions][kMaxTerms][H / 32]
+  uint8_t* hq;          // [max_edges][kMaxTerms][I]
+  uint8_t* hqs;         // [max_edges][kMaxTerms][I / 32]
 };
+
+// Most fp8 terms an activation row is split into (fp32 rows take three).
+constexpr int kMaxTerms = 3;
 
 uint64_t workspace_bytes(const Geo& g, int max_edges, int max_positions);
 bool carve_workspace(void* base, uint64_t bytes, const Geo& g, int max_edges,
@@ -121,6 +131,16 @@ int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws,
 int launch_verify_layer(const Geo& g, int n_edges, int n_positions,
                         const void* x, int x_dtype, void* out, int out_dtype,
                         const Workspace& ws, bool pipelined, hipStream_t stream);
+// Per-position route-ordered combine of ws.y (edge outputs) into out.
+int launch_verify_combine(const Geo& g, int n_positions, void* out, int out_dtype,
+                          const Workspace& ws, hipStream_t stream);
+// Matrix-core verify (k3_verify_mfma.hip): split x, gate/up units, split h,
+// down units, combine.  Needs a plan in ws whose experts each have at most 16
+// edges, and a geometry verify_mfma_supported accepts.
+bool verify_mfma_supported(const Geo& g);
+int launch_verify_mfma(const Geo& g, int n_edges, int n_positions, const void* x,
+                       int x_dtype, void* out, int out_dtype, const Workspace& ws,
+                       hipStream_t stream);
 int launch_synth_bank(const Geo& g, uint8_t* bank, uint64_t stride,
                       int n_experts, uint64_t first_expert, uint64_t seed,
                       int lo, int hi, hipStream_t stream);
@@ -146,6 +166,9 @@ enum KernelClass : int {
   KC_COMBINE,
   KC_SYNTH,
   KC_DECODE_FUSED,
+  KC_SPLIT,
+  KC_GLU_MFMA,
+  KC_DOWN_MFMA,
   KC_COUNT
 };
 

@@ -31,6 +31,7 @@
 
 #include "k3_device.h"
 #include "k3_internal.h"
+#include "k3_launch.h"
 
 namespace k3 {
 
@@ -290,13 +291,6 @@ __device__ __forceinline__ void load_x_chunk<float>(XChunk<float>& xc, const flo
   for (int i = 0; i < 32; ++i) xc.v[i] = cs.valid ? xc.v[i] : 0.0f;
 }
 
-// Workgroup barrier ordering only LDS: outstanding global loads (prefetched
-// weight batches) and global stores stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // ======================================================================
 // decode phase A: gate/up rows + activation -> h
@@ -1598,11 +1592,8 @@ __global__ __launch_bounds__(256, 2) void k_glu_verify(const Geo g, const XT* __
   auto load = [&](GluVBatch<XT, kR, kG>& bt, int it) {
     const int unit = unit_at(it);
     const int uid = unit / upe;
-    const uint64_t sp = s_span[uid];
-    const uint64_t spu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(sp >> 32)) << 32) |
-                         (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)sp);
-    glu_load_rows(bt.w, reinterpret_cast<const uint8_t*>(spu), g, (unit - uid * upe) * kR, cs,
-                  gg);
+    const uint8_t* spu = uniform_ptr(reinterpret_cast<const uint8_t*>(s_span[uid]));
+    glu_load_rows(bt.w, spu, g, (unit - uid * upe) * kR, cs, gg);
     load_x_chunk<XT>(bt.x0, x + (size_t)s_pos[s_uoff[uid]] * g.hidden, cs);
   };
   int nbar = 0;  // barriers passed (uniform): selects the red buffer
@@ -1943,20 +1934,6 @@ constexpr int kRowsVerifyB = 16;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Every launch goes through hipExtLaunchKernel so that an open timing window
-// gets the dispatch's own start/end stamps (null events: an ordinary launch).
-template <typename F, typename... Args>
-void launch_timed(const TimedLaunch& tl, F kernel, const dim3& grid, const dim3& block,
-                  uint32_t lds, hipStream_t st, Args... args) {
-  hipExtLaunchKernelGGL(kernel, grid, block, lds, st, tl.start(), tl.stop(), 0u, args...);
-}
-
-int launched(TimedLaunch& tl, const char* what) {
-  const hipError_t e = hipGetLastError();
-  if (e == hipSuccess) return K3_HIP_OK;
-  tl.failed();
-  return hip_fail(what, e);
-}
 
 template <typename XT, typename OT>
 int gemv1_dispatch(const uint8_t* p, const uint8_t* s, const XT* x, OT* y, int rows, int cols,
@@ -2401,6 +2378,11 @@ int launch_verify_layer(const Geo& g, int n_edges, int n_positions, const void* 
   if (rc != K3_HIP_OK) return rc;
   rc = down_verify_dispatch(g, n_edges, ws, pipelined, st);
   if (rc != K3_HIP_OK) return rc;
+  return launch_verify_combine(g, n_positions, out, out_dtype, ws, st);
+}
+
+int launch_verify_combine(const Geo& g, int n_positions, void* out, int out_dtype,
+                          const Workspace& ws, hipStream_t st) {
   const int64_t n = (int64_t)g.hidden * n_positions;
   const dim3 grid((unsigned)((n + 255) / 256)), block(256);
   TimedLaunch tl(KC_COMBINE, st);

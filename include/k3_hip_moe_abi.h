@@ -353,6 +353,26 @@ int k3_hip_timing_end(K3HipKernelTimingV1* out, int capacity, int* n_out,
  * slower on MI355X.  Returns the previous setting. */
 int k3_hip_set_fused_decode(int enabled);
 
+/* ============================== verify path selection */
+/* No reference counterpart.  How the two verify calls above run:
+ *   K3_VERIFY_AUTO (default): batches of two or more positions go through the
+ *     matrix-core union path where the geometry allows it (raw-v1 spans,
+ *     hidden and intermediate multiples of 512) and no expert carries more
+ *     than 16 edges; otherwise one decode layer per position, or the union
+ *     VALU kernels when a caller route's positions share most experts;
+ *   K3_VERIFY_POSITIONS: one decode layer per position (an expert chosen by
+ *     several positions is read once per position, as in the reference);
+ *   K3_VERIFY_UNION_MFMA: every routed expert read once per batch and
+ *     multiplied on the block-scaled FP4 matrix cores; a call whose geometry
+ *     or route does not allow it returns K3_HIP_E_CAPABILITY;
+ *   K3_VERIFY_UNION_VALU: every routed expert read once per batch on the
+ *     first-design VALU union kernels.
+ * Process-wide; returns the previous mode, or K3_HIP_E_INVALID for an
+ * unknown mode (the mode is then unchanged). */
+enum { K3_VERIFY_AUTO = 0, K3_VERIFY_POSITIONS = 1, K3_VERIFY_UNION_MFMA = 2,
+       K3_VERIFY_UNION_VALU = 3 };
+int k3_hip_set_verify_mode(int mode);
+
 /* ============================== synthetic inputs (benchmark support) */
 /* No reference counterpart.  Fill device memory with the counter-based
  * synthetic distribution shared with oracle/orc.c: packed bytes uniform,

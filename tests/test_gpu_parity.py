@@ -362,14 +362,10 @@ def test_verify_table_matches_layer(gpu):
         assert oracle.cond_rel_err(out[p], ref, mag, g.intermediate) <= TOL
 
 
-@pytest.mark.skip(reason="the pipelined verify kernels (rank-sorted plan, k_glu_verify, "
-                         "k_down_verify64) are switched off in the library: a timing run of "
-                         "device-routed verify over a 384-expert bank faulted the GPU and no "
-                         "cause has been found; the first-design kernels serve every call")
 @pytest.mark.parametrize("m", [4, 16])
 def test_verify_route_bank384(gpu, m):
-    """Device-routed verify over a config-3-sized bank (384 experts), the case
-    the pipelined verify kernels faulted on."""
+    """Device-routed verify over a config-3-sized bank (384 experts, 8.98 GB:
+    span addresses on both sides of every 2^31 boundary of the low word)."""
     import torch
     from deltafin_amd import moe
     g = moe.preset(2)
