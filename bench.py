@@ -80,6 +80,8 @@ def parse() -> argparse.Namespace:
                     help="CPU work budget for the reference CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--parity-tokens", type=int, default=2)
+    ap.add_argument("--verify-only", action="store_true",
+                    help="time only the config-3 verify paths (one JSON line)")
     ap.add_argument("--verify-batches", type=int, default=20,
                     help="verify batches timed per M for the config-3 line (0 skips it)")
     ap.add_argument("--streamed", action="store_true",
@@ -465,6 +467,11 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"bank of {N_BANK} experts ({N_BANK * stride / 1e9:.2f} GB) synthesised in HBM")
 
+    if args.verify_only:
+        print(json.dumps(_verify_config3(moe, _lib, g, bank, stride, max(1, args.verify_batches))),
+              flush=True)
+        return 0
+
     fn = lib.k3_hip_moe_route_layer_device
     gref = C.byref(g)
     ws_base, ws_bytes = moe._ws_args(ws)
@@ -633,37 +640,46 @@ def _traffic_from_profiles(kernel: str):
     return None
 
 
-MFMA_PEAK_FP4_TFLOPS = 10100.0  # dense MXFP4 on MI355X
+# The verify matrix-core path multiplies fp4 weights by fp8 activation terms:
+# v_mfma_scale_f32_16x16x128_f8f6f4 with one fp8 operand runs at the dense fp8
+# rate of MI355X (5.0 PFLOP/s).
+MFMA_PEAK_FP8_TFLOPS = 5000.0
+MFMA_FLOPS = 2 * 16 * 16 * 128  # one 16x16x128 block-scaled MFMA
+X_TERMS, H_TERMS = 2, 3         # fp8 terms per bf16 x row / fp32 h row
 
 
-def _verify_config3(moe, _lib, g, bank, stride, batches: int) -> dict:
-    """BASELINE configs[3]: batched speculative verify over the same resident
-    bank: M positions, each with its own top-16 of 384 N(0,1) logits and bf16
-    x; each routed expert's bytes are read once per batch (union of the M
-    routes).  Per M: `batches` batches timed back to back (after 3 warm-up
-    batches), bytes = union experts x span + M x (x + logits + out)."""
+def _mfma_issued_per_expert() -> int:
+    """MFMA instructions the union kernels issue per unique expert: gate and up
+    (I/16 row tiles each, H/128 K steps, one per x term) and down (H/16 row
+    tiles, I/128 K steps, one per h term).  Each covers 16 token columns."""
+    glu = 2 * (INTER // 16) * (HIDDEN // 128) * X_TERMS
+    down = (HIDDEN // 16) * (INTER // 128) * H_TERMS
+    return glu + down
+
+
+def _verify_batches(moe, _lib, g, bank, stride, logits, x, batches: int) -> dict:
+    """Time `batches` verify calls (after 3 warm-up calls) on each path:
+    AUTO (the library's choice), the matrix-core union path and one decode
+    layer per position; per-kernel stamps for the union path."""
     import torch
 
-    out = {}
-    for m in (4, 8, 16):
-        n = batches + 3
-        logits = moe.synth_normal(n * m * N_BANK, torch.float32, SEED + 30 + m, 1).view(n, m, N_BANK)
-        x = moe.synth_normal(n * m * HIDDEN, torch.bfloat16, SEED + 30 + m, 2).view(n, m, HIDDEN)
-        y = torch.empty((n, m, HIDDEN), dtype=torch.bfloat16, device="cuda")
-        ws = moe.workspace(g, m * TOP_K, m)
-        base, nbytes = moe._ws_args(ws)
-        st = moe.stream_handle()
-        lib = _lib.load()
-        ids = torch.empty((n, m, TOP_K), dtype=torch.int32, device="cuda")
+    n, m = logits.shape[0], logits.shape[1]
+    y = torch.empty((n, m, HIDDEN), dtype=torch.bfloat16, device="cuda")
+    ws = moe.workspace(g, m * TOP_K, m)
+    base, nbytes = moe._ws_args(ws)
+    st = moe.stream_handle()
+    lib = _lib.load()
+    ids = torch.empty((n, m, TOP_K), dtype=torch.int32, device="cuda")
 
-        def call(i: int) -> None:
-            rc = lib.k3_hip_moe_verify_route_device(
-                C.byref(g), bank.data_ptr(), stride, N_BANK, logits[i].data_ptr(), m, TOP_K,
-                x[i].data_ptr(), _lib.K3_DTYPE_BF16, y[i].data_ptr(), _lib.K3_DTYPE_BF16,
-                ids[i].data_ptr(), None, base, nbytes, st)
-            if rc != 0:
-                raise _lib.K3HipError(rc, "k3_hip_moe_verify_route_device")
+    def call(i: int) -> None:
+        rc = lib.k3_hip_moe_verify_route_device(
+            C.byref(g), bank.data_ptr(), stride, N_BANK, logits[i].data_ptr(), m, TOP_K,
+            x[i].data_ptr(), _lib.K3_DTYPE_BF16, y[i].data_ptr(), _lib.K3_DTYPE_BF16,
+            ids[i].data_ptr(), None, base, nbytes, st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_moe_verify_route_device")
 
+    def timed(stamps: bool):
         for i in range(3):
             call(i)
         torch.cuda.synchronize()
@@ -672,23 +688,91 @@ def _verify_config3(moe, _lib, g, bank, stride, batches: int) -> dict:
             call(i)
         torch.cuda.synchronize()
         sec = (time.perf_counter() - t0) / batches
-        union = float(np.mean([len(set(ids[i].cpu().numpy().ravel().tolist())) for i in range(3, n)]))
-        nbytes_alg = union * SPAN + m * (X_BYTES + LOGIT_BYTES + OUT_BYTES)
-        flops = m * (KERNEL_FLOPS["glu_decode"] + KERNEL_FLOPS["down_decode"])
-        out[f"M{m}"] = {
-            "us_per_batch": round(sec * 1e6, 1),
-            "token_layers_per_s": round(m / sec, 1),
-            "union_experts": round(union, 1),
-            "algorithmic_bytes": int(nbytes_alg),
-            "achieved_gbs": round(nbytes_alg / sec / 1e9, 1),
-            "hbm_frac": round(nbytes_alg / sec / 1e9 / HBM_PEAK_GBS, 4),
-            "mfma_util": flops / sec / (MFMA_PEAK_FP4_TFLOPS * 1e12),
-        }
-        log(f"verify M={m}: {sec * 1e6:.1f} us/batch, union {union:.1f}, "
-            f"{nbytes_alg / sec / 1e9:.0f} GB/s")
-        del ws
-    return {"config": "BASELINE configs[3]: M positions each routing top-16 of 384, "
-                      "bf16 x/out, every routed expert read once per batch", **out}
+        kern = None
+        if stamps:
+            _lib.timing_begin(64 * n)
+            for i in range(3, n):
+                call(i)
+            torch.cuda.synchronize()
+            kern, _ = _lib.timing_end()
+        return sec, kern
+
+    res = {}
+    for path, mode in (("auto", _lib.VERIFY_AUTO), ("union_mfma", _lib.VERIFY_UNION_MFMA),
+                       ("positions", _lib.VERIFY_POSITIONS)):
+        prev = _lib.set_verify_mode(mode)
+        try:
+            res[path] = timed(path != "positions")
+        finally:
+            _lib.set_verify_mode(prev)
+    union = float(np.mean([len(set(ids[i].cpu().numpy().ravel().tolist())) for i in range(3, n)]))
+    auto_path = "union_mfma" if "glu_mfma" in res["auto"][1] else "positions"
+    sec = res["auto"][0]
+    nbytes_alg = union * SPAN + m * (X_BYTES + LOGIT_BYTES + OUT_BYTES)
+    useful = m * (KERNEL_FLOPS["glu_decode"] + KERNEL_FLOPS["down_decode"])
+    issued = union * _mfma_issued_per_expert() * MFMA_FLOPS
+    usec, kern = res["union_mfma"]
+    kus = {k: round(v["total_ms"] * 1e3 / batches, 2) for k, v in kern.items()}
+    mfma_s = (kus.get("glu_mfma", 0.0) + kus.get("down_mfma", 0.0)) * 1e-6
+    out = {
+        "default_path": auto_path,
+        "us_per_batch": round(sec * 1e6, 1),
+        "token_layers_per_s": round(m / sec, 1),
+        "union_experts": round(union, 1),
+        "edges": m * TOP_K,
+        "algorithmic_bytes": int(nbytes_alg),
+        "achieved_gbs": round(nbytes_alg / sec / 1e9, 1),
+        "hbm_frac": round(nbytes_alg / sec / 1e9 / HBM_PEAK_GBS, 4),
+        "union_mfma_us_per_batch": round(usec * 1e6, 1),
+        "union_mfma_gbs": round(nbytes_alg / usec / 1e9, 1),
+        "positions_us_per_batch": round(res["positions"][0] * 1e6, 1),
+        "union_mfma_speedup_vs_positions": round(res["positions"][0] / usec, 3),
+        "union_mfma_kernels_us": kus,
+        "glu_mfma_gbs": round(union * 2 * MAT_BYTES / (kus["glu_mfma"] * 1e-6) / 1e9, 1)
+        if kus.get("glu_mfma") else None,
+        "down_mfma_gbs": round(union * MAT_BYTES / (kus["down_mfma"] * 1e-6) / 1e9, 1)
+        if kus.get("down_mfma") else None,
+        "mfma_issued_tflops": round(issued / mfma_s / 1e12, 1) if mfma_s else None,
+        "mfma_util": round(issued / mfma_s / (MFMA_PEAK_FP8_TFLOPS * 1e12), 4) if mfma_s else None,
+        "useful_tflops_union_mfma": round(useful / usec / 1e12, 2),
+    }
+    log(f"verify M={m}: auto -> {auto_path} {sec * 1e6:.1f} us/batch (union {union:.1f} of "
+        f"{m * TOP_K} edges); union/mfma {usec * 1e6:.1f} us, per-position "
+        f"{res['positions'][0] * 1e6:.1f} us; mfma kernels {kus}")
+    return out
+
+
+def _verify_config3(moe, _lib, g, bank, stride, batches: int) -> dict:
+    """BASELINE configs[3]: batched speculative verify over the same resident
+    bank: M positions, each with its own top-16 of 384 N(0,1) logits and bf16
+    x.  Each M is timed on the library's default path (AUTO: the matrix-core
+    union kernels when the expected union is under 77% of the edges, else one
+    decode layer per position) and on both paths explicitly.  A second case,
+    `shared_M16`, gives 16 positions logits with a common N(0,1) component
+    (logits = z_common + 0.5 z_position, as consecutive draft tokens of one
+    sequence share much of their routing): there the union is small and the
+    matrix cores carry a real small-M contraction."""
+    import torch
+
+    out = {}
+    for m in (4, 8, 16):
+        n = batches + 3
+        logits = moe.synth_normal(n * m * N_BANK, torch.float32, SEED + 30 + m, 1).view(n, m, N_BANK)
+        x = moe.synth_normal(n * m * HIDDEN, torch.bfloat16, SEED + 30 + m, 2).view(n, m, HIDDEN)
+        out[f"M{m}"] = _verify_batches(moe, _lib, g, bank, stride, logits, x, batches)
+    m = 16
+    n = batches + 3
+    common = moe.synth_normal(n * N_BANK, torch.float32, SEED + 60, 1).view(n, 1, N_BANK)
+    own = moe.synth_normal(n * m * N_BANK, torch.float32, SEED + 60, 2).view(n, m, N_BANK)
+    logits = (common + 0.5 * own).contiguous()
+    x = moe.synth_normal(n * m * HIDDEN, torch.bfloat16, SEED + 60, 3).view(n, m, HIDDEN)
+    out["shared_M16"] = _verify_batches(moe, _lib, g, bank, stride, logits, x, batches)
+    return {"config": "BASELINE configs[3]: M positions each routing top-16 of 384, bf16 x/out; "
+                      "us_per_batch on the default path; union_mfma_* on the matrix-core union "
+                      "kernels (every routed expert read once per batch); mfma_util = issued "
+                      "block-scaled MFMA flops (16 token columns each) / (gate/up + down kernel "
+                      "time x 5.0 PFLOP/s dense fp8)",
+            **out}
 
 
 def _parity(moe, oracle, synth, g, bank, stride, logits, x, ws, n_tokens: int) -> dict:

@@ -633,6 +633,21 @@ int check_dtype(int d) { return d == K3_DTYPE_F32 || d == K3_DTYPE_BF16; }
 // Process-wide verify path (k3_hip_set_verify_mode).
 std::atomic<int> g_verify_mode{K3_VERIFY_AUTO};
 
+// AUTO picks the matrix-core union path when the batch's unique experts are
+// at most this fraction of its edges: the union kernels stream about 1/1.3 of
+// the decode kernels' rate on MI355X (config 3: ~4.6 vs ~6 TB/s), so they win
+// once they read under 1/1.3 of the bytes.
+constexpr double kUnionFraction = 0.77;
+
+// Expected unique experts of n_positions independent top_k routes over n_bank
+// experts (uniform routing, the least sharing a verify batch can have).
+double expected_union(int n_bank, int top_k, int n_positions) {
+  const double p = (double)top_k / (double)n_bank;
+  double miss = 1.0;
+  for (int i = 0; i < n_positions; ++i) miss *= 1.0 - p;
+  return (double)n_bank * (1.0 - miss);
+}
+
 }  // namespace
 }  // namespace k3
 
@@ -977,8 +992,11 @@ int k3_hip_moe_verify_route_device(const K3HipGeometryV1* gd, const uint8_t* ban
   // by expert, then read each routed expert once for all of its positions.
   // A position's top_k experts are distinct, so no expert has more than
   // n_positions <= 16 edges.
+  const bool shared = expected_union(n_bank, top_k, n_positions) <=
+                      kUnionFraction * (double)n_edges;
   const bool mfma = mode == K3_VERIFY_UNION_MFMA ||
-                    (mode == K3_VERIFY_AUTO && n_positions >= 2 && verify_mfma_supported(g));
+                    (mode == K3_VERIFY_AUTO && n_positions >= 2 && shared &&
+                     verify_mfma_supported(g));
   if (mfma || mode == K3_VERIFY_UNION_VALU) {
     int rc = launch_route(logits, n_bank, top_k, n_positions, ws.ids, ws.w, route_ids,
                           route_weights, st);
@@ -1076,13 +1094,14 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
                 "verify: no matrix-core path (geometry/layout, or an expert with %d > 16 edges)",
                 max_edges_per_expert);
   const bool mfma = mode == K3_VERIFY_UNION_MFMA ||
-                    (mode == K3_VERIFY_AUTO && n_positions >= 2 && mfma_ok);
+                    (mode == K3_VERIFY_AUTO && n_positions >= 2 && mfma_ok &&
+                     n_unique <= kUnionFraction * n_edges);
   // Without the matrix-core path, positions that share most of their experts
   // take the VALU union kernels (each shared expert read once); otherwise one
   // decode layer per position (about twice the streaming rate of the VALU
   // union kernels, so they win unless the union is under half the edges).
   const bool valu = mode == K3_VERIFY_UNION_VALU ||
-                    (mode == K3_VERIFY_AUTO && !mfma && 2 * n_unique <= n_edges);
+                    (mode == K3_VERIFY_AUTO && !mfma && !mfma_ok && 2 * n_unique <= n_edges);
   if (mfma || valu) {
     int rc = launch_verify_plan_table(tbl, ws, st);
     if (rc != K3_HIP_OK) return rc;

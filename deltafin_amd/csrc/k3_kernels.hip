@@ -1366,67 +1366,9 @@ __device__ void plan_core(const uint8_t* key, int e, int n_edges, int n_position
   }
 }
 
-// The first plan routine (first appearance order, serial prefix in thread
-// 0), kept for the caller-table plan: the rank-sorted plan above runs the
-// device-routed plan only (see the verify dispatch).
-__device__ void plan_core_serial(const uint8_t* key, int e, int n_edges, int n_positions,
-                          const Workspace& ws) {
-  __shared__ const uint8_t* kp[K3_HIP_MAX_EDGES];
-  __shared__ int first[K3_HIP_MAX_EDGES];
-  __shared__ int uid_of_first[K3_HIP_MAX_EDGES];
-  __shared__ int ucount[K3_HIP_MAX_EDGES];
-  __shared__ int uoff[K3_HIP_MAX_EDGES + 1];
-  if (e < n_edges) kp[e] = key;
-  __syncthreads();
-  int f = e;
-  if (e < n_edges) {
-    for (int j = 0; j < e; ++j) {
-      if (kp[j] == key) {
-        f = j;
-        break;
-      }
-    }
-    first[e] = f;
-  }
-  __syncthreads();
-  if (e < n_edges && f == e) {
-    int u = 0, cnt = 0;
-    for (int j = 0; j < n_edges; ++j) {
-      u += (j < e) && (first[j] == j);
-      cnt += (kp[j] == key);
-    }
-    uid_of_first[e] = u;
-    ucount[u] = cnt;
-    ws.uptr[u] = key;
-  }
-  __syncthreads();
-  if (e == 0) {
-    int u = 0, off = 0;
-    for (int j = 0; j < n_edges; ++j) {
-      if (first[j] == j) {
-        uoff[u] = off;
-        ws.uoff[u] = off;
-        off += ucount[u];
-        ++u;
-      }
-    }
-    uoff[u] = off;
-    ws.uoff[u] = off;
-    ws.plan->n_unique = u;
-    ws.plan->n_edges = n_edges;
-    ws.plan->n_positions = n_positions;
-  }
-  __syncthreads();
-  if (e < n_edges) {
-    int rank = 0;
-    for (int j = 0; j < e; ++j) rank += (kp[j] == key);
-    ws.uedges[uoff[uid_of_first[first[e]]] + rank] = e;
-  }
-}
-
 __global__ __launch_bounds__(256) void k_verify_plan_bank(const uint8_t* bank, uint64_t stride,
                                                           int n_positions, int top_k,
-                                                          const Workspace ws, bool rank_plan) {
+                                                          const Workspace ws) {
   const int e = threadIdx.x;
   const int n_edges = n_positions * top_k;
   const uint8_t* key = nullptr;
@@ -1435,10 +1377,7 @@ __global__ __launch_bounds__(256) void k_verify_plan_bank(const uint8_t* bank, u
     ws.epos[e] = e / top_k;
   }
   if (e <= n_positions) ws.poff[e] = e * top_k;
-  if (rank_plan)
-    plan_core(key, e, n_edges, n_positions, ws);
-  else
-    plan_core_serial(key, e, n_edges, n_positions, ws);
+  plan_core(key, e, n_edges, n_positions, ws);
 }
 
 __global__ __launch_bounds__(256) void k_verify_plan_table(const EdgeTable tbl,
@@ -1453,7 +1392,7 @@ __global__ __launch_bounds__(256) void k_verify_plan_table(const EdgeTable tbl,
     ws.epos[e] = p;
   }
   if (e <= tbl.n_positions) ws.poff[e] = tbl.pos_off[e];
-  plan_core_serial(key, e, tbl.n_edges, tbl.n_positions, ws);
+  plan_core(key, e, tbl.n_edges, tbl.n_positions, ws);
 }
 
 // ======================================================================
@@ -2283,11 +2222,11 @@ int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x, in
 int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride, int n_positions,
                             int top_k, const Workspace& ws, hipStream_t st) {
   (void)g;
-  // The serial plan serves both verify designs; the rank-sorted one belongs
-  // to the pipelined path, which is switched off.
+  // Rank-sorted plan: unique experts in span-pointer order, each expert's
+  // edges in edge order (every union kernel takes any expert order).
   TimedLaunch tl(KC_VERIFY_PLAN, st);
   launch_timed(tl, k_verify_plan_bank, dim3(1), dim3(256), 0, st, bank, stride, n_positions,
-               top_k, ws, false);
+               top_k, ws);
   return launched(tl, "verify plan launch");
 }
 

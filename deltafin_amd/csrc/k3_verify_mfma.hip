@@ -168,11 +168,15 @@ __global__ __launch_bounds__(256) void k_split_terms(const SrcT* __restrict__ sr
 // both gate and up (phase A).  A workgroup is S column-split waves: wave w
 // covers K steps [w KS, (w + 1) KS) of every row, KS = K / (128 S).
 // Workgroup b takes units b, b + NWG, ... and each wave walks the flattened
-// (unit, K step) items with two items in flight: item i + 1 is requested
-// before item i is multiplied.  At a unit's last K step every wave writes its
-// tiles' partial sums to LDS (two slots by unit parity, one barrier per unit)
-// and wave w sums tile w (w + S, ...) over the waves in wave order, applies
-// the activation (phase A) and stores its tokens' rows.
+// (unit, K-step pair) items with two items in flight: item i + 1 is requested
+// before item i is multiplied.  An item takes two adjacent K steps, so the
+// two 64-byte halves of each 128-byte line of a weight row are requested
+// back to back (one K step per item fetched every line twice: its halves
+// were requested a whole item apart and the line was gone from L2 in
+// between).  At a unit's last item every wave writes its tiles' partial sums
+// to LDS (two slots by unit parity, one barrier per unit) and wave w sums
+// tile w (w + S, ...) over the waves in wave order, applies the activation
+// (phase A) and stores its tokens' rows.
 //
 // Every address is in range by construction: units are below U * n_rb,
 // rows below the matrix's rows, K steps below K / 128, and lanes whose token
@@ -185,12 +189,24 @@ struct MfmaPlan {
   int orow[K3_HIP_MAX_EDGES];  // output row (the edge) of the i-th grouped edge
 };
 
-template <int kTiles, int T>
-struct MfmaItem {
-  u32x4 a[kTiles];
-  uint32_t sa[kTiles];
-  u32x4 b[T][2];
-  uint32_t sb[T];
+// Loads of one item: KI adjacent K steps from ks.  Scale dwords hold the 4
+// block scales of one K step for the lane's row (weights) or token
+// (activations); lane group g takes byte g.
+// Scale block of a wave's unit: its rows' E8M0 bytes for its K steps, KS
+// dwords per row (one per K step), kTiles * 16 * KS dwords in all, loaded as
+// dwords by the whole wave at the unit's first item (at most kScaleLoads per
+// lane) and parked in the wave's LDS region as [tile][row][K step].
+constexpr int kScaleLoads = 16;
+
+template <int kTiles, int KI>
+struct MfmaA {  // weights: streamed from HBM, two items in flight
+  u32x4 a[kTiles][KI];
+  uint32_t sblk[kScaleLoads];  // the unit's scale block (first item of a unit)
+};
+template <int T, int KI>
+struct MfmaB {  // activation terms: L2-resident, one item ahead
+  u32x4 b[T][KI][2];  // [term][K step][K runs 16 g.. and 64 + 16 g..]
+  uint32_t sb[T][KI];
 };
 
 __device__ __forceinline__ v8i a_operand(u32x4 w) {
@@ -207,14 +223,34 @@ __device__ __forceinline__ v8i b_operand(u32x4 lo, u32x4 hi) {
 // (cached) loads, unlike the streamed weight chunks.
 __device__ __forceinline__ u32x4 load_b16(const uint8_t* p) { return *(gu32x4*)(p); }
 
-template <bool kGlu, int NT, int T>
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) const u32x2 gu32x2;
+
+// KI scale dwords from p (4 KI-byte aligned): one per K step.
+template <int KI>
+__device__ __forceinline__ void load_scales(uint32_t (&d)[KI], const uint8_t* p) {
+  static_assert(KI == 2 || KI == 4, "two or four K steps per item");
+  if constexpr (KI == 2) {
+    const u32x2 v = *(gu32x2*)(p);
+    d[0] = v.x;
+    d[1] = v.y;
+  } else {
+    const u32x4 v = *(gu32x4*)(p);
+    d[0] = v.x;
+    d[1] = v.y;
+    d[2] = v.z;
+    d[3] = v.w;
+  }
+}
+
+template <bool kGlu, int NT, int T, int KI>
 __global__ __launch_bounds__(256, 2) void k_verify_mfma(const Geo g, const Workspace ws,
                                                         const uint8_t* __restrict__ bq,
                                                         const uint8_t* __restrict__ bqs,
                                                         int n_brows, float* __restrict__ out) {
   constexpr int kM = kGlu ? 2 : 1;
   constexpr int kTiles = kM * NT;
-  extern __shared__ v4f red[];  // [2][S][kTiles][64]
+  extern __shared__ v4f red[];  // [2][S][kTiles][64] sums, then [S][64 * kScaleLoads] scales
   __shared__ MfmaPlan pl;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -222,7 +258,8 @@ __global__ __launch_bounds__(256, 2) void k_verify_mfma(const Geo g, const Works
   const int r16 = lane & 15, qb = lane >> 4;
   const int K = kGlu ? g.hidden : g.inter;
   const int rows = kGlu ? g.inter : g.hidden;
-  const int KS = (K >> 7) / S;
+  const int KS = (K >> 7) / S;  // a multiple of KI (host check)
+  const int KP = KS / KI;       // items per wave and unit
   const int n_rb = rows / (16 * NT);
   const size_t rowb = (size_t)K >> 1, srowb = (size_t)K >> 5;
   const uint64_t wp[2] = {kGlu ? g.w1p : g.w2p, g.w3p};
@@ -243,48 +280,78 @@ __global__ __launch_bounds__(256, 2) void k_verify_mfma(const Geo g, const Works
   const int b0 = blockIdx.x;
   if (b0 >= n_units) return;  // whole workgroup
   const int iters = (n_units - b0 + NWG - 1) / NWG;
-  const int n_items = iters * KS;
+  const int n_items = iters * KP;
 
-  typedef MfmaItem<kTiles, T> Item;
+  typedef MfmaA<kTiles, KI> ItemA;
+  typedef MfmaB<T, KI> ItemB;
   // Loads address a wave-uniform base (scalar registers: the expert's span,
   // the activation terms) plus a 32-bit per-lane offset, so each load needs
   // one VGPR of address instead of two.
   const uint32_t a_lane = (uint32_t)(r16 * rowb) + 16u * qb;  // + row block, tile, K step
-  const uint32_t s_lane = (uint32_t)(r16 * srowb) + qb;
-  auto load = [&](Item& it, int i) {
-    const int ui = i / KS;
+  auto load_b = [&](ItemB& it, int i) {
+    const int ui = i / KP;
     const int unit = b0 + ui * NWG;
-    const int ks = wave * KS + (i - ui * KS);
+    const int ks = wave * KS + KI * (i - ui * KP);
     const int uid = unit / n_rb;
-    const int rb = unit - uid * n_rb;
-    const uint8_t* span = uniform_ptr(pl.uptr[uid]);
     const int e0 = pl.uoff[uid], m = pl.uoff[uid + 1] - e0;
     const bool tok = r16 < m;
     const int brow = pl.brow[min(e0 + (tok ? r16 : 0), n_edges - 1)];
     const uint32_t boff = (uint32_t)(brow * T * K) + 128u * ks + 16u * qb;
-    const uint32_t bsoff = (uint32_t)(brow * T * (int)srowb) + 4u * ks + qb;
+    const uint32_t bsoff = (uint32_t)(brow * T * (int)srowb) + 4u * ks;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       if (tok) {
-        it.b[t][0] = load_b16(bq + (boff + (uint32_t)(t * K)));
-        it.b[t][1] = load_b16(bq + (boff + (uint32_t)(t * K) + 64u));
-        it.sb[t] = load_scale(bqs + (bsoff + (uint32_t)(t * (int)srowb)));
+#pragma unroll
+        for (int k = 0; k < KI; ++k) {
+          it.b[t][k][0] = load_b16(bq + (boff + (uint32_t)(t * K + 128 * k)));
+          it.b[t][k][1] = load_b16(bq + (boff + (uint32_t)(t * K + 128 * k) + 64u));
+        }
+        load_scales<KI>(it.sb[t], bqs + (bsoff + (uint32_t)(t * (int)srowb)));
       } else {
-        it.b[t][0] = u32x4{0u, 0u, 0u, 0u};
-        it.b[t][1] = u32x4{0u, 0u, 0u, 0u};
-        it.sb[t] = 0u;
+#pragma unroll
+        for (int k = 0; k < KI; ++k) {
+          it.b[t][k][0] = u32x4{0u, 0u, 0u, 0u};
+          it.b[t][k][1] = u32x4{0u, 0u, 0u, 0u};
+          it.sb[t][k] = 0u;
+        }
       }
     }
+  };
+  // Scale block addressing: dword j*64 + lane of the block is tile
+  // idx / (16 KS), row (idx / KS) % 16, K step idx % KS of the wave's range.
+  const int n_sdw = kTiles * 16 * KS;  // <= 64 * kScaleLoads (host check)
+  auto load_a = [&](ItemA& it, int i) {
+    const int ui = i / KP;
+    const int unit = b0 + ui * NWG;
+    const int kp = i - ui * KP;
+    const int ks = wave * KS + KI * kp;
+    const int uid = unit / n_rb;
+    const int rb = unit - uid * n_rb;
+    const uint8_t* span = uniform_ptr(pl.uptr[uid]);
     const uint32_t rbase = (uint32_t)rb * 16u * NT;
+    if (kp == 0) {
+#pragma unroll
+      for (int j = 0; j < kScaleLoads; ++j) {
+        const int idx = 64 * j + lane;
+        if (64 * j < n_sdw) {
+          const int ii = min(idx, n_sdw - 1);
+          const int t = ii / (16 * KS), rem = ii - t * 16 * KS;
+          const int row = rem / KS, d = rem - row * KS;
+          const int mt = t / NT, tt = t - mt * NT;
+          it.sblk[j] = load_u32(span + ((uint32_t)wsc[mt] +
+                                        (rbase + 16u * tt + row) * (uint32_t)srowb +
+                                        4u * (wave * KS + d)));
+        }
+      }
+    }
 #pragma unroll
     for (int mt = 0; mt < kM; ++mt) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const uint32_t r = rbase + 16u * t;
-        it.a[mt * NT + t] =
-            load_chunk(span + ((uint32_t)wp[mt] + r * (uint32_t)rowb + 64u * ks + a_lane));
-        it.sa[mt * NT + t] =
-            load_scale(span + ((uint32_t)wsc[mt] + r * (uint32_t)srowb + 4u * ks + s_lane));
+        const uint32_t ao = (uint32_t)wp[mt] + r * (uint32_t)rowb + 64u * ks + a_lane;
+#pragma unroll
+        for (int k = 0; k < KI; ++k) it.a[mt * NT + t][k] = load_chunk(span + (ao + 64u * k));
       }
     }
   };
@@ -321,40 +388,61 @@ __global__ __launch_bounds__(256, 2) void k_verify_mfma(const Geo g, const Works
     }
   };
 
-  auto compute = [&](const Item& it, int i) {
-    const int ui = i / KS;
-    const int k = i - ui * KS;
-    if (k == 0) {
+  const uint32_t sh = 8u * qb;  // this lane group's byte in each scale dword
+  uint32_t* sblk_lds = reinterpret_cast<uint32_t*>(red + (size_t)2 * S * kTiles * 64) +
+                       (size_t)wave * 64 * kScaleLoads;
+  auto compute = [&](const ItemA& ia, const ItemB& ib, int i) {
+    const int ui = i / KP;
+    const int kp = i - ui * KP;
+    if (kp == 0) {
 #pragma unroll
       for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < kScaleLoads; ++j)
+        if (64 * j < n_sdw) sblk_lds[64 * j + lane] = ia.sblk[j];
     }
+    uint32_t sa_w[kTiles][KI];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
+      const uint32_t* src = sblk_lds + (t * 16 + r16) * KS + KI * kp;
 #pragma unroll
-      for (int j = 0; j < T; ++j)
-        acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            a_operand(it.a[t]), b_operand(it.b[j][0], it.b[j][1]), acc[t], 4 /* A: fp4 */,
-            0 /* B: fp8 e4m3 */, 0, (int)it.sa[t], 0, (int)it.sb[j]);
+      for (int k = 0; k < KI; ++k) sa_w[t][k] = src[k];
     }
-    if (k == KS - 1) epilogue(ui);
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+        const int sa = (int)((sa_w[t][k] >> sh) & 0xffu);
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+          const int sb = (int)((ib.sb[j][k] >> sh) & 0xffu);
+          acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              a_operand(ia.a[t][k]), b_operand(ib.b[j][k][0], ib.b[j][k][1]), acc[t],
+              4 /* A: fp4 */, 0 /* B: fp8 e4m3 */, 0, sa, 0, sb);
+        }
+      }
+    }
+    if (kp == KP - 1) epilogue(ui);
   };
 
-  Item A, B;
-  load(A, 0);
-  load(B, min(1, n_items - 1));
+  // Issue order per item: activation terms of item i + 1, then weights of
+  // item i + 2.  Waiting for item i + 1's terms (loads complete in order)
+  // then leaves item i + 2's weights in flight, so the weight stream stays
+  // two items deep while the terms need one buffer.
+  ItemA A0, A1;
+  ItemB Bc;
+  load_b(Bc, 0);
+  load_a(A0, 0);
+  load_a(A1, min(1, n_items - 1));
   for (int i = 0;; i += 2) {
-    compute(A, i);
-    if (i + 2 >= n_items) {
-      if (i + 1 < n_items) compute(B, i + 1);
-      break;
-    }
-    load(A, i + 2);
-    compute(B, i + 1);
-    if (i + 3 >= n_items) {
-      compute(A, i + 2);
-      break;
-    }
-    load(B, i + 3);
+    compute(A0, Bc, i);
+    if (i + 1 >= n_items) break;
+    load_b(Bc, i + 1);
+    if (i + 2 < n_items) load_a(A0, i + 2);
+    compute(A1, Bc, i + 1);
+    if (i + 2 >= n_items) break;
+    load_b(Bc, i + 2);
+    if (i + 3 < n_items) load_a(A1, i + 3);
   }
 }
 
@@ -363,8 +451,41 @@ __global__ __launch_bounds__(256, 2) void k_verify_mfma(const Geo g, const Works
 // ======================================================================
 namespace {
 
-constexpr int kMfmaWaves = 4;  // column-split waves per workgroup
-constexpr int kMfmaTiles = 4;  // 16-row tiles per matrix per unit
+#ifndef K3_MFMA_KI
+#define K3_MFMA_KI 2
+#endif
+constexpr int kItemSteps = K3_MFMA_KI;  // K steps per item (2 or 4)
+// 16-row tiles per unit: of gate and of up, and of down.  Each keeps two
+// items of weights and one of activation terms within the 256 VGPRs of two
+// waves per SIMD without spilling (8 KB of weights per item).
+template <bool kGlu, int T>
+constexpr int unit_tiles() {
+  return kGlu ? 2 : 4;
+}
+
+// Column-split waves for K = k_elems: the most (up to max_s) that leave every
+// wave a whole number of items.
+#ifndef K3_MFMA_GLU_WAVES
+#define K3_MFMA_GLU_WAVES 4
+#endif
+#ifndef K3_MFMA_DOWN_WAVES
+#define K3_MFMA_DOWN_WAVES 1  // down rows have K = intermediate: longer units per wave
+#endif
+// Column-split waves for K = k_elems and kTiles tiles per unit: the preferred
+// max_s if every wave gets a whole number of items and its scale block fits,
+// else the nearest wider split that does, else the nearest narrower; 0 if
+// none of 1, 2, 4 does.
+int mfma_waves(int k_elems, int k_tiles, int max_s) {
+  const int nk = k_elems / 128;
+  auto ok = [&](int s) {
+    return nk % (kItemSteps * s) == 0 && k_tiles * 16 * (nk / s) <= 64 * kScaleLoads;
+  };
+  for (int s = max_s; s <= 4; s <<= 1)
+    if (ok(s)) return s;
+  for (int s = max_s >> 1; s >= 1; s >>= 1)
+    if (ok(s)) return s;
+  return 0;
+}
 
 template <int T, typename SrcT>
 int split_launch(const SrcT* src, int n_rows, int K, uint8_t* q, uint8_t* qs, hipStream_t st) {
@@ -378,27 +499,36 @@ int split_launch(const SrcT* src, int n_rows, int K, uint8_t* q, uint8_t* qs, hi
 template <bool kGlu, int T>
 int mfma_launch(const Geo& g, int n_edges, const Workspace& ws, const uint8_t* bq,
                 const uint8_t* bqs, int n_brows, float* out, hipStream_t st) {
-  constexpr int kTiles = (kGlu ? 2 : 1) * kMfmaTiles;
+  constexpr int NT = unit_tiles<kGlu, T>();
+  constexpr int kTiles = (kGlu ? 2 : 1) * NT;
   const int rows = kGlu ? g.inter : g.hidden;
-  const int max_units = n_edges * (rows / (16 * kMfmaTiles));
-  const int grid = std::max(1, std::min(2 * std::max(1, device_cu_count()), max_units));
-  const unsigned lds = (unsigned)(2 * kMfmaWaves * kTiles * 64 * sizeof(v4f));
-  const void* kfn = reinterpret_cast<const void*>(k_verify_mfma<kGlu, kMfmaTiles, T>);
-  if (!lds_fits(kfn, 64 * kMfmaWaves, lds))
+  const int S = mfma_waves(kGlu ? g.hidden : g.inter, kTiles,
+                          kGlu ? K3_MFMA_GLU_WAVES : K3_MFMA_DOWN_WAVES);
+  if (S < 1) return fail(K3_HIP_E_INVALID, "verify: no column split fits this geometry");
+  const int max_units = n_edges * (rows / (16 * NT));
+  // eight resident waves per CU (two per SIMD, the kernel's register budget)
+  const int grid = std::max(1, std::min((8 / S) * std::max(1, device_cu_count()), max_units));
+  const unsigned lds = (unsigned)(2 * S * kTiles * 64 * sizeof(v4f) +
+                                  (size_t)S * 64 * kScaleLoads * sizeof(uint32_t));
+  const void* kfn = reinterpret_cast<const void*>(k_verify_mfma<kGlu, NT, T, kItemSteps>);
+  if (!lds_fits(kfn, 64 * S, lds))
     return fail(K3_HIP_E_EXEC, "verify: %u B of LDS per workgroup not available", lds);
   TimedLaunch tl(kGlu ? KC_GLU_MFMA : KC_DOWN_MFMA, st);
-  launch_timed(tl, k_verify_mfma<kGlu, kMfmaTiles, T>, dim3(grid), dim3(64 * kMfmaWaves), lds, st,
-               g, ws, bq, bqs, n_brows, out);
+  launch_timed(tl, k_verify_mfma<kGlu, NT, T, kItemSteps>, dim3(grid), dim3(64 * S), lds, st, g,
+               ws, bq, bqs, n_brows, out);
   return launched(tl, kGlu ? "verify gate/up (mfma) launch" : "verify down (mfma) launch");
 }
 
 }  // namespace
 
 bool verify_mfma_supported(const Geo& g) {
-  // K steps of 128 split evenly over the column waves, whole 64-row units.
-  return g.layout == K3_LAYOUT_RAW_V1 && g.hidden % (128 * kMfmaWaves) == 0 &&
-         g.inter % (128 * kMfmaWaves) == 0 && g.hidden % (16 * kMfmaTiles) == 0 &&
-         g.inter % (16 * kMfmaTiles) == 0;
+  // Whole K-step pairs (256 elements) per column wave, whole units of rows.
+  constexpr int kGluTiles = 2 * unit_tiles<true, 2>(), kDownTiles = unit_tiles<false, 3>();
+  static_assert(unit_tiles<true, 2>() == unit_tiles<true, 3>(), "one gate/up unit shape");
+  return g.layout == K3_LAYOUT_RAW_V1 && g.hidden % 128 == 0 && g.inter % 128 == 0 &&
+         g.inter % (16 * unit_tiles<true, 2>()) == 0 && g.hidden % (16 * kDownTiles) == 0 &&
+         mfma_waves(g.hidden, kGluTiles, K3_MFMA_GLU_WAVES) > 0 &&
+         mfma_waves(g.inter, kDownTiles, K3_MFMA_DOWN_WAVES) > 0;
 }
 
 int launch_verify_mfma(const Geo& g, int n_edges, int n_positions, const void* x, int x_dtype,

@@ -355,11 +355,14 @@ int k3_hip_set_fused_decode(int enabled);
 
 /* ============================== verify path selection */
 /* No reference counterpart.  How the two verify calls above run:
- *   K3_VERIFY_AUTO (default): batches of two or more positions go through the
- *     matrix-core union path where the geometry allows it (raw-v1 spans,
- *     hidden and intermediate multiples of 512) and no expert carries more
- *     than 16 edges; otherwise one decode layer per position, or the union
- *     VALU kernels when a caller route's positions share most experts;
+ *   K3_VERIFY_AUTO (default): batches of two or more positions whose unique
+ *     experts are at most 77% of their edges (exactly, for a caller route;
+ *     the expected union of independent routes, for device routing) go
+ *     through the matrix-core union path where it applies (raw-v1 spans,
+ *     hidden and intermediate multiples of 256, at most 16 edges per
+ *     expert); otherwise one decode layer per position, or the union VALU
+ *     kernels when the matrix-core path does not apply and a caller route's
+ *     positions share most experts;
  *   K3_VERIFY_POSITIONS: one decode layer per position (an expert chosen by
  *     several positions is read once per position, as in the reference);
  *   K3_VERIFY_UNION_MFMA: every routed expert read once per batch and
