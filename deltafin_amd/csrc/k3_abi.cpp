@@ -607,7 +607,7 @@ int positions_locked(Context& c, const Geo& lg, const uint8_t* const* blobs, int
     rc = launch_verify_plan_table(tbl, ws, c.stream);
     if (rc == K3_HIP_OK)
       rc = launch_verify_layer(c.geo, n_edges, n_pos, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws,
-                               false, c.stream);
+                               c.stream);
   }
   if (rc == K3_HIP_OK &&
       (e = hipMemcpyAsync(c.hout, c.dout, bytes, hipMemcpyDeviceToHost, c.stream)) != hipSuccess)
@@ -1004,8 +1004,7 @@ int k3_hip_moe_verify_route_device(const K3HipGeometryV1* gd, const uint8_t* ban
       rc = launch_verify_plan_bank(g, bank, expert_stride, n_positions, top_k, ws, st);
     if (rc != K3_HIP_OK) return rc;
     return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
-                : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws,
-                                      true, st);
+                : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
   }
   // One routed decode layer per position, in order on the stream: each
   // position's gate/up kernel ranks its own logits, so the routes equal the
@@ -1106,8 +1105,7 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
     int rc = launch_verify_plan_table(tbl, ws, st);
     if (rc != K3_HIP_OK) return rc;
     return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
-                : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws,
-                                      false, st);
+                : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
   }
   const size_t xb = x_dtype == K3_DTYPE_BF16 ? 2 : 4, ob = out_dtype == K3_DTYPE_BF16 ? 2 : 4;
   for (int p = 0; p < n_positions; ++p) {

@@ -126,11 +126,10 @@ int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride,
                             hipStream_t stream);
 int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws,
                              hipStream_t stream);
-// pipelined: the plan came from the device router (rank-sorted plan); the
-// pipelined verify kernels then run where they are enabled.
+// The VALU union verify kernels over the plan in ws, then the combine.
 int launch_verify_layer(const Geo& g, int n_edges, int n_positions,
                         const void* x, int x_dtype, void* out, int out_dtype,
-                        const Workspace& ws, bool pipelined, hipStream_t stream);
+                        const Workspace& ws, hipStream_t stream);
 // Per-position route-ordered combine of ws.y (edge outputs) into out.
 int launch_verify_combine(const Geo& g, int n_positions, void* out, int out_dtype,
                           const Workspace& ws, hipStream_t stream);

@@ -672,7 +672,7 @@ struct DownBatch {
 // holds the nibble of group cc[c] of row r (flattened index r * GB + cc[c];
 // GB is even, so the nibble is the high one exactly when cc[c] is odd), and
 // down_dots turns it into base + index.
-template <int CPL, int kB, bool kG, bool kRs = false, bool kS4 = false>
+template <int CPL, int kB, bool kG, bool kS4 = false>
 __device__ __forceinline__ void down_load(DownBatch<CPL, kB, kG>& bt, const uint8_t* span,
                                           const Geo& g, const int* cc, int r0, int nrows) {
   static_assert(!kS4 || !kG, "scale4-v2 down loads use the byte-scale path");
@@ -688,22 +688,11 @@ __device__ __forceinline__ void down_load(DownBatch<CPL, kB, kG>& bt, const uint
     // scalar-base form of the load: no per-row address registers).
     const int d = min(cc[0], nrows * 16 - 1);
     const uint32_t lo = (uint32_t)cc[0] << 4;
-    if constexpr (kRs) {
-      const Rsrc rp = make_rsrc(dp, (uint32_t)(g.hidden * cpb));
-      const Rsrc rs = make_rsrc(ds, (uint32_t)(g.hidden * 64));
-      bt.s[0][0] = rsrc_load_u32(rs, (uint32_t)(4 * d), (uint32_t)r0 * 64u);
+    bt.s[0][0] = load_u32(ds + (size_t)r0 * 64 + 4 * d);
 #pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        const int r = r0 + min(u, nrows - 1);
-        bt.w[u][0] = rsrc_load_chunk_nt(rp, lo, (uint32_t)r * (uint32_t)cpb);
-      }
-    } else {
-      bt.s[0][0] = load_u32(ds + (size_t)r0 * 64 + 4 * d);
-#pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        const int r = r0 + min(u, nrows - 1);
-        bt.w[u][0] = load_chunk(dp + (size_t)r * cpb + lo);
-      }
+    for (int u = 0; u < kB; ++u) {
+      const int r = r0 + min(u, nrows - 1);
+      bt.w[u][0] = load_chunk(dp + (size_t)r * cpb + lo);
     }
   } else {
 #pragma unroll
@@ -856,9 +845,9 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
     XChunk<float> hs[CPLB];
     load_h_slice<CPLB>(hs, h + (size_t)e * g.inter, cc, valid);
     DownBatch<CPLB, kB> A, B;
-    down_load<CPLB, kB, false, false, kS4>(A, span, g, cc, row_of(0), rows_in(0));
+    down_load<CPLB, kB, false, kS4>(A, span, g, cc, row_of(0), rows_in(0));
     const int b1 = min(1, nb - 1);
-    down_load<CPLB, kB, false, false, kS4>(B, span, g, cc, row_of(b1), rows_in(b1));
+    down_load<CPLB, kB, false, kS4>(B, span, g, cc, row_of(b1), rows_in(b1));
     for (int b = 0;; b += 2) {
       const float va = down_dots<CPLB, kB, false, kS4>(A, hs, lane, base, shift4);
       if (writer && idx < rows_in(b)) ybuf[e][b * kB + idx] = va;
@@ -869,7 +858,7 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
         }
         break;
       }
-      down_load<CPLB, kB, false, false, kS4>(A, span, g, cc, row_of(b + 2), rows_in(b + 2));
+      down_load<CPLB, kB, false, kS4>(A, span, g, cc, row_of(b + 2), rows_in(b + 2));
       const float vb = down_dots<CPLB, kB, false, kS4>(B, hs, lane, base, shift4);
       if (writer && idx < rows_in(b + 1)) ybuf[e][(b + 1) * kB + idx] = vb;
       if (b + 3 >= nb) {
@@ -877,7 +866,7 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
         if (writer && idx < rows_in(b + 2)) ybuf[e][(b + 2) * kB + idx] = va2;
         break;
       }
-      down_load<CPLB, kB, false, false, kS4>(B, span, g, cc, row_of(b + 3), rows_in(b + 3));
+      down_load<CPLB, kB, false, kS4>(B, span, g, cc, row_of(b + 3), rows_in(b + 3));
     }
   }
   __syncthreads();
@@ -1396,7 +1385,8 @@ __global__ __launch_bounds__(256) void k_verify_plan_table(const EdgeTable tbl,
 }
 
 // ======================================================================
-// verify phase A, first design (every shape but the pipelined one below):
+// verify phase A on the VALU (the union path where the matrix-core one does
+// not apply):
 // one workgroup per (unique expert, 32-row block); the expert's positions are
 // staged in LDS a group at a time
 // ======================================================================
@@ -1472,141 +1462,6 @@ __global__ __launch_bounds__(256) void k_glu_verify_rows(const Geo g, const XT* 
 }
 
 // ======================================================================
-// verify phase A: the decode gate/up pipeline over the verify plan
-// ======================================================================
-// A unit is kR rows of one unique expert's gate and up matrices; its bytes
-// are read once and applied to every position that routed to the expert
-// (sorted edges uoff[u] .. uoff[u + 1] of the plan, staged in LDS).  A
-// workgroup is one pipeline of S column-split waves, so its barriers stay
-// uniform whatever the number of positions of its unit.  The x chunk of a
-// unit's first position travels with its weights in the double buffer; the
-// next position's chunk is requested before the first position's dots, and
-// further ones (an expert picked by three or more positions) when needed.
-template <typename XT, int kR, bool kG>
-struct GluVBatch {
-  GluBatch<XT, kR, kG> w;
-  XChunk<XT> x0;
-};
-
-template <typename XT, int kR, bool kG>
-__global__ __launch_bounds__(256, 2) void k_glu_verify(const Geo g, const XT* __restrict__ x,
-                                                    const Workspace ws, int S) {
-  constexpr int N = 2 * kR;
-  constexpr int L = log2c<N>();
-  __shared__ float red[2][4][N];
-  __shared__ int s_uoff[K3_HIP_MAX_EDGES + 1];
-  __shared__ int s_edge[K3_HIP_MAX_EDGES];
-  __shared__ int s_pos[K3_HIP_MAX_EDGES];
-  __shared__ uint64_t s_span[K3_HIP_MAX_EDGES];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;  // column slice of the workgroup's pipeline
-  const int G = g.hidden >> 5;
-  const ColSplit cs = col_split(G, S, wave, lane);
-  const GluGather gg = glu_gather(G, S, wave, lane, kR);
-  const int row_step = (G + S - 1) / S;
-  const int U = ws.plan->n_unique;
-  const int E = ws.plan->n_edges;
-  for (int i = threadIdx.x; i <= U; i += blockDim.x) s_uoff[i] = ws.uoff[i];
-  for (int i = threadIdx.x; i < U; i += blockDim.x)
-    s_span[i] = reinterpret_cast<uint64_t>(ws.uptr[i]);
-  for (int i = threadIdx.x; i < E; i += blockDim.x) {
-    const int e = ws.uedges[i];
-    s_edge[i] = e;
-    s_pos[i] = ws.epos[e];
-  }
-  __syncthreads();
-  const int upe = g.inter / kR;
-  const int n_units = U * upe;
-  // Workgroup q takes units q, q + Q, ...; every workgroup runs the same
-  // number of iterations (a unit past the end repeats unit 0 and stores
-  // nothing).  U is the same for the whole grid.
-  const int Q = gridDim.x;
-  const int iters = (n_units + Q - 1) / Q;
-  if (iters == 0) return;
-  const int q0 = blockIdx.x;
-  auto unit_at = [&](int it) {
-    const int u = q0 + it * Q;
-    return u < n_units ? u : 0;
-  };
-  auto load = [&](GluVBatch<XT, kR, kG>& bt, int it) {
-    const int unit = unit_at(it);
-    const int uid = unit / upe;
-    const uint8_t* spu = uniform_ptr(reinterpret_cast<const uint8_t*>(s_span[uid]));
-    glu_load_rows(bt.w, spu, g, (unit - uid * upe) * kR, cs, gg);
-    load_x_chunk<XT>(bt.x0, x + (size_t)s_pos[s_uoff[uid]] * g.hidden, cs);
-  };
-  int nbar = 0;  // barriers passed (uniform): selects the red buffer
-  auto finish = [&](const GluVBatch<XT, kR, kG>& bt, int it) {
-    const bool live = q0 + it * Q < n_units;
-    const int unit = unit_at(it);
-    const int uid = unit / upe;
-    const int r0 = (unit - uid * upe) * kR;
-    const int t0 = s_uoff[uid], m = s_uoff[uid + 1] - t0;
-    float sg[kR], su[kR];
-#pragma unroll
-    for (int r = 0; r < kR; ++r) {
-      if constexpr (kG) {
-        sg[r] = e8m0_scale(gathered_scale(bt.w.sg[0], gg.bp, row_step, r, lane));
-        su[r] = e8m0_scale(gathered_scale(bt.w.su[0], gg.bp, row_step, r, lane));
-      } else {
-        sg[r] = e8m0_scale(bt.w.sg[r]);
-        su[r] = e8m0_scale(bt.w.su[r]);
-      }
-    }
-    auto edge_out = [&](const XChunk<XT>& xk, int k) {
-      float v[N];
-#pragma unroll
-      for (int r = 0; r < kR; ++r) {
-        // Opaque copies: decoding the codes again per position costs a few
-        // instructions; hoisting the decoded values out of the position loop
-        // would hold 16 registers per chunk.
-        u32x4 wg = bt.w.wg[r], wu = bt.w.wu[r];
-        asm volatile("" : "+v"(wg), "+v"(wu));
-        v[r] = xk.dot(wg) * sg[r];
-        v[kR + r] = xk.dot(wu) * su[r];
-      }
-      wave_reduce_multi<N>(v, lane);
-      const int par = nbar & 1;
-      if ((lane & ((1 << (6 - L)) - 1)) == 0) red[par][wave][lane >> (6 - L)] = v[0];
-      lds_barrier();
-      ++nbar;
-      if (live && wave == 0 && lane < kR) {
-        float gv = red[par][0][lane], uv = red[par][0][kR + lane];
-        for (int w = 1; w < S; ++w) {
-          gv += red[par][w][lane];
-          uv += red[par][w][kR + lane];
-        }
-        ws.h[(size_t)s_edge[t0 + k] * g.inter + r0 + lane] = activate(g.act, gv, uv);
-      }
-    };
-    XChunk<XT> xk;
-    if (m > 1) load_x_chunk<XT>(xk, x + (size_t)s_pos[t0 + 1] * g.hidden, cs);
-    edge_out(bt.x0, 0);
-    for (int k = 1; k < m; ++k) {
-      if (k > 1) load_x_chunk<XT>(xk, x + (size_t)s_pos[t0 + k] * g.hidden, cs);
-      edge_out(xk, k);
-    }
-  };
-  GluVBatch<XT, kR, kG> A, B;
-  load(A, 0);
-  load(B, min(1, iters - 1));
-  for (int it = 0;; it += 2) {
-    finish(A, it);
-    if (it + 2 >= iters) {
-      if (it + 1 < iters) finish(B, it + 1);
-      break;
-    }
-    load(A, it + 2);
-    finish(B, it + 1);
-    if (it + 3 >= iters) {
-      finish(A, it + 2);
-      break;
-    }
-    load(B, it + 3);
-  }
-}
-
-// ======================================================================
 // verify phase B: one workgroup per (unique expert, row block); each wave
 // holds the h slices of up to kE edges and streams its rows once per group
 // ======================================================================
@@ -1664,116 +1519,6 @@ __global__ __launch_bounds__(256) void k_down_verify(const Geo g, const Workspac
           if (lane == 0) ws.y[(size_t)edge[t] * g.hidden + row] = v;
         }
       }
-    }
-  }
-}
-
-// Two h slices against one gathered-scale batch: 8 partials (slice i >> 2,
-// row i & 3) reduced together; lane l ends with value l >> 3.
-__device__ __forceinline__ float down_dots2(const DownBatch<1, 4, true>& bt,
-                                            const XChunk<float>& h0, const XChunk<float>& h1,
-                                            int lane) {
-  float v[8];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const uint32_t word =
-        (uint32_t)__builtin_amdgcn_ds_bpermute((16 * u + (lane >> 2)) << 2, (int)bt.s[0][0]);
-    const float sc = e8m0_scale((word >> (8 * (lane & 3))) & 0xffu);
-    float a, b;
-    chunk_dot_f32_x2(bt.w[u][0], h0.v, h1.v, a, b);
-    v[u] = a * sc;
-    v[4 + u] = b * sc;
-  }
-  wave_reduce_multi<8>(v, lane);
-  return v[0];
-}
-
-// ======================================================================
-// verify phase B for intermediate 2048: down rows of every unique expert
-// ======================================================================
-// A wave owns units (unique expert u, run of kDVSlots 4-row batches of its
-// down matrix).  For each pair of the expert's edges (or its last single
-// edge) the wave transposes the h slices through its LDS regions and streams
-// the unit's rows in a fully unrolled double buffer (gathered scales),
-// writing y[edge][row]; an expert with more edges streams its rows once per
-// pair.  Slots past the unit's end re-read its last batch and store nothing.
-constexpr int kDVSlots = 16;
-
-template <bool kTwo>
-__device__ __forceinline__ void down_verify_pass(const Geo& g, const Workspace& ws,
-                                                 const uint8_t* span, int e0, int e1, int b0,
-                                                 int nb, float4* hw0, float4* hw1, float* yw,
-                                                 int lane) {
-  constexpr int kB = 4;
-  XChunk<float> hs0, hs1;
-  {
-    float4 ht[8];
-    h_slice_issue(ht, ws.h + (size_t)e0 * g.inter, lane);
-    h_slice_transpose(hs0, ht, hw0, lane);
-    if constexpr (kTwo) {
-      h_slice_issue(ht, ws.h + (size_t)e1 * g.inter, lane);
-      h_slice_transpose(hs1, ht, hw1, lane);
-    }
-  }
-  const int cc[1] = {lane};
-  auto row_of = [&](int i) { return (b0 + min(i, nb - 1)) * kB; };
-  auto rows_in = [&](int i) { return min(kB, g.hidden - row_of(i)); };
-  DownBatch<1, kB, true> bt[2];
-  down_load<1, kB, true, true>(bt[0], span, g, cc, row_of(0), rows_in(0));
-  down_load<1, kB, true, true>(bt[1], span, g, cc, row_of(1), rows_in(1));
-#pragma unroll
-  for (int b = 0; b < kDVSlots; ++b) {
-    float v;
-    if constexpr (kTwo)
-      v = down_dots2(bt[b & 1], hs0, hs1, lane);
-    else
-      v = down_dots(bt[b & 1], &hs0, lane);
-    if (b + 2 < kDVSlots)
-      down_load<1, kB, true, true>(bt[b & 1], span, g, cc, row_of(b + 2), rows_in(b + 2));
-    // Results go to the wave's LDS row buffer yw[edge slot][slot row] and to
-    // memory after the loop: global stores share the load counter, and
-    // interleaving them with the weight loads makes every wait a full drain.
-    if constexpr (kTwo) {
-      const int i8 = lane >> 3;
-      if ((lane & 7) == 0) yw[(i8 >> 2) * (kDVSlots * kB) + b * kB + (i8 & 3)] = v;
-    } else {
-      if ((lane & 15) == 0) yw[b * kB + (lane >> 4)] = v;
-    }
-  }
-  const int rows = min(kDVSlots * kB, g.hidden - b0 * kB);
-  if (lane < rows) {
-    ws.y[(size_t)e0 * g.hidden + b0 * kB + lane] = yw[lane];
-    if constexpr (kTwo) ws.y[(size_t)e1 * g.hidden + b0 * kB + lane] = yw[kDVSlots * kB + lane];
-  }
-}
-
-__global__ __launch_bounds__(512) void k_down_verify64(const Geo g, const Workspace ws) {
-  extern __shared__ float4 hbuf[];  // 2 * kHSliceF4 float4 per wave
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPR
-  const int nw = blockDim.x >> 6;
-  const int U = ws.plan->n_unique;
-  const int total_w = gridDim.x * nw;
-  const int nbt = (g.hidden + 3) / 4;
-  const int upe = (nbt + kDVSlots - 1) / kDVSlots;
-  const int n_units = U * upe;
-  float4* hw0 = hbuf + (2 * wave) * kHSliceF4;
-  float4* hw1 = hw0 + kHSliceF4;
-  __shared__ float ybuf[16][2 * kDVSlots * 4];
-  float* yw = ybuf[wave];
-  for (int unit = blockIdx.x * nw + wave; unit < n_units; unit += total_w) {
-    const int uid = unit / upe;
-    const int b0 = (unit - uid * upe) * kDVSlots;
-    const int nb = min(kDVSlots, nbt - b0);
-    const uint8_t* span = ws.uptr[uid];
-    const int t0 = ws.uoff[uid], m = ws.uoff[uid + 1] - t0;
-    for (int k0 = 0; k0 < m; k0 += 2) {
-      const int e0 = ws.uedges[t0 + k0];
-      if (k0 + 1 < m)
-        down_verify_pass<true>(g, ws, span, e0, ws.uedges[t0 + k0 + 1], b0, nb, hw0, hw1, yw,
-                               lane);
-      else
-        down_verify_pass<false>(g, ws, span, e0, e0, b0, nb, hw0, hw1, yw, lane);
     }
   }
 }
@@ -2238,31 +1983,9 @@ int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws, hipStr
 
 namespace {
 
-// The pipelined verify kernels (rank-sorted plan, k_glu_verify,
-// k_down_verify64) are switched off: they passed their parity tests on a
-// 48-expert bank, but a timing run over a 384-expert bank faulted the GPU
-// and no cause has been found yet.  Every verify call runs the first-design
-// kernels until one is.
-constexpr bool kVerifyPipelinedEnabled = false;
-
-bool verify_pipelined(const Geo& g, int x_dtype, bool device_plan) {
-  return kVerifyPipelinedEnabled && device_plan && x_dtype == K3_DTYPE_BF16 &&
-         g.hidden == 7168 && g.inter == 2048;
-}
-
 template <typename XT>
 int glu_verify_dispatch(const Geo& g, int n_edges, const XT* x, const Workspace& ws,
-                        bool pipelined, hipStream_t st) {
-  if (pipelined) {
-    const int G = g.hidden / 32;
-    const int S = (G + 63) / 64;  // 4
-    // Eight waves per CU: 8 / S single-pipeline workgroups per CU.
-    const int grid = std::max(1, device_cu_count()) * (8 / S);
-    TimedLaunch tl(KC_GLU_VERIFY, st);
-    launch_timed(tl, (k_glu_verify<XT, kRowsGlu, true>), dim3(grid), dim3(64 * S), 0, st, g, x,
-                 ws, S);
-    return launched(tl, "verify gate/up launch");
-  }
+                        hipStream_t st) {
   constexpr int kG = VerifyA<XT>::kGroup;
   const size_t lds = (size_t)kG * g.hidden * sizeof(XT);
   if (lds > 96 * 1024) return fail(K3_HIP_E_INVALID, "verify: hidden %d too wide", g.hidden);
@@ -2273,19 +1996,8 @@ int glu_verify_dispatch(const Geo& g, int n_edges, const XT* x, const Workspace&
   return launched(tl, "verify gate/up launch");
 }
 
-int down_verify_dispatch(const Geo& g, int n_edges, const Workspace& ws, bool pipelined,
-                         hipStream_t st) {
+int down_verify_dispatch(const Geo& g, int n_edges, const Workspace& ws, hipStream_t st) {
   const int GB = g.inter / 32;
-  if (pipelined) {
-    const int nw = 8;
-    const unsigned lds = (unsigned)(nw * 2 * kHSliceF4 * sizeof(float4));
-    if (!lds_fits((const void*)k_down_verify64, 64 * nw, lds))
-      return fail(K3_HIP_E_EXEC, "verify: %u B of LDS per workgroup not available", lds);
-    TimedLaunch tl(KC_DOWN_VERIFY, st);
-    launch_timed(tl, k_down_verify64, dim3(std::max(1, device_cu_count())), dim3(64 * nw), lds, st,
-                 g, ws);
-    return launched(tl, "verify down launch");
-  }
   const int cplb = (GB + 63) / 64;
   const int upe = (g.hidden + 4 * kRowsVerifyB - 1) / (4 * kRowsVerifyB);
   const dim3 grid(upe * n_edges), block(256);
@@ -2304,18 +2016,14 @@ int down_verify_dispatch(const Geo& g, int n_edges, const Workspace& ws, bool pi
 }  // namespace
 
 int launch_verify_layer(const Geo& g, int n_edges, int n_positions, const void* x, int x_dtype,
-                        void* out, int out_dtype, const Workspace& ws, bool device_plan,
-                        hipStream_t st) {
+                        void* out, int out_dtype, const Workspace& ws, hipStream_t st) {
   if (g.inter % (4 * kRowsVerifyA) != 0)
     return fail(K3_HIP_E_INVALID, "verify: intermediate must be a multiple of 32");
-  const bool pipelined = verify_pipelined(g, x_dtype, device_plan);
   int rc = x_dtype == K3_DTYPE_BF16
-               ? glu_verify_dispatch<uint16_t>(g, n_edges, static_cast<const uint16_t*>(x), ws,
-                                               pipelined, st)
-               : glu_verify_dispatch<float>(g, n_edges, static_cast<const float*>(x), ws,
-                                            pipelined, st);
+               ? glu_verify_dispatch<uint16_t>(g, n_edges, static_cast<const uint16_t*>(x), ws, st)
+               : glu_verify_dispatch<float>(g, n_edges, static_cast<const float*>(x), ws, st);
   if (rc != K3_HIP_OK) return rc;
-  rc = down_verify_dispatch(g, n_edges, ws, pipelined, st);
+  rc = down_verify_dispatch(g, n_edges, ws, st);
   if (rc != K3_HIP_OK) return rc;
   return launch_verify_combine(g, n_positions, out, out_dtype, ws, st);
 }
