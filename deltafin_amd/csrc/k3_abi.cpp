@@ -634,10 +634,11 @@ int check_dtype(int d) { return d == K3_DTYPE_F32 || d == K3_DTYPE_BF16; }
 std::atomic<int> g_verify_mode{K3_VERIFY_AUTO};
 
 // AUTO picks the matrix-core union path when the batch's unique experts are
-// at most this fraction of its edges: the union kernels stream about 1/1.3 of
-// the decode kernels' rate on MI355X (config 3: ~4.6 vs ~6 TB/s), so they win
-// once they read under 1/1.3 of the bytes.
-constexpr double kUnionFraction = 0.77;
+// at most this fraction of its edges: per byte the union path (5-6.4 TB/s in
+// its two kernels, plus five small launches) costs about 1.08x what one decode
+// layer per position does on MI355X (config 3), so it wins once it reads
+// under ~92 % of the bytes.
+constexpr double kUnionFraction = 0.92;
 
 // Expected unique experts of n_positions independent top_k routes over n_bank
 // experts (uniform routing, the least sharing a verify batch can have).

@@ -356,7 +356,7 @@ int k3_hip_set_fused_decode(int enabled);
 /* ============================== verify path selection */
 /* No reference counterpart.  How the two verify calls above run:
  *   K3_VERIFY_AUTO (default): batches of two or more positions whose unique
- *     experts are at most 77% of their edges (exactly, for a caller route;
+ *     experts are at most 92% of their edges (exactly, for a caller route;
  *     the expected union of independent routes, for device routing) go
  *     through the matrix-core union path where it applies (raw-v1 spans,
  *     hidden and intermediate multiples of 256, at most 16 edges per
