@@ -746,7 +746,7 @@ def _verify_config3(moe, _lib, g, bank, stride, batches: int) -> dict:
     """batched speculative verify over the same resident
     bank: M positions, each with its own top-16 of 384 N(0,1) logits and bf16
     x.  Each M is timed on the library's default path (AUTO: the matrix-core
-    union kernels when the expected union is under 77% of the edges, else one
+    union kernels when the expected union is under 92% of the edges, else one
     decode layer per position) and on both paths explicitly.  A second case,
     `shared_M16`, gives 16 positions logits with a common N(0,1) component
     (logits = z_common + 0.5 z_position, as consecutive draft tokens of one

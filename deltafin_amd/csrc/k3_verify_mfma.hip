@@ -487,7 +487,7 @@ int down_tiles(const Geo& g) { return g.hidden % 56 == 0 ? 7 : 4; }
 #define K3_MFMA_GLU_WAVES 4
 #endif
 #ifndef K3_MFMA_DOWN_WAVES
-#define K3_MFMA_DOWN_WAVES 1  // down rows have K = intermediate: longer units per wave
+#define K3_MFMA_DOWN_WAVES 2  // down rows have K = intermediate: longer units per wave
 #endif
 
 // Column-split waves for K = k_elems and kTiles tiles per unit: the preferred
