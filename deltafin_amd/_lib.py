@@ -1,4 +1,5 @@
-"""ctypes binding of libk3hipmoe.so (the C ABI in include/k3_hip_moe_abi.h).
+"""ctypes binding of libk3hipmoe.so (the C ABI in include/k3_hip_moe_abi.h and
+include/k3_hip_spine_abi.h).
 
 The library is loaded after torch so that it binds to the HIP runtime torch
 already mapped (both carry the SONAME libamdhip64.so.7); loading fails loudly if
@@ -84,7 +85,7 @@ _i64 = C.c_int64
 _GP = C.POINTER(K3HipGeometryV1)
 _DP = C.POINTER(K3HipExpertDescriptorV1)
 
-# name -> (restype, argtypes); every symbol declared in include/k3_hip_moe_abi.h
+# name -> (restype, argtypes); every symbol declared in include/*.h
 SIGNATURES = {
     "k3_hip_geometry_span": (_u64, [_u32, _u32]),
     "k3_hip_geometry_preset": (_i32, [_i32, _GP]),
@@ -137,6 +138,14 @@ SIGNATURES = {
     "k3_hip_scale4_check_header": (_i32, [_vp, _u64]),
     "k3_hip_synth_bank": (_i32, [_GP, _vp, _u64, _i32, _u64, _u64, _i32, _i32, _vp]),
     "k3_hip_synth_normal": (_i32, [_vp, _i32, _u64, _u64, _u64, _vp]),
+    # include/k3_hip_spine_abi.h
+    "k3_hip_spine_bf16_abi_version": (_u32, []),
+    "k3_hip_spine_last_error": (C.c_char_p, []),
+    "k3_hip_spine_bf16_available": (_i32, [_i32, C.POINTER(_i32), C.POINTER(_i32)]),
+    "k3_hip_spine_bf16_launch_v1": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "k3_hip_spine_bf16_decode_bits": (_i32, [_vp, _vp, _i32, _vp]),
+    "k3_hip_spine_int8_launch_v1": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "k3_hip_rms_norm": (_i32, [_vp, _vp, _vp, _i32, _i32, C.c_float, _vp]),
 }
 
 _LIB: C.CDLL | None = None
@@ -194,6 +203,28 @@ def last_error() -> str:
 def check(status: int, what: str) -> None:
     if status != K3_HIP_OK:
         raise K3HipError(status, what)
+
+
+K3_SPINE_OK = 0
+K3_SPINE_E_INVALID = -1
+K3_SPINE_E_RUNTIME = -2
+K3_SPINE_E_UNSUPPORTED = -3
+K3_SPINE_MAX_POSITIONS = 64
+K3_RMS_EPS = 1.0e-5  # the reference's kRmsEpsilon (provider_moe.cpp:87)
+
+
+class K3SpineError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        lib = _LIB if _LIB is not None else load()
+        msg = lib.k3_hip_spine_last_error()
+        super().__init__(f"{what} failed with status {status}: "
+                         f"{msg.decode(errors='replace') if msg else ''}")
+        self.status = status
+
+
+def check_spine(status: int, what: str) -> None:
+    if status != K3_SPINE_OK:
+        raise K3SpineError(status, what)
 
 
 def geometry(hidden: int, intermediate: int, activation: int) -> K3HipGeometryV1:

@@ -49,8 +49,8 @@ CXX_FLAGS = [
     "-Wextra",
     "-Wno-unused-parameter",
 ]
-KERNEL_SOURCES = ["k3_kernels.hip", "k3_verify_mfma.hip"]
-HOST_SOURCES = ["k3_abi.cpp", "k3_cache.cpp", "k3_timing.cpp"]
+KERNEL_SOURCES = ["k3_kernels.hip", "k3_verify_mfma.hip", "k3_spine.hip"]
+HOST_SOURCES = ["k3_abi.cpp", "k3_cache.cpp", "k3_timing.cpp", "k3_spine_abi.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

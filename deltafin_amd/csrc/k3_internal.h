@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "../../include/k3_hip_moe_abi.h"
+#include "../../include/k3_hip_spine_abi.h"
 
 namespace k3 {
 
@@ -168,6 +169,8 @@ enum KernelClass : int {
   KC_SPLIT,
   KC_GLU_MFMA,
   KC_DOWN_MFMA,
+  KC_SPINE,
+  KC_RMS_NORM,
   KC_COUNT
 };
 
@@ -187,5 +190,15 @@ class TimedLaunch {
  private:
   int slot_;
 };
+
+// Spine projections (k3_spine.hip).  Statuses are the K3_SPINE_* codes of the
+// spine surface; failures record their reason through spine_fail.
+enum { K3_SPINE_KIND_BF16 = 0, K3_SPINE_KIND_INT8 = 1 };
+int spine_fail(int status, const char* fmt, ...);
+int spine_gemv(int kind, const void* weights, const float* row_scales, const float* x,
+               float* y, int rows, int cols, int positions, hipStream_t stream);
+int spine_decode_bits(const uint16_t* in, uint32_t* out, int count, hipStream_t stream);
+int spine_rms_norm(const float* in, const float* weight, float* out, int rows, int cols,
+                   float eps, hipStream_t stream);
 
 }  // namespace k3

@@ -1,0 +1,367 @@
+// Resident spine projections around the routed experts on gfx950: the exact
+// BF16 x FP32 GEMV (replacing native/provider_gate/provider_spine_bf16_cuda.cu:
+// 95-165), the row-int8 x FP32 GEMV (at::_weight_int8pack_mm as called by
+// provider_moe.cpp:507-516), the BF16 bit decode canary (:282-303) and the
+// routed RMS norm (provider_moe.cpp:535-542).
+//
+// The GEMV is HBM-bound at decode (2 bytes per BF16 weight, 1 per int8 weight,
+// one multiply-add per weight and position).  A wave owns R whole rows and
+// requests them as 1 KB pieces (16 bytes per lane, the contiguous-row access
+// that streams fastest on this part); every piece is requested before any
+// arithmetic, so R x NJ pieces per wave are in flight.  The activation of up
+// to PG positions sits in LDS, laid out so each ds_read_b128 of a wave reads
+// one contiguous KB; the weights stay in registers while the positions are
+// walked in groups of PG, so each weight byte is read from HBM once for all
+// 1..64 positions.  A row whose byte length is not a whole number of pieces
+// has a short last piece: lanes past its end load the row's first 16 bytes
+// (in bounds) and replace them by zero weights, so every lane issues the same
+// loads and the compiler's wait counts stay exact.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <utility>
+
+#include "k3_device.h"
+#include "k3_launch.h"
+
+namespace k3 {
+namespace {
+
+constexpr int kSpineThreads = 256;
+constexpr int kSpineWaves = kSpineThreads / kWave;
+constexpr int kSpineMaxNj = 16;                // pieces per row on the fast path
+constexpr uint32_t kSpineLdsBudget = 65536;    // activation bytes per workgroup
+
+template <int kKind>
+struct SpineElem;
+template <>
+struct SpineElem<K3_SPINE_KIND_BF16> {
+  static constexpr int kPerChunk = 8;  // columns per 16-byte lane chunk
+  static constexpr int kBytes = 2;
+};
+template <>
+struct SpineElem<K3_SPINE_KIND_INT8> {
+  static constexpr int kPerChunk = 16;
+  static constexpr int kBytes = 1;
+};
+
+// 16 bytes of BF16 bits -> 8 fp32 values, exactly (bits << 16).
+__device__ __forceinline__ void decode_chunk(u32x4 w, float* f, SpineElem<K3_SPINE_KIND_BF16>) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    f[2 * d] = __uint_as_float(w[d] << 16);
+    f[2 * d + 1] = __uint_as_float(w[d] & 0xffff0000u);
+  }
+}
+
+// 16 int8 values -> 16 fp32 values, exactly (byte b of each dword, sign-extended).
+__device__ __forceinline__ void decode_chunk(u32x4 w, float* f, SpineElem<K3_SPINE_KIND_INT8>) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      f[4 * d + b] = (float)((int32_t)(w[d] << (24 - 8 * b)) >> 24);
+  }
+}
+
+// LDS slot of activation column c: lane l's float4 q of piece j lives at
+// ((j * kQ + q) * 64 + l) * 4, so one ds_read_b128 of the wave reads 1 KB.
+template <int kKind>
+__device__ __forceinline__ int lds_slot(int c) {
+  constexpr int kPer = SpineElem<kKind>::kPerChunk;
+  constexpr int kQ = kPer / 4;
+  const int j = c / (64 * kPer);
+  const int in = c - j * 64 * kPer;
+  const int l = in / kPer;
+  const int q = (in - l * kPer) >> 2;
+  return ((j * kQ + q) * 64 + l) * 4 + (c & 3);
+}
+
+template <int kKind, int NJ, int R, int PG>
+__global__ __launch_bounds__(kSpineThreads, 4) void k_spine_gemv(
+    const uint8_t* __restrict__ w, const float* __restrict__ row_scale,
+    const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions,
+    int tail_lanes) {
+  using E = SpineElem<kKind>;
+  constexpr int kQ = E::kPerChunk / 4;
+  constexpr int kPad = NJ * 64 * E::kPerChunk;  // columns per staged position
+  extern __shared__ float4 xs4[];               // [PG][kPad / 4]
+  float* xs = reinterpret_cast<float*>(xs4);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const uint64_t row_bytes = (uint64_t)cols * E::kBytes;
+  const int row0 = (blockIdx.x * kSpineWaves + wave) * R;
+  const bool tail_ok = lane < tail_lanes;
+
+  u32x4 wv[R][NJ];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = min(row0 + r, rows - 1);
+    const uint8_t* base = w + (uint64_t)row * row_bytes;
+    const uint8_t* rp = base + 16 * lane;
+#pragma unroll
+    for (int j = 0; j < NJ - 1; ++j) wv[r][j] = load_chunk(rp + 1024 * j);
+    wv[r][NJ - 1] = load_chunk(tail_ok ? rp + 1024 * (NJ - 1) : base);
+  }
+
+  for (int p0 = 0; p0 < positions; p0 += PG) {
+    const int pg = min(PG, positions - p0);
+    if (p0) __syncthreads();
+    for (int p = 0; p < pg; ++p) {
+      const float* xp = x + (uint64_t)(p0 + p) * cols;
+      for (int c = 4 * threadIdx.x; c < kPad; c += 4 * kSpineThreads) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < cols) v = *reinterpret_cast<const float4*>(xp + c);
+        *reinterpret_cast<float4*>(xs + p * kPad + lds_slot<kKind>(c)) = v;
+      }
+    }
+    __syncthreads();
+
+    float acc[R][PG];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < PG; ++p) acc[r][p] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      // This piece's activation, read once for all R rows; the scheduling
+      // fence at the end keeps later pieces' reads and decodes from being
+      // hoisted here (they would hold every piece's values in registers).
+      float4 xv[PG][kQ];
+#pragma unroll
+      for (int p = 0; p < PG; ++p) {
+        if (p < pg) {
+#pragma unroll
+          for (int q = 0; q < kQ; ++q) xv[p][q] = xs4[(p * kPad) / 4 + (j * kQ + q) * 64 + lane];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        u32x4 wc = wv[r][j];
+        if (j == NJ - 1 && !tail_ok) wc = u32x4{0u, 0u, 0u, 0u};
+        // Opaque to the optimiser, so the decode is not hoisted out of the
+        // position-group loop (that would keep every decoded piece live).
+        asm volatile("" : "+v"(wc));
+        float f[E::kPerChunk];
+        decode_chunk(wc, f, E{});
+#pragma unroll
+        for (int p = 0; p < PG; ++p) {
+          if (p < pg) {
+#pragma unroll
+            for (int q = 0; q < kQ; ++q) {
+              acc[r][p] = fmaf(f[4 * q + 0], xv[p][q].x, acc[r][p]);
+              acc[r][p] = fmaf(f[4 * q + 1], xv[p][q].y, acc[r][p]);
+              acc[r][p] = fmaf(f[4 * q + 2], xv[p][q].z, acc[r][p]);
+              acc[r][p] = fmaf(f[4 * q + 3], xv[p][q].w, acc[r][p]);
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = row0 + r;
+      const float scale = kKind == K3_SPINE_KIND_INT8 ? row_scale[min(row, rows - 1)] : 1.f;
+#pragma unroll
+      for (int p = 0; p < PG; ++p) {
+        if (p < pg) {
+          float s = wave_sum(acc[r][p]);
+          if (kKind == K3_SPINE_KIND_INT8) s *= scale;
+          if (lane == 0 && row < rows) y[(uint64_t)(p0 + p) * rows + row] = s;
+        }
+      }
+    }
+  }
+}
+
+// Any shape and alignment: one wave per row, lanes stride the columns.
+template <int kKind>
+__global__ __launch_bounds__(kSpineThreads) void k_spine_gemv_generic(
+    const uint8_t* __restrict__ w, const float* __restrict__ row_scale,
+    const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * kSpineWaves + threadIdx.x / kWave;
+  if (row >= rows) return;
+  for (int p = 0; p < positions; ++p) {
+    const float* xp = x + (uint64_t)p * cols;
+    float acc = 0.f;
+    for (int c = lane; c < cols; c += kWave) {
+      const uint64_t i = (uint64_t)row * cols + c;
+      float wf;
+      if (kKind == K3_SPINE_KIND_BF16) {
+        wf = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(w)[i] << 16);
+      } else {
+        wf = (float)reinterpret_cast<const int8_t*>(w)[i];
+      }
+      acc = fmaf(wf, xp[c], acc);
+    }
+    float s = wave_sum(acc);
+    if (kKind == K3_SPINE_KIND_INT8) s *= row_scale[row];
+    if (lane == 0) y[(uint64_t)p * rows + row] = s;
+  }
+}
+
+__global__ __launch_bounds__(kSpineThreads) void k_bf16_decode_bits(const uint16_t* __restrict__ in,
+                                                                    uint32_t* __restrict__ out,
+                                                                    int count) {
+  const int i = blockIdx.x * kSpineThreads + threadIdx.x;
+  if (i < count) out[i] = (uint32_t)in[i] << 16;
+}
+
+// One workgroup per row: sum of squares in a fixed order (lane-strided fp32
+// partials, wave sums, then the four waves in order), 1 / sqrt(mean + eps),
+// then weight * (x * r) as the reference's ATen ops compose it.
+__global__ __launch_bounds__(kSpineThreads) void k_rms_norm(const float* __restrict__ in,
+                                                            const float* __restrict__ weight,
+                                                            float* __restrict__ out, int cols,
+                                                            float eps) {
+  __shared__ float part[kSpineWaves];
+  const float* xp = in + (uint64_t)blockIdx.x * cols;
+  float* op = out + (uint64_t)blockIdx.x * cols;
+  float s = 0.f;
+  for (int c = threadIdx.x; c < cols; c += kSpineThreads) s = fmaf(xp[c], xp[c], s);
+  s = wave_sum(s);
+  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = s;
+  __syncthreads();
+  float total = part[0];
+#pragma unroll
+  for (int v = 1; v < kSpineWaves; ++v) total += part[v];
+  const float r = 1.0f / sqrtf(total / (float)cols + eps);
+  __syncthreads();  // every read of xp above precedes any in-place write below
+  for (int c = threadIdx.x; c < cols; c += kSpineThreads) op[c] = weight[c] * (xp[c] * r);
+}
+
+template <int kKind, int NJ>
+int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, float* y, int rows,
+                      int cols, int positions, int tail_lanes, int pg, hipStream_t st) {
+  // Two rows per wave for short rows (int8 decodes twice the values per piece).
+  constexpr int R = NJ <= (kKind == K3_SPINE_KIND_BF16 ? 4 : 2) ? 2 : 1;
+  constexpr uint32_t kPadBytes = NJ * 64u * SpineElem<kKind>::kPerChunk * 4u;
+  const int rows_per_group = kSpineWaves * R;
+  const dim3 grid((unsigned)((rows + rows_per_group - 1) / rows_per_group));
+  TimedLaunch tl(KC_SPINE, st);
+  // Only the position groups whose activation fits the LDS budget exist.
+  if constexpr (4 * kPadBytes <= kSpineLdsBudget) {
+    if (pg == 4)
+      launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 4>), grid, dim3(kSpineThreads), 4 * kPadBytes,
+                   st, w, scales, x, y, rows, cols, positions, tail_lanes);
+  }
+  if constexpr (2 * kPadBytes <= kSpineLdsBudget) {
+    if (pg == 2)
+      launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 2>), grid, dim3(kSpineThreads), 2 * kPadBytes,
+                   st, w, scales, x, y, rows, cols, positions, tail_lanes);
+  }
+  if (pg == 1)
+    launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 1>), grid, dim3(kSpineThreads), kPadBytes, st,
+                 w, scales, x, y, rows, cols, positions, tail_lanes);
+  const bool launched_one = pg == 1 || (pg == 2 && 2 * kPadBytes <= kSpineLdsBudget) ||
+                            (pg == 4 && 4 * kPadBytes <= kSpineLdsBudget);
+  if (!launched_one) {
+    tl.failed();
+    return spine_fail(K3_SPINE_E_INVALID, "spine GEMV: no kernel for %d positions per group", pg);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return K3_SPINE_OK;
+  tl.failed();
+  return spine_fail(K3_SPINE_E_RUNTIME, "spine GEMV launch: %s", hipGetErrorString(e));
+}
+
+typedef int (*SpineFastFn)(const uint8_t*, const float*, const float*, float*, int, int, int,
+                           int, int, hipStream_t);
+
+template <int kKind, int... NJ>
+constexpr SpineFastFn spine_fast_table(int nj, std::integer_sequence<int, NJ...>) {
+  SpineFastFn table[] = {nullptr, &spine_fast_launch<kKind, NJ + 1>...};
+  return table[nj];
+}
+
+int preflight(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return K3_SPINE_OK;
+  return spine_fail(K3_SPINE_E_RUNTIME, "%s preflight: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace
+
+int spine_gemv(int kind, const void* weights, const float* row_scales, const float* x,
+               float* y, int rows, int cols, int positions, hipStream_t st) {
+  const char* what = kind == K3_SPINE_KIND_BF16 ? "RAW_BF16 GEMV" : "row-int8 GEMV";
+  if (!weights || !x || !y || (kind == K3_SPINE_KIND_INT8 && !row_scales))
+    return spine_fail(K3_SPINE_E_INVALID, "%s: null input or output pointer", what);
+  if (rows <= 0 || cols <= 0 || positions <= 0 || positions > K3_SPINE_MAX_POSITIONS)
+    return spine_fail(K3_SPINE_E_INVALID,
+                      "%s: rows/columns must be positive and positions must be 1..%d", what,
+                      K3_SPINE_MAX_POSITIONS);
+  if ((uint64_t)rows > (uint64_t)INT32_MAX / 2)
+    return spine_fail(K3_SPINE_E_INVALID, "%s: too many rows", what);
+  int rc = preflight(what);
+  if (rc != K3_SPINE_OK) return rc;
+  const auto* w = static_cast<const uint8_t*>(weights);
+  const int esize = kind == K3_SPINE_KIND_BF16 ? 2 : 1;
+  const uint64_t row_bytes = (uint64_t)cols * esize;
+  const int nj = (int)((row_bytes + 1023) / 1024);
+  const int per_position = nj * 64 * (16 / esize) * 4;  // staged activation bytes
+  const bool aligned = (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(x) & 15) == 0 && row_bytes % 16 == 0;
+  if (aligned && nj <= kSpineMaxNj && (uint32_t)per_position <= kSpineLdsBudget) {
+    // Positions per LDS group: 1, 2 or 4 (the instantiated kernels), at most
+    // what the budget holds; 3 positions take one group of 4.
+    const int fit = (int)(kSpineLdsBudget / (uint32_t)per_position);
+    const int want = positions >= 3 ? 4 : positions;
+    const int pg = std::min(want, fit >= 4 ? 4 : fit >= 2 ? 2 : 1);
+    const uint64_t tail_bytes = row_bytes - 1024ull * (nj - 1);
+    const int tail_lanes = (int)(tail_bytes / 16);
+    const auto seq = std::make_integer_sequence<int, kSpineMaxNj>{};
+    const SpineFastFn fn = kind == K3_SPINE_KIND_BF16
+                               ? spine_fast_table<K3_SPINE_KIND_BF16>(nj, seq)
+                               : spine_fast_table<K3_SPINE_KIND_INT8>(nj, seq);
+    return fn(w, row_scales, x, y, rows, cols, positions, tail_lanes, pg, st);
+  }
+  const dim3 grid((unsigned)((rows + kSpineWaves - 1) / kSpineWaves));
+  TimedLaunch tl(KC_SPINE, st);
+  if (kind == K3_SPINE_KIND_BF16)
+    launch_timed(tl, k_spine_gemv_generic<K3_SPINE_KIND_BF16>, grid, dim3(kSpineThreads), 0, st,
+                 w, row_scales, x, y, rows, cols, positions);
+  else
+    launch_timed(tl, k_spine_gemv_generic<K3_SPINE_KIND_INT8>, grid, dim3(kSpineThreads), 0, st,
+                 w, row_scales, x, y, rows, cols, positions);
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return K3_SPINE_OK;
+  tl.failed();
+  return spine_fail(K3_SPINE_E_RUNTIME, "%s launch: %s", what, hipGetErrorString(e));
+}
+
+int spine_decode_bits(const uint16_t* in, uint32_t* out, int count, hipStream_t st) {
+  if (!in || !out || count <= 0)
+    return spine_fail(K3_SPINE_E_INVALID, "RAW_BF16 decode: invalid input, output, or count");
+  int rc = preflight("RAW_BF16 decode");
+  if (rc != K3_SPINE_OK) return rc;
+  const int blocks = (int)(((int64_t)count + kSpineThreads - 1) / kSpineThreads);
+  hipLaunchKernelGGL(k_bf16_decode_bits, dim3(blocks), dim3(kSpineThreads), 0, st, in, out,
+                     count);
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return K3_SPINE_OK;
+  return spine_fail(K3_SPINE_E_RUNTIME, "RAW_BF16 decode launch: %s", hipGetErrorString(e));
+}
+
+int spine_rms_norm(const float* in, const float* weight, float* out, int rows, int cols,
+                   float eps, hipStream_t st) {
+  if (!in || !weight || !out)
+    return spine_fail(K3_SPINE_E_INVALID, "RMS norm: null input, weight or output");
+  if (rows <= 0 || cols <= 0)
+    return spine_fail(K3_SPINE_E_INVALID, "RMS norm: rows and columns must be positive");
+  if (!(eps >= 0.f) || eps == INFINITY)
+    return spine_fail(K3_SPINE_E_INVALID, "RMS norm: eps must be finite and non-negative");
+  int rc = preflight("RMS norm");
+  if (rc != K3_SPINE_OK) return rc;
+  TimedLaunch tl(KC_RMS_NORM, st);
+  launch_timed(tl, k_rms_norm, dim3(rows), dim3(kSpineThreads), 0, st, in, weight, out, cols, eps);
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return K3_SPINE_OK;
+  tl.failed();
+  return spine_fail(K3_SPINE_E_RUNTIME, "RMS norm launch: %s", hipGetErrorString(e));
+}
+
+}  // namespace k3

@@ -25,7 +25,8 @@ namespace {
 const char* const kClassNames[KC_COUNT] = {
     "gemv",        "activate",    "route",       "glu_decode", "down_decode",
     "verify_plan", "glu_verify",  "down_verify", "combine",    "synth",
-    "decode_fused", "split_terms", "glu_mfma",   "down_mfma",
+    "decode_fused", "split_terms", "glu_mfma",   "down_mfma",  "spine_gemv",
+    "rms_norm",
 };
 
 struct TimingState {

@@ -1,0 +1,143 @@
+"""CPU pins of the spine oracle (oracle/spine.py) and host-side checks of the
+spine C ABI (include/k3_hip_spine_abi.h) that need no GPU.
+
+Each oracle function is checked against something other than its own formula:
+closed-form BF16 values, pure-Python loops, linearity, one-hot inputs, the
+dense row-int8 materialisation and closed-form RMS norms.
+"""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import spine as S
+
+
+def _py_bf16(bits: int) -> float:
+    return struct.unpack("<f", struct.pack("<I", (bits & 0xFFFF) << 16))[0]
+
+
+def test_bf16_fixture_patterns_closed_form():
+    # IEEE binary32 with the low 16 bits zero: sign, 8-bit exponent, 7-bit fraction.
+    want = {
+        0x0000: 0.0, 0x0001: 2.0 ** -133, 0x007F: 127 * 2.0 ** -133, 0x0080: 2.0 ** -126,
+        0x3D00: 0.03125, 0x3E80: 0.25, 0x3F00: 0.5, 0x3F80: 1.0, 0x4000: 2.0, 0x4040: 3.0,
+        0x4080: 4.0, 0x8000: -0.0, 0xBD00: -0.03125, 0xBE80: -0.25, 0xBF00: -0.5, 0xBF80: -1.0,
+    }
+    got = S.bf16_to_f32(S.FIXTURE_PATTERNS)
+    for bits, value in zip(S.FIXTURE_PATTERNS.tolist(), got.tolist()):
+        assert value == want[bits], hex(bits)
+        assert math.copysign(1.0, value) == math.copysign(1.0, want[bits])
+
+
+def test_bf16_special_encodings():
+    bits = np.array([0x7F80, 0xFF80, 0x7FC0, 0x7F81, 0x7F7F, 0x3F81], dtype=np.uint16)
+    v = S.bf16_to_f32(bits)
+    assert v[0] == np.inf and v[1] == -np.inf
+    assert np.isnan(v[2]) and np.isnan(v[3])
+    assert v[4] == np.float32((2 - 2.0 ** -7) * 2.0 ** 127)  # largest finite BF16
+    assert v[5] == np.float32(1 + 2.0 ** -7)
+    every = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    assert np.array_equal(S.bf16_to_f32_bits(every), np.arange(65536, dtype=np.uint32) << 16)
+
+
+def test_spine_bf16_against_python_loops():
+    rng = np.random.default_rng(7)
+    w = rng.integers(0, 65536, size=(5, 37), dtype=np.uint32).astype(np.uint16)
+    w[(S.bf16_to_f32_bits(w) & 0x7F800000) == 0x7F800000] = 0x3F80  # finite only
+    x = rng.standard_normal((3, 37)).astype(np.float32)
+    got = S.spine_bf16_f64(w, x)
+    for p in range(3):
+        for r in range(5):
+            want = sum(_py_bf16(int(w[r, c])) * float(x[p, c]) for c in range(37))
+            assert got[p, r] == pytest.approx(want, rel=1e-12, abs=1e-300)
+
+
+def test_spine_bf16_linearity_and_one_hot():
+    rng = np.random.default_rng(8)
+    w = (rng.standard_normal((9, 64)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    a = rng.standard_normal((1, 64)).astype(np.float32)
+    b = rng.standard_normal((1, 64)).astype(np.float32)
+    lin = S.spine_bf16_f64(w, a) * 2.0 - S.spine_bf16_f64(w, b) * 0.5
+    both = S.spine_bf16_f64(w, (2 * a.astype(np.float64) - 0.5 * b).astype(np.float32))
+    assert np.allclose(lin, both, rtol=1e-6, atol=1e-6)
+    for c in (0, 17, 63):
+        e = np.zeros((1, 64), np.float32)
+        e[0, c] = 1.0
+        assert np.array_equal(S.spine_bf16_f64(w, e)[0], S.bf16_to_f32(w[:, c]).astype(np.float64))
+
+
+def test_spine_int8_against_dense_and_loops():
+    rng = np.random.default_rng(9)
+    q = rng.integers(-128, 128, size=(6, 48), dtype=np.int8)
+    s = rng.uniform(0.001, 0.1, size=6).astype(np.float32)
+    x = rng.standard_normal((2, 48)).astype(np.float32)
+    dense = q.astype(np.float64) * s.astype(np.float64)[:, None]  # materialize_row_int8
+    got = S.spine_int8_f64(q, s, x)
+    assert np.allclose(got, x.astype(np.float64) @ dense.T, rtol=1e-12, atol=1e-12)
+    want = [[float(s[r]) * sum(int(q[r, c]) * float(x[p, c]) for c in range(48)) for r in range(6)]
+            for p in range(2)]
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+    ones = np.ones((6, 48), np.int8)
+    assert np.allclose(S.spine_int8_f64(ones, s, x)[1], s * x[1].astype(np.float64).sum())
+
+
+def test_rms_norm_closed_forms():
+    eps = 1e-5
+    for c in (0.0, 1.0, -3.0, 1e-3):
+        x = np.full((1, 16), c, np.float32)
+        w = np.arange(1, 17, dtype=np.float32)
+        got = S.rms_norm_f64(x, w, eps)[0]
+        c = float(np.float32(c))
+        want = w.astype(np.float64) * (c / math.sqrt(c * c + float(np.float32(eps))))
+        assert np.allclose(got, want, rtol=1e-12, atol=0)
+    x = np.array([[3.0, 4.0]], np.float32)  # mean square 12.5
+    got = S.rms_norm_f64(x, np.array([1.0, 2.0], np.float32), 0.0)[0]
+    assert np.allclose(got, [3 / math.sqrt(12.5), 8 / math.sqrt(12.5)], rtol=1e-15)
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((3, 100)).astype(np.float32)
+    w = rng.standard_normal(100).astype(np.float32)
+    assert np.allclose(S.rms_norm_f64(x, w, 0.0), S.rms_norm_f64(8 * x, w, 0.0), rtol=1e-12)
+
+
+def test_reference_fixture_shapes_and_bound():
+    w, act, exp = S.spine_fixture(19, 521, 5)
+    assert w.shape == (19, 521) and act.shape == (521,) and exp.shape == (19,)
+    assert w[0, 0] == S.FIXTURE_PATTERNS[5] and w[0, 1] == S.FIXTURE_PATTERNS[(13 + 5) % 16]
+    assert act[0] == np.float32((5 % 29 - 14) / 31.0)
+    assert S.spine_close(exp, exp)
+    assert not S.spine_close(exp + 1e-3, exp)
+    bad = exp.copy()
+    bad[3] = np.nan
+    assert not S.spine_close(bad, exp)
+
+
+# ----------------------------------------------------------- host-side ABI checks
+
+
+def test_spine_abi_host_checks():
+    from deltafin_amd import _lib
+    lib = _lib.load()
+    assert lib.k3_hip_spine_bf16_abi_version() == 1
+    buf = np.zeros(64, np.float32)
+    p = buf.ctypes.data
+    # argument checks fail before anything is enqueued (-1, as the reference's)
+    assert lib.k3_hip_spine_bf16_launch_v1(None, p, p, 1, 8, 1, None) == _lib.K3_SPINE_E_INVALID
+    assert "null" in lib.k3_hip_spine_last_error().decode()
+    assert lib.k3_hip_spine_bf16_launch_v1(p, p, p, 1, 8, 65, None) == _lib.K3_SPINE_E_INVALID
+    assert lib.k3_hip_spine_bf16_launch_v1(p, p, p, 1, 8, 0, None) == _lib.K3_SPINE_E_INVALID
+    assert lib.k3_hip_spine_bf16_launch_v1(p, p, p, 0, 8, 1, None) == _lib.K3_SPINE_E_INVALID
+    assert lib.k3_hip_spine_int8_launch_v1(p, None, p, p, 1, 16, 1, None) == _lib.K3_SPINE_E_INVALID
+    assert lib.k3_hip_spine_bf16_decode_bits(p, p, 0, None) == _lib.K3_SPINE_E_INVALID
+    assert lib.k3_hip_rms_norm(p, p, p, 1, 0, 1e-5, None) == _lib.K3_SPINE_E_INVALID
+    assert lib.k3_hip_rms_norm(p, p, p, 1, 8, float("nan"), None) == _lib.K3_SPINE_E_INVALID
+
+
+def test_spine_available_without_device():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    from deltafin_amd import _lib
+    lib = _lib.load()
+    assert lib.k3_hip_spine_bf16_available(0, None, None) < 0
