@@ -91,6 +91,9 @@ def parse() -> argparse.Namespace:
                     help="timed tokens of --streamed (the default bench line carries a "
                          "300-token run; 0 there skips it)")
     ap.add_argument("--streamed-line-tokens", type=int, default=300)
+    ap.add_argument("--spine-only", action="store_true",
+                    help="print only the spine-projection timings (K3 spine shapes)")
+    ap.add_argument("--no-spine", action="store_true", help="skip the spine timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 4 plain device copies of 1 GiB (the known-size kernel "
                          "the HBM byte counters are scaled by) and exit")
@@ -471,6 +474,11 @@ def main() -> int:
         print(json.dumps(_verify_config3(moe, _lib, g, bank, stride, max(1, args.verify_batches))),
               flush=True)
         return 0
+    if args.spine_only:
+        del bank
+        torch.cuda.empty_cache()
+        print(json.dumps(_spine_bench()), flush=True)
+        return 0
 
     fn = lib.k3_hip_moe_route_layer_device
     gref = C.byref(g)
@@ -591,6 +599,8 @@ def main() -> int:
     }
     if args.verify_batches > 0:
         res["verify"] = _verify_config3(moe, _lib, g, bank, stride, args.verify_batches)
+    if not args.no_spine:
+        res["spine"] = _spine_bench()
     if args.streamed_line_tokens > 0:
         try:
             res["streamed"] = streamed_config4(args.streamed_line_tokens)
@@ -739,6 +749,82 @@ def _verify_batches(moe, _lib, g, bank, stride, logits, x, batches: int) -> dict
     log(f"verify M={m}: auto -> {auto_path} {sec * 1e6:.1f} us/batch (union {union:.1f} of "
         f"{m * TOP_K} edges); union/mfma {usec * 1e6:.1f} us, per-position "
         f"{res['positions'][0] * 1e6:.1f} us; mfma kernels {kus}")
+    return out
+
+
+# The K3 spine around the routed experts (provider_moe.cpp:428-447): rows x
+# columns of each resident matrix, in the order one token runs them.
+SPINE_SHAPES = (("router", 896, 7168), ("routed_down", 3584, 7168), ("routed_up", 7168, 3584),
+                ("shared_gate_up", 12288, 7168), ("shared_down", 7168, 6144))
+SPINE_POSITIONS = (1, 4, 16)
+SPINE_ROTATE_BYTES = 600_000_000  # > the 256 MB Infinity Cache: every pass streams HBM
+
+
+def _spine_bench(launches: int = 24) -> dict:
+    """Spine projections at the K3 shapes, BF16 and row-int8, at 1, 4 and 16
+    positions: each shape is launched `launches` times over enough distinct
+    copies that no launch finds its matrix in the Infinity Cache; `us` is the
+    kernel's device time per launch (the library's dispatch stamps).
+    Algorithmic bytes = matrix (+ int8 row scales) + activation + output."""
+    import torch
+
+    from deltafin_amd import _lib, spine
+
+    out = {"positions": list(SPINE_POSITIONS), "launches": launches}
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    for kind in ("bf16", "int8"):
+        per_kind = {}
+        tok_us = {p: 0.0 for p in SPINE_POSITIONS}
+        tok_bytes = {p: 0 for p in SPINE_POSITIONS}
+        for name, rows, cols in SPINE_SHAPES:
+            mat_bytes = rows * cols * (2 if kind == "bf16" else 1) + (rows * 4 if kind == "int8" else 0)
+            copies = max(2, -(-SPINE_ROTATE_BYTES // mat_bytes))
+            if kind == "bf16":
+                mats = [(torch.randn(rows, cols, device="cuda", generator=gen) * 0.02)
+                        .to(torch.bfloat16).view(torch.int16) for _ in range(copies)]
+            else:
+                mats = [torch.randint(-128, 128, (rows, cols), dtype=torch.int8, device="cuda",
+                                      generator=gen) for _ in range(copies)]
+                scales = torch.rand(rows, device="cuda", generator=gen) * 1e-3
+            xs = torch.randn(max(SPINE_POSITIONS), cols, device="cuda", generator=gen)
+            y = torch.empty(max(SPINE_POSITIONS), rows, device="cuda")
+            res = {}
+            for p in SPINE_POSITIONS:
+                x = xs[:p]
+
+                def run(i):
+                    if kind == "bf16":
+                        spine.bf16_gemv(mats[i % copies], x, out=y[:p])
+                    else:
+                        spine.int8_gemv(mats[i % copies], scales, x, out=y[:p])
+
+                for i in range(copies):
+                    run(i)
+                torch.cuda.synchronize()
+                _lib.timing_begin(launches)
+                for i in range(launches):
+                    run(i)
+                torch.cuda.synchronize()
+                kern, _ = _lib.timing_end()
+                us = kern["spine_gemv"]["total_ms"] * 1e3 / kern["spine_gemv"]["launches"]
+                alg = mat_bytes + p * cols * 4 + p * rows * 4
+                res[f"p{p}"] = {"us": round(us, 2), "gbs": round(alg / us / 1e3, 1),
+                                "hbm_frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4)}
+                tok_us[p] += us
+                tok_bytes[p] += alg
+            per_kind[name] = {"rows": rows, "cols": cols, "matrix_bytes": mat_bytes, **res}
+            del mats
+            torch.cuda.empty_cache()
+        per_kind["all_five"] = {f"p{p}": {"us": round(tok_us[p], 2),
+                                          "gbs": round(tok_bytes[p] / tok_us[p] / 1e3, 1),
+                                          "hbm_frac": round(tok_bytes[p] / tok_us[p] / 1e3
+                                                            / HBM_PEAK_GBS, 4)}
+                                for p in SPINE_POSITIONS}
+        out[kind] = per_kind
+        log(f"spine {kind}: " + ", ".join(
+            f"{n} {per_kind[n]['p1']['us']}us/{per_kind[n]['p1']['gbs']}GB/s" for n, _, _ in
+            SPINE_SHAPES) + f"; all five p1 {per_kind['all_five']['p1']}")
     return out
 
 

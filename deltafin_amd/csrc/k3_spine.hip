@@ -32,6 +32,10 @@ constexpr int kSpineThreads = 256;
 constexpr int kSpineWaves = kSpineThreads / kWave;
 constexpr int kSpineMaxNj = 16;                // pieces per row on the fast path
 constexpr uint32_t kSpineLdsBudget = 65536;    // activation bytes per workgroup
+#ifndef K3_SPINE_STREAM_WAVES_PER_CU
+#define K3_SPINE_STREAM_WAVES_PER_CU 8
+#endif
+constexpr int kStreamWavesPerCu = K3_SPINE_STREAM_WAVES_PER_CU;
 
 template <int kKind>
 struct SpineElem;
@@ -176,6 +180,95 @@ __global__ __launch_bounds__(kSpineThreads, 4) void k_spine_gemv(
   }
 }
 
+// One position group (positions <= PG), persistent waves: the workgroup stages
+// the activation once, then each wave walks rows row0, row0 + W, ... (W waves
+// in the grid, sized by the host so every wave gets the same number of rows)
+// with the next row's pieces requested while the current one is summed.  The
+// prefetch past the last row is clamped to row rows - 1 (every wave reads the
+// same bytes, served from cache) so that the loads are unconditional.
+template <int kKind, int NJ, int PG>
+__global__ __launch_bounds__(kSpineThreads, 2) void k_spine_stream(
+    const uint8_t* __restrict__ w, const float* __restrict__ row_scale,
+    const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions,
+    int tail_lanes) {
+  using E = SpineElem<kKind>;
+  constexpr int kQ = E::kPerChunk / 4;
+  constexpr int kPad = NJ * 64 * E::kPerChunk;
+  extern __shared__ float4 xs4[];  // [PG][kPad / 4]
+  float* xs = reinterpret_cast<float*>(xs4);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int stride = gridDim.x * kSpineWaves;
+  const uint64_t row_bytes = (uint64_t)cols * E::kBytes;
+  const bool tail_ok = lane < tail_lanes;
+
+  auto load_row = [&](u32x4* buf, int row) {
+    const uint8_t* base = w + (uint64_t)min(row, rows - 1) * row_bytes;
+    const uint8_t* rp = base + 16 * lane;
+#pragma unroll
+    for (int j = 0; j < NJ - 1; ++j) buf[j] = load_chunk(rp + 1024 * j);
+    buf[NJ - 1] = load_chunk(tail_ok ? rp + 1024 * (NJ - 1) : base);
+  };
+  auto sum_row = [&](const u32x4* buf, int row) {
+    float acc[PG];
+#pragma unroll
+    for (int p = 0; p < PG; ++p) acc[p] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      u32x4 wc = buf[j];
+      if (j == NJ - 1 && !tail_ok) wc = u32x4{0u, 0u, 0u, 0u};
+      float f[E::kPerChunk];
+      decode_chunk(wc, f, E{});
+#pragma unroll
+      for (int p = 0; p < PG; ++p) {
+        if (p < positions) {
+#pragma unroll
+          for (int q = 0; q < kQ; ++q) {
+            const float4 xv = xs4[(p * kPad) / 4 + (j * kQ + q) * 64 + lane];
+            acc[p] = fmaf(f[4 * q + 0], xv.x, acc[p]);
+            acc[p] = fmaf(f[4 * q + 1], xv.y, acc[p]);
+            acc[p] = fmaf(f[4 * q + 2], xv.z, acc[p]);
+            acc[p] = fmaf(f[4 * q + 3], xv.w, acc[p]);
+          }
+        }
+      }
+    }
+    const float scale = kKind == K3_SPINE_KIND_INT8 ? row_scale[row] : 1.f;
+#pragma unroll
+    for (int p = 0; p < PG; ++p) {
+      if (p < positions) {
+        float s = wave_sum(acc[p]);
+        if (kKind == K3_SPINE_KIND_INT8) s *= scale;
+        if (lane == 0) y[(uint64_t)p * rows + row] = s;
+      }
+    }
+  };
+
+  int row = blockIdx.x * kSpineWaves + threadIdx.x / kWave;
+  u32x4 a[NJ], b[NJ];
+  load_row(a, row);
+  for (int p = 0; p < positions; ++p) {
+    const float* xp = x + (uint64_t)p * cols;
+    for (int c = 4 * threadIdx.x; c < kPad; c += 4 * kSpineThreads) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (c < cols) v = *reinterpret_cast<const float4*>(xp + c);
+      *reinterpret_cast<float4*>(xs + p * kPad + lds_slot<kKind>(c)) = v;
+    }
+  }
+  __syncthreads();
+  if (row >= rows) return;  // no barrier follows
+  for (;;) {
+    const int rb = row + stride;
+    load_row(b, rb);
+    sum_row(a, row);
+    if (rb >= rows) break;
+    const int ra = rb + stride;
+    load_row(a, ra);
+    sum_row(b, rb);
+    if (ra >= rows) break;
+    row = ra;
+  }
+}
+
 // Any shape and alignment: one wave per row, lanes stride the columns.
 template <int kKind>
 __global__ __launch_bounds__(kSpineThreads) void k_spine_gemv_generic(
@@ -235,13 +328,32 @@ __global__ __launch_bounds__(kSpineThreads) void k_rms_norm(const float* __restr
 
 template <int kKind, int NJ>
 int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, float* y, int rows,
-                      int cols, int positions, int tail_lanes, int pg, hipStream_t st) {
+                      int cols, int positions, int tail_lanes, int pg, int stream_waves,
+                      hipStream_t st) {
   // Two rows per wave for short rows (int8 decodes twice the values per piece).
   constexpr int R = NJ <= (kKind == K3_SPINE_KIND_BF16 ? 4 : 2) ? 2 : 1;
   constexpr uint32_t kPadBytes = NJ * 64u * SpineElem<kKind>::kPerChunk * 4u;
-  const int rows_per_group = kSpineWaves * R;
-  const dim3 grid((unsigned)((rows + rows_per_group - 1) / rows_per_group));
   TimedLaunch tl(KC_SPINE, st);
+  if (positions <= pg && stream_waves > 0) {
+    // One position group: persistent waves, each with the same row count.
+    const dim3 sgrid((unsigned)(stream_waves / kSpineWaves));
+    const uint32_t lds = (uint32_t)pg * kPadBytes;
+    if constexpr (4 * kPadBytes <= kSpineLdsBudget) {
+      if (pg == 4)
+        launch_timed(tl, (k_spine_stream<kKind, NJ, 4>), sgrid, dim3(kSpineThreads), lds, st, w,
+                     scales, x, y, rows, cols, positions, tail_lanes);
+    }
+    if constexpr (2 * kPadBytes <= kSpineLdsBudget) {
+      if (pg == 2)
+        launch_timed(tl, (k_spine_stream<kKind, NJ, 2>), sgrid, dim3(kSpineThreads), lds, st, w,
+                     scales, x, y, rows, cols, positions, tail_lanes);
+    }
+    if (pg == 1)
+      launch_timed(tl, (k_spine_stream<kKind, NJ, 1>), sgrid, dim3(kSpineThreads), lds, st, w,
+                   scales, x, y, rows, cols, positions, tail_lanes);
+  } else {
+    const int rows_per_group = kSpineWaves * R;
+    const dim3 grid((unsigned)((rows + rows_per_group - 1) / rows_per_group));
   // Only the position groups whose activation fits the LDS budget exist.
   if constexpr (4 * kPadBytes <= kSpineLdsBudget) {
     if (pg == 4)
@@ -256,6 +368,7 @@ int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, flo
   if (pg == 1)
     launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 1>), grid, dim3(kSpineThreads), kPadBytes, st,
                  w, scales, x, y, rows, cols, positions, tail_lanes);
+  }
   const bool launched_one = pg == 1 || (pg == 2 && 2 * kPadBytes <= kSpineLdsBudget) ||
                             (pg == 4 && 4 * kPadBytes <= kSpineLdsBudget);
   if (!launched_one) {
@@ -269,7 +382,7 @@ int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, flo
 }
 
 typedef int (*SpineFastFn)(const uint8_t*, const float*, const float*, float*, int, int, int,
-                           int, int, hipStream_t);
+                           int, int, int, hipStream_t);
 
 template <int kKind, int... NJ>
 constexpr SpineFastFn spine_fast_table(int nj, std::integer_sequence<int, NJ...>) {
@@ -317,7 +430,16 @@ int spine_gemv(int kind, const void* weights, const float* row_scales, const flo
     const SpineFastFn fn = kind == K3_SPINE_KIND_BF16
                                ? spine_fast_table<K3_SPINE_KIND_BF16>(nj, seq)
                                : spine_fast_table<K3_SPINE_KIND_INT8>(nj, seq);
-    return fn(w, row_scales, x, y, rows, cols, positions, tail_lanes, pg, st);
+    // Persistent waves for one position group: about kStreamWavesPerCu per CU,
+    // rounded so every wave gets ceil(rows / target) rows, in whole workgroups.
+    int stream_waves = 0;
+    if (positions <= pg) {
+      const int target = std::max(kSpineWaves, std::max(1, device_cu_count()) * kStreamWavesPerCu);
+      const int per_wave = (rows + target - 1) / target;
+      stream_waves = (rows + per_wave - 1) / per_wave;
+      stream_waves = (stream_waves + kSpineWaves - 1) / kSpineWaves * kSpineWaves;
+    }
+    return fn(w, row_scales, x, y, rows, cols, positions, tail_lanes, pg, stream_waves, st);
   }
   const dim3 grid((unsigned)((rows + kSpineWaves - 1) / kSpineWaves));
   TimedLaunch tl(KC_SPINE, st);
