@@ -656,15 +656,18 @@ def _traffic_from_profiles(kernel: str):
 MFMA_PEAK_FP8_TFLOPS = 5000.0
 MFMA_FLOPS = 2 * 16 * 16 * 128  # one 16x16x128 block-scaled MFMA
 X_TERMS, H_TERMS = 2, 3         # fp8 terms per bf16 x row / fp32 h row
+PARITY_SPLIT = 2                # MFMA rows per weight row in a parity-split tile
 
 
 def _mfma_issued_per_expert() -> int:
     """MFMA instructions the union kernels issue per unique expert: gate and up
     (I/16 row tiles each, H/128 K steps, one per x term) and down (H/16 row
-    tiles, I/128 K steps, one per h term).  Each covers 16 token columns."""
+    tiles, I/128 K steps, one per h term), times 2 for the parity split (a
+    tile's 16 MFMA rows hold 8 weight rows, each as an even and an odd K
+    step).  Each covers 16 token columns."""
     glu = 2 * (INTER // 16) * (HIDDEN // 128) * X_TERMS
     down = (HIDDEN // 16) * (INTER // 128) * H_TERMS
-    return glu + down
+    return PARITY_SPLIT * (glu + down)
 
 
 def _verify_batches(moe, _lib, g, bank, stride, logits, x, batches: int) -> dict:
