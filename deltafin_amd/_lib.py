@@ -73,6 +73,38 @@ class K3HipKernelTimingV1(C.Structure):
     ]
 
 
+class K3HipMoeSpineV1(C.Structure):
+    _fields_ = [
+        ("abi_version", C.c_uint32),
+        ("struct_bytes", C.c_uint32),
+        ("matrix_kind", C.c_uint32),
+        ("hidden", C.c_uint32),
+        ("routed_hidden", C.c_uint32),
+        ("shared_intermediate", C.c_uint32),
+        ("experts", C.c_uint32),
+        ("top_k", C.c_uint32),
+        ("router", C.c_void_p),
+        ("router_scales", C.c_void_p),
+        ("router_bias", C.c_void_p),
+        ("routed_down", C.c_void_p),
+        ("routed_down_scales", C.c_void_p),
+        ("routed_norm", C.c_void_p),
+        ("routed_up", C.c_void_p),
+        ("routed_up_scales", C.c_void_p),
+        ("shared_gate", C.c_void_p),
+        ("shared_gate_scales", C.c_void_p),
+        ("shared_up", C.c_void_p),
+        ("shared_up_scales", C.c_void_p),
+        ("shared_down", C.c_void_p),
+        ("shared_down_scales", C.c_void_p),
+    ]
+
+
+K3_SPINE_MATRIX_BF16 = 0
+K3_SPINE_MATRIX_INT8 = 1
+K3_MOE_SPINE_ABI_V1 = 1
+
+assert C.sizeof(K3HipMoeSpineV1) == 144
 assert C.sizeof(K3HipKernelTimingV1) == 64
 assert C.sizeof(K3HipExpertDescriptorV1) == 32
 assert C.sizeof(K3HipGeometryV1) == 32
@@ -138,6 +170,10 @@ SIGNATURES = {
     "k3_hip_scale4_check_header": (_i32, [_vp, _u64]),
     "k3_hip_synth_bank": (_i32, [_GP, _vp, _u64, _i32, _u64, _u64, _i32, _i32, _vp]),
     "k3_hip_synth_normal": (_i32, [_vp, _i32, _u64, _u64, _u64, _vp]),
+    "k3_hip_moe_block_workspace_bytes": (_u64, [C.POINTER(K3HipMoeSpineV1), _GP, _i32]),
+    "k3_hip_moe_block_device": (
+        _i32, [C.POINTER(K3HipMoeSpineV1), _GP, _vp, _u64, _vp, _i32, _vp, _vp, _vp, _vp, _u64,
+               _vp]),
     # include/k3_hip_spine_abi.h
     "k3_hip_spine_bf16_abi_version": (_u32, []),
     "k3_hip_spine_last_error": (C.c_char_p, []),

@@ -649,12 +649,193 @@ double expected_union(int n_bank, int top_k, int n_positions) {
   return (double)n_bank * (1.0 - miss);
 }
 
+// ---------------------------------------------------------------- MoE block
+static_assert(sizeof(K3HipMoeSpineV1) == 144, "K3HipMoeSpineV1 layout changed");
+
+// Block workspace: the expert workspace, then logits [P, E], routed_in and
+// routed_out [P, R], shared gate and up [P, S] (h overwrites gate), each
+// 256-byte aligned.
+struct BlockBufs {
+  uint8_t* expert_ws;
+  uint64_t expert_ws_bytes;
+  float* logits;
+  float* routed_in;
+  float* routed_out;
+  float* gate;
+  float* up;
+};
+
+uint64_t block_layout(const K3HipMoeSpineV1& sp, const Geo& g, int max_positions,
+                      uint8_t* base, BlockBufs* b) {
+  const uint64_t P = (uint64_t)max_positions;
+  uint64_t off = 0;
+  const uint64_t ew = align256(workspace_bytes(g, max_positions * (int)sp.top_k, max_positions));
+  if (b) {
+    b->expert_ws = base;
+    b->expert_ws_bytes = ew;
+  }
+  off += ew;
+  auto take = [&](float** dst, uint64_t n) {
+    if (b) *dst = reinterpret_cast<float*>(base + off);
+    off += align256(n * sizeof(float));
+  };
+  take(b ? &b->logits : nullptr, P * sp.experts);
+  take(b ? &b->routed_in : nullptr, P * sp.routed_hidden);
+  take(b ? &b->routed_out : nullptr, P * sp.routed_hidden);
+  take(b ? &b->gate : nullptr, P * sp.shared_intermediate);
+  take(b ? &b->up : nullptr, P * sp.shared_intermediate);
+  return off;
+}
+
+const char* check_spine(const K3HipMoeSpineV1* sp, const Geo& g) {
+  if (!sp) return "null spine";
+  if (sp->abi_version != K3_MOE_SPINE_ABI_V1 || sp->struct_bytes != sizeof(K3HipMoeSpineV1))
+    return "spine header (abi_version / struct_bytes) mismatch";
+  if (sp->matrix_kind != K3_SPINE_MATRIX_BF16 && sp->matrix_kind != K3_SPINE_MATRIX_INT8)
+    return "unknown spine matrix kind";
+  if (sp->hidden == 0 || sp->routed_hidden == 0 || sp->shared_intermediate == 0 ||
+      sp->hidden > (1u << 20) || sp->routed_hidden > (1u << 20) ||
+      sp->shared_intermediate > (1u << 20))
+    return "spine widths must be in [1, 2^20]";
+  if (sp->routed_hidden != (uint32_t)g.hidden)
+    return "spine routed_hidden differs from the expert geometry's hidden";
+  if (sp->experts == 0 || sp->experts > 4096) return "spine experts must be in [1, 4096]";
+  if (sp->top_k == 0 || sp->top_k > K3_HIP_MAX_TOKEN_EXPERTS || sp->top_k > sp->experts)
+    return "spine top_k must be in [1, min(32, experts)]";
+  if (!sp->router || !sp->router_bias || !sp->routed_down || !sp->routed_norm || !sp->routed_up ||
+      !sp->shared_gate || !sp->shared_up || !sp->shared_down)
+    return "a spine matrix or vector is null";
+  if (sp->matrix_kind == K3_SPINE_MATRIX_INT8 &&
+      (!sp->router_scales || !sp->routed_down_scales || !sp->routed_up_scales ||
+       !sp->shared_gate_scales || !sp->shared_up_scales || !sp->shared_down_scales))
+    return "row-int8 spine matrices need their row scales";
+  return nullptr;
+}
+
+// A spine-surface status as a K3_HIP_* status, carrying the spine's reason.
+int from_spine(int rc, const char* step) {
+  if (rc == K3_SPINE_OK) return K3_HIP_OK;
+  return fail(rc == K3_SPINE_E_INVALID ? K3_HIP_E_INVALID : K3_HIP_E_EXEC, "MoE block %s: %s",
+              step, k3_hip_spine_last_error());
+}
+
+// The routed experts of P positions whose routes are already in ws.ids /
+// ws.w ([P][top_k]): the union path (plan + matrix-core or VALU kernels) when
+// the verify mode asks for it or AUTO expects the union to pay, else one
+// decode layer per position on the device route.
+int experts_on_device_routes(const Geo& g, const uint8_t* bank, uint64_t stride, int n_bank,
+                             int P, int top_k, const float* x, float* out, const Workspace& ws,
+                             hipStream_t st) {
+  const int n_edges = P * top_k;
+  const int mode = g_verify_mode.load();
+  if (mode == K3_VERIFY_UNION_MFMA && !verify_mfma_supported(g))
+    return fail(K3_HIP_E_CAPABILITY, "MoE block: this geometry/layout has no matrix-core path");
+  const bool shared = expected_union(n_bank, top_k, P) <= kUnionFraction * (double)n_edges;
+  const bool mfma = P >= 2 && (mode == K3_VERIFY_UNION_MFMA ||
+                               (mode == K3_VERIFY_AUTO && shared && verify_mfma_supported(g)));
+  if (mfma || (P >= 2 && mode == K3_VERIFY_UNION_VALU)) {
+    int rc = launch_verify_plan_bank(g, bank, stride, P, top_k, ws, st);
+    if (rc != K3_HIP_OK) return rc;
+    return mfma ? launch_verify_mfma(g, n_edges, P, x, K3_DTYPE_F32, out, K3_DTYPE_F32, ws, st)
+                : launch_verify_layer(g, n_edges, P, x, K3_DTYPE_F32, out, K3_DTYPE_F32, ws, st);
+  }
+  for (int p = 0; p < P; ++p) {
+    TokenRoute route;
+    memset(&route, 0, sizeof(route));
+    route.bank = bank;
+    route.stride = stride;
+    route.ids = ws.ids + (size_t)p * top_k;
+    route.wdev = ws.w + (size_t)p * top_k;
+    route.n = top_k;
+    const int rc = launch_decode_layer(g, route, x + (size_t)p * g.hidden, K3_DTYPE_F32,
+                                       out + (size_t)p * g.hidden, K3_DTYPE_F32, ws, st);
+    if (rc != K3_HIP_OK) return rc;
+  }
+  return K3_HIP_OK;
+}
+
 }  // namespace
 }  // namespace k3
 
 using namespace k3;
 
 extern "C" {
+
+uint64_t k3_hip_moe_block_workspace_bytes(const K3HipMoeSpineV1* spine,
+                                          const K3HipGeometryV1* experts, int max_positions) {
+  Geo g;
+  if (!geometry_from(experts, &g) || check_spine(spine, g) || max_positions <= 0 ||
+      max_positions > K3_HIP_MAX_POSITIONS ||
+      max_positions * (int)spine->top_k > K3_HIP_MAX_EDGES)
+    return 0;
+  return block_layout(*spine, g, max_positions, nullptr, nullptr);
+}
+
+int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1* experts,
+                            const uint8_t* bank, uint64_t expert_stride, const float* hidden,
+                            int n_positions, float* out, int32_t* route_ids,
+                            float* route_weights, void* workspace, uint64_t workspace_bytes,
+                            void* stream) {
+  Geo g;
+  if (!geometry_from(experts, &g)) return fail(K3_HIP_E_INVALID, "MoE block: invalid geometry");
+  if (const char* why = check_spine(spine, g)) return fail(K3_HIP_E_INVALID, "MoE block: %s", why);
+  const K3HipMoeSpineV1& sp = *spine;
+  if (!bank || !hidden || !out) return fail(K3_HIP_E_INVALID, "MoE block: null pointer");
+  if (expert_stride < g.span || expert_stride % 16 != 0 || ((uintptr_t)bank & 15u) != 0)
+    return fail(K3_HIP_E_INVALID, "MoE block: bank must be 16-byte aligned with stride >= span");
+  if ((((uintptr_t)hidden | (uintptr_t)out) & 15u) != 0)
+    return fail(K3_HIP_E_INVALID, "MoE block: hidden and out must be 16-byte aligned");
+  const int top_k = (int)sp.top_k;
+  if (n_positions <= 0 || n_positions > K3_HIP_MAX_POSITIONS ||
+      n_positions * top_k > K3_HIP_MAX_EDGES)
+    return fail(K3_HIP_E_INVALID, "MoE block: positions %d outside [1, %d] (or too many edges)",
+                n_positions, K3_HIP_MAX_POSITIONS);
+  if (!workspace || ((uintptr_t)workspace & 255u) != 0 ||
+      workspace_bytes < block_layout(sp, g, n_positions, nullptr, nullptr))
+    return fail(K3_HIP_E_INVALID, "MoE block: workspace missing, misaligned or too small");
+  BlockBufs b;
+  block_layout(sp, g, n_positions, static_cast<uint8_t*>(workspace), &b);
+  Workspace ws;
+  if (!carve_workspace(b.expert_ws, b.expert_ws_bytes, g, n_positions * top_k, n_positions, &ws))
+    return fail(K3_HIP_E_INVALID, "MoE block: expert workspace carve failed");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int kind =
+      sp.matrix_kind == K3_SPINE_MATRIX_BF16 ? K3_SPINE_KIND_BF16 : K3_SPINE_KIND_INT8;
+  const int P = n_positions, H = (int)sp.hidden, R = (int)sp.routed_hidden;
+  const int S = (int)sp.shared_intermediate, E = (int)sp.experts;
+  int rc;
+  // prepare: router logits, the route, routed_down
+  if ((rc = from_spine(spine_gemv(kind, sp.router, sp.router_scales, hidden, b.logits, E, H, P,
+                                  false, st), "router")))
+    return rc;
+  if ((rc = launch_route_sigmoid_bias(b.logits, sp.router_bias, E, top_k, P, ws.ids, ws.w,
+                                      route_ids, route_weights, st)))
+    return rc;
+  if ((rc = from_spine(spine_gemv(kind, sp.routed_down, sp.routed_down_scales, hidden,
+                                  b.routed_in, R, H, P, false, st), "routed_down")))
+    return rc;
+  // the routed experts
+  if ((rc = experts_on_device_routes(g, bank, expert_stride, E, P, top_k, b.routed_in,
+                                     b.routed_out, ws, st)))
+    return rc;
+  // the shared expert: h = situ(gate, up) overwrites gate
+  if ((rc = from_spine(spine_gemv(kind, sp.shared_gate, sp.shared_gate_scales, hidden, b.gate, S,
+                                  H, P, false, st), "shared_gate")))
+    return rc;
+  if ((rc = from_spine(spine_gemv(kind, sp.shared_up, sp.shared_up_scales, hidden, b.up, S, H, P,
+                                  false, st), "shared_up")))
+    return rc;
+  if ((rc = launch_activation(b.gate, b.up, b.gate, (int64_t)P * S, K3_ACT_SITU, st))) return rc;
+  // complete: routed RMS norm, routed_up, + shared_down h (one fp32 add)
+  if ((rc = from_spine(spine_rms_norm(b.routed_out, sp.routed_norm, b.routed_out, P, R,
+                                      K3_RMS_EPSILON, st), "routed RMS norm")))
+    return rc;
+  if ((rc = from_spine(spine_gemv(kind, sp.routed_up, sp.routed_up_scales, b.routed_out, out, H,
+                                  R, P, false, st), "routed_up")))
+    return rc;
+  return from_spine(spine_gemv(kind, sp.shared_down, sp.shared_down_scales, b.gate, out, H, S, P,
+                               true, st), "shared_down");
+}
 
 uint64_t k3_hip_geometry_span(uint32_t hidden, uint32_t intermediate) {
   if (hidden == 0 || intermediate == 0 || hidden % 32 != 0 || intermediate % 32 != 0) return 0;

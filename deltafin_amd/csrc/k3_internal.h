@@ -112,6 +112,11 @@ int launch_activation(const float* gate, const float* up, float* h, int64_t n,
 int launch_route(const float* logits, int n_bank, int top_k, int n_positions,
                  int32_t* ids_ws, float* w_ws, int32_t* ids_user,
                  float* w_user, hipStream_t stream);
+// K3 router: top_k of sigmoid(logits) + bias per position, weighted by the
+// selected sigmoids over their sum + 1e-20 (provider_moe.cpp:1673-1683).
+int launch_route_sigmoid_bias(const float* logits, const float* bias, int n_bank, int top_k,
+                              int n_positions, int32_t* ids_ws, float* w_ws, int32_t* ids_user,
+                              float* w_user, hipStream_t stream);
 // Decode layer.  When route.logits is set (router mode) the gate/up kernel
 // routes the token itself and publishes the route to ws.ids / ws.w.
 int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x,
@@ -195,8 +200,9 @@ class TimedLaunch {
 // spine surface; failures record their reason through spine_fail.
 enum { K3_SPINE_KIND_BF16 = 0, K3_SPINE_KIND_INT8 = 1 };
 int spine_fail(int status, const char* fmt, ...);
+// accumulate: y += W x instead of y = W x (one fp32 add per output).
 int spine_gemv(int kind, const void* weights, const float* row_scales, const float* x,
-               float* y, int rows, int cols, int positions, hipStream_t stream);
+               float* y, int rows, int cols, int positions, bool accumulate, hipStream_t stream);
 int spine_decode_bits(const uint16_t* in, uint32_t* out, int count, hipStream_t stream);
 int spine_rms_norm(const float* in, const float* weight, float* out, int rows, int cols,
                    float eps, hipStream_t stream);

@@ -556,8 +556,10 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
   const int grp = wave / S;
   const int gw = wave - grp * S;  // wave within its group
   const ColSplit cs = col_split(g.hidden >> 5, S, gw, lane);
-  const GluGather gg = kS4 ? glu_gather4(g.hidden >> 5, S, gw, lane, kR)
-                           : glu_gather(g.hidden >> 5, S, gw, lane, kR);
+  // Only the gathered forms read gg (glu_gather needs cw >= 4).
+  const GluGather gg = kS4   ? glu_gather4(g.hidden >> 5, S, gw, lane, kR)
+                       : kG ? glu_gather(g.hidden >> 5, S, gw, lane, kR)
+                            : GluGather{0, 0};
   // cw (scale4-v2: cw / 2): bpermute bytes per row
   const int row_step = (((g.hidden >> 5) + S - 1) / S) >> (kS4 ? 1 : 0);
   XChunk<XT> xc;
@@ -1207,6 +1209,12 @@ __global__ void k_activate(const float* __restrict__ gate, const float* __restri
 // ======================================================================
 constexpr int kRouteMaxBank = 4096;
 
+// Bytes of block_topk's key scratch (the host's route_scratch_bytes).
+__device__ __forceinline__ size_t route_scratch_bytes_dev(int n_bank, int top_k) {
+  const size_t nseg = (size_t)(n_bank + 63) / 64;
+  return (nseg * 64 + ((nseg * (size_t)top_k + 1) & ~(size_t)1)) * sizeof(uint64_t);
+}
+
 // Inverse of route_key's value half (NaN comes back as -inf, -0 as +0).
 __device__ __forceinline__ float key_value(uint64_t key) {
   uint32_t u = (uint32_t)(key >> 32);
@@ -1296,6 +1304,42 @@ __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits
     w_ws[o] = wsel[j];
     if (ids_user) ids_user[o] = sel[j];
     if (w_user) w_user[o] = wsel[j];
+  }
+}
+
+// K3 router (prepare_moe_t1, native/provider_gate/provider_moe.cpp:1673-1683):
+// scores = sigmoid(logits), choice = scores + correction bias; the top_k
+// largest choices (descending, lower index on ties, as block_topk ranks) are
+// the route, each weighted by its unbiased score over the selected scores' sum
+// + 1e-20 (one wave, fixed order).  choice sits in LDS after the rank keys.
+__device__ __forceinline__ float sigmoid_f32(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+__global__ __launch_bounds__(1024) void k_route_sigmoid_bias(
+    const float* __restrict__ logits, const float* __restrict__ bias, int n_bank, int top_k,
+    int32_t* __restrict__ ids_ws, float* __restrict__ w_ws, int32_t* __restrict__ ids_user,
+    float* __restrict__ w_user) {
+  extern __shared__ __attribute__((aligned(16))) uint64_t rsm[];
+  __shared__ int sel[K3_HIP_MAX_TOKEN_EXPERTS];
+  __shared__ float wsel[K3_HIP_MAX_TOKEN_EXPERTS];
+  const int p = blockIdx.x;
+  const float* lg = logits + (size_t)p * n_bank;
+  float* choice = reinterpret_cast<float*>(
+      reinterpret_cast<uint8_t*>(rsm) + route_scratch_bytes_dev(n_bank, top_k));
+  for (int i = threadIdx.x; i < n_bank; i += blockDim.x) choice[i] = sigmoid_f32(lg[i]) + bias[i];
+  __syncthreads();
+  block_topk(choice, n_bank, top_k, rsm, sel, wsel);  // its softmax weights are not used
+  if (threadIdx.x < 64) {
+    const int j = threadIdx.x;
+    const float sc = j < top_k ? sigmoid_f32(lg[sel[j]]) : 0.0f;
+    const float sum = wave_sum(sc);
+    if (j < top_k) {
+      const int o = p * top_k + j;
+      const float wj = sc / (sum + 1e-20f);
+      ids_ws[o] = sel[j];
+      w_ws[o] = wj;
+      if (ids_user) ids_user[o] = sel[j];
+      if (w_user) w_user[o] = wj;
+    }
   }
 }
 
@@ -1716,6 +1760,25 @@ int launch_route(const float* logits, int n_bank, int top_k, int n_positions, in
   launch_timed(tl, k_route, dim3(n_positions), dim3(threads), (unsigned)lds, st, logits, n_bank,
                      top_k, ids_ws, w_ws, ids_user, w_user);
   return launched(tl, "router launch");
+}
+
+int launch_route_sigmoid_bias(const float* logits, const float* bias, int n_bank, int top_k,
+                              int n_positions, int32_t* ids_ws, float* w_ws, int32_t* ids_user,
+                              float* w_user, hipStream_t st) {
+  if (!logits || !bias) return fail(K3_HIP_E_INVALID, "K3 router: null logits or bias");
+  if (n_bank <= 0 || n_bank > kRouteMaxBank)
+    return fail(K3_HIP_E_INVALID, "K3 router: n_bank must be in [1, %d]", kRouteMaxBank);
+  if (top_k <= 0 || top_k > K3_HIP_MAX_TOKEN_EXPERTS || top_k > n_bank)
+    return fail(K3_HIP_E_INVALID, "K3 router: top_k must be in [1, min(%d, n_bank)]",
+                K3_HIP_MAX_TOKEN_EXPERTS);
+  if (n_positions <= 0) return fail(K3_HIP_E_INVALID, "K3 router: no positions");
+  const int nseg = (n_bank + 63) / 64;
+  const int threads = std::min(1024, nseg * 64);
+  const size_t lds = route_scratch_bytes(n_bank, top_k) + (size_t)n_bank * sizeof(float);
+  TimedLaunch tl(KC_ROUTE, st);
+  launch_timed(tl, k_route_sigmoid_bias, dim3(n_positions), dim3(threads), (unsigned)lds, st,
+               logits, bias, n_bank, top_k, ids_ws, w_ws, ids_user, w_user);
+  return launched(tl, "K3 router launch");
 }
 
 namespace {

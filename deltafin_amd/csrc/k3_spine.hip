@@ -86,7 +86,7 @@ template <int kKind, int NJ, int R, int PG>
 __global__ __launch_bounds__(kSpineThreads, 4) void k_spine_gemv(
     const uint8_t* __restrict__ w, const float* __restrict__ row_scale,
     const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions,
-    int tail_lanes) {
+    int tail_lanes, int accumulate) {
   using E = SpineElem<kKind>;
   constexpr int kQ = E::kPerChunk / 4;
   constexpr int kPad = NJ * 64 * E::kPerChunk;  // columns per staged position
@@ -173,7 +173,10 @@ __global__ __launch_bounds__(kSpineThreads, 4) void k_spine_gemv(
         if (p < pg) {
           float s = wave_sum(acc[r][p]);
           if (kKind == K3_SPINE_KIND_INT8) s *= scale;
-          if (lane == 0 && row < rows) y[(uint64_t)(p0 + p) * rows + row] = s;
+          if (lane == 0 && row < rows) {
+            float* yp = y + (uint64_t)(p0 + p) * rows + row;
+            *yp = accumulate ? *yp + s : s;
+          }
         }
       }
     }
@@ -190,7 +193,7 @@ template <int kKind, int NJ, int PG>
 __global__ __launch_bounds__(kSpineThreads, 2) void k_spine_stream(
     const uint8_t* __restrict__ w, const float* __restrict__ row_scale,
     const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions,
-    int tail_lanes) {
+    int tail_lanes, int accumulate) {
   using E = SpineElem<kKind>;
   constexpr int kQ = E::kPerChunk / 4;
   constexpr int kPad = NJ * 64 * E::kPerChunk;
@@ -238,7 +241,10 @@ __global__ __launch_bounds__(kSpineThreads, 2) void k_spine_stream(
       if (p < positions) {
         float s = wave_sum(acc[p]);
         if (kKind == K3_SPINE_KIND_INT8) s *= scale;
-        if (lane == 0) y[(uint64_t)p * rows + row] = s;
+        if (lane == 0) {
+          float* yp = y + (uint64_t)p * rows + row;
+          *yp = accumulate ? *yp + s : s;
+        }
       }
     }
   };
@@ -273,7 +279,8 @@ __global__ __launch_bounds__(kSpineThreads, 2) void k_spine_stream(
 template <int kKind>
 __global__ __launch_bounds__(kSpineThreads) void k_spine_gemv_generic(
     const uint8_t* __restrict__ w, const float* __restrict__ row_scale,
-    const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions) {
+    const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions,
+    int accumulate) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * kSpineWaves + threadIdx.x / kWave;
   if (row >= rows) return;
@@ -292,7 +299,10 @@ __global__ __launch_bounds__(kSpineThreads) void k_spine_gemv_generic(
     }
     float s = wave_sum(acc);
     if (kKind == K3_SPINE_KIND_INT8) s *= row_scale[row];
-    if (lane == 0) y[(uint64_t)p * rows + row] = s;
+    if (lane == 0) {
+      float* yp = y + (uint64_t)p * rows + row;
+      *yp = accumulate ? *yp + s : s;
+    }
   }
 }
 
@@ -329,7 +339,7 @@ __global__ __launch_bounds__(kSpineThreads) void k_rms_norm(const float* __restr
 template <int kKind, int NJ>
 int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, float* y, int rows,
                       int cols, int positions, int tail_lanes, int pg, int stream_waves,
-                      hipStream_t st) {
+                      int accumulate, hipStream_t st) {
   // Two rows per wave for short rows (int8 decodes twice the values per piece).
   constexpr int R = NJ <= (kKind == K3_SPINE_KIND_BF16 ? 4 : 2) ? 2 : 1;
   constexpr uint32_t kPadBytes = NJ * 64u * SpineElem<kKind>::kPerChunk * 4u;
@@ -341,16 +351,16 @@ int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, flo
     if constexpr (4 * kPadBytes <= kSpineLdsBudget) {
       if (pg == 4)
         launch_timed(tl, (k_spine_stream<kKind, NJ, 4>), sgrid, dim3(kSpineThreads), lds, st, w,
-                     scales, x, y, rows, cols, positions, tail_lanes);
+                     scales, x, y, rows, cols, positions, tail_lanes, accumulate);
     }
     if constexpr (2 * kPadBytes <= kSpineLdsBudget) {
       if (pg == 2)
         launch_timed(tl, (k_spine_stream<kKind, NJ, 2>), sgrid, dim3(kSpineThreads), lds, st, w,
-                     scales, x, y, rows, cols, positions, tail_lanes);
+                     scales, x, y, rows, cols, positions, tail_lanes, accumulate);
     }
     if (pg == 1)
       launch_timed(tl, (k_spine_stream<kKind, NJ, 1>), sgrid, dim3(kSpineThreads), lds, st, w,
-                   scales, x, y, rows, cols, positions, tail_lanes);
+                   scales, x, y, rows, cols, positions, tail_lanes, accumulate);
   } else {
     const int rows_per_group = kSpineWaves * R;
     const dim3 grid((unsigned)((rows + rows_per_group - 1) / rows_per_group));
@@ -358,16 +368,16 @@ int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, flo
   if constexpr (4 * kPadBytes <= kSpineLdsBudget) {
     if (pg == 4)
       launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 4>), grid, dim3(kSpineThreads), 4 * kPadBytes,
-                   st, w, scales, x, y, rows, cols, positions, tail_lanes);
+                   st, w, scales, x, y, rows, cols, positions, tail_lanes, accumulate);
   }
   if constexpr (2 * kPadBytes <= kSpineLdsBudget) {
     if (pg == 2)
       launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 2>), grid, dim3(kSpineThreads), 2 * kPadBytes,
-                   st, w, scales, x, y, rows, cols, positions, tail_lanes);
+                   st, w, scales, x, y, rows, cols, positions, tail_lanes, accumulate);
   }
   if (pg == 1)
     launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 1>), grid, dim3(kSpineThreads), kPadBytes, st,
-                 w, scales, x, y, rows, cols, positions, tail_lanes);
+                 w, scales, x, y, rows, cols, positions, tail_lanes, accumulate);
   }
   const bool launched_one = pg == 1 || (pg == 2 && 2 * kPadBytes <= kSpineLdsBudget) ||
                             (pg == 4 && 4 * kPadBytes <= kSpineLdsBudget);
@@ -382,7 +392,7 @@ int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, flo
 }
 
 typedef int (*SpineFastFn)(const uint8_t*, const float*, const float*, float*, int, int, int,
-                           int, int, int, hipStream_t);
+                           int, int, int, int, hipStream_t);
 
 template <int kKind, int... NJ>
 constexpr SpineFastFn spine_fast_table(int nj, std::integer_sequence<int, NJ...>) {
@@ -399,7 +409,7 @@ int preflight(const char* what) {
 }  // namespace
 
 int spine_gemv(int kind, const void* weights, const float* row_scales, const float* x,
-               float* y, int rows, int cols, int positions, hipStream_t st) {
+               float* y, int rows, int cols, int positions, bool accumulate, hipStream_t st) {
   const char* what = kind == K3_SPINE_KIND_BF16 ? "RAW_BF16 GEMV" : "row-int8 GEMV";
   if (!weights || !x || !y || (kind == K3_SPINE_KIND_INT8 && !row_scales))
     return spine_fail(K3_SPINE_E_INVALID, "%s: null input or output pointer", what);
@@ -439,16 +449,17 @@ int spine_gemv(int kind, const void* weights, const float* row_scales, const flo
       stream_waves = (rows + per_wave - 1) / per_wave;
       stream_waves = (stream_waves + kSpineWaves - 1) / kSpineWaves * kSpineWaves;
     }
-    return fn(w, row_scales, x, y, rows, cols, positions, tail_lanes, pg, stream_waves, st);
+    return fn(w, row_scales, x, y, rows, cols, positions, tail_lanes, pg, stream_waves,
+              accumulate ? 1 : 0, st);
   }
   const dim3 grid((unsigned)((rows + kSpineWaves - 1) / kSpineWaves));
   TimedLaunch tl(KC_SPINE, st);
   if (kind == K3_SPINE_KIND_BF16)
     launch_timed(tl, k_spine_gemv_generic<K3_SPINE_KIND_BF16>, grid, dim3(kSpineThreads), 0, st,
-                 w, row_scales, x, y, rows, cols, positions);
+                 w, row_scales, x, y, rows, cols, positions, accumulate);
   else
     launch_timed(tl, k_spine_gemv_generic<K3_SPINE_KIND_INT8>, grid, dim3(kSpineThreads), 0, st,
-                 w, row_scales, x, y, rows, cols, positions);
+                 w, row_scales, x, y, rows, cols, positions, accumulate);
   const hipError_t e = hipGetLastError();
   if (e == hipSuccess) return K3_SPINE_OK;
   tl.failed();

@@ -59,7 +59,7 @@ int k3_hip_spine_bf16_available(int device, int* compute_major, int* compute_min
 int k3_hip_spine_bf16_launch_v1(const uint16_t* weights, const float* activation, float* output,
                                 int rows, int columns, int positions, void* stream) {
   return spine_gemv(K3_SPINE_KIND_BF16, weights, nullptr, activation, output, rows, columns,
-                    positions, static_cast<hipStream_t>(stream));
+                    positions, false, static_cast<hipStream_t>(stream));
 }
 
 int k3_hip_spine_bf16_decode_bits(const uint16_t* input, uint32_t* output, int count,
@@ -71,7 +71,7 @@ int k3_hip_spine_int8_launch_v1(const int8_t* quantized, const float* row_scales
                                 const float* activation, float* output, int rows, int columns,
                                 int positions, void* stream) {
   return spine_gemv(K3_SPINE_KIND_INT8, quantized, row_scales, activation, output, rows, columns,
-                    positions, static_cast<hipStream_t>(stream));
+                    positions, false, static_cast<hipStream_t>(stream));
 }
 
 int k3_hip_rms_norm(const float* input, const float* weight, float* output, int rows, int columns,

@@ -10,6 +10,8 @@ path.
 """
 from __future__ import annotations
 
+import ctypes as C
+
 import torch
 
 from . import _lib
@@ -96,3 +98,78 @@ def decode_bits(bits: torch.Tensor) -> torch.Tensor:
                                                        bits.numel(), _stream()),
                      "k3_hip_spine_bf16_decode_bits")
     return out
+
+
+class MoeSpine:
+    """The eight resident spine slots of one MoE layer on the device
+    (MoeSpineT1, native/provider_gate/provider_moe.h:66-100), as the
+    K3HipMoeSpineV1 descriptor of k3_hip_moe_block_device.
+
+    Matrices are row-major device tensors: BF16 bits (int16 / uint16 /
+    bfloat16) for kind "bf16", int8 with fp32 row scales for kind "int8"."""
+
+    MATRICES = ("router", "routed_down", "routed_up", "shared_gate", "shared_up", "shared_down")
+
+    def __init__(self, kind: str, router, router_bias, routed_down, routed_norm, routed_up,
+                 shared_gate, shared_up, shared_down, scales: dict | None = None,
+                 top_k: int = 16):
+        if kind not in ("bf16", "int8"):
+            raise ValueError("kind must be 'bf16' or 'int8'")
+        self.kind = kind
+        self.router, self.router_bias = router, router_bias
+        self.routed_down, self.routed_norm, self.routed_up = routed_down, routed_norm, routed_up
+        self.shared_gate, self.shared_up, self.shared_down = shared_gate, shared_up, shared_down
+        self.scales = dict(scales or {})
+        self.top_k = top_k
+        self.hidden = router.shape[1]
+        self.routed_hidden = routed_down.shape[0]
+        self.shared_intermediate = shared_gate.shape[0]
+        self.experts = router.shape[0]
+        if kind == "int8" and set(self.scales) != set(self.MATRICES):
+            raise ValueError("row-int8 spines need a scale vector for every matrix")
+
+    def descriptor(self) -> _lib.K3HipMoeSpineV1:
+        d = _lib.K3HipMoeSpineV1()
+        d.abi_version = _lib.K3_MOE_SPINE_ABI_V1
+        d.struct_bytes = C.sizeof(_lib.K3HipMoeSpineV1)
+        d.matrix_kind = _lib.K3_SPINE_MATRIX_BF16 if self.kind == "bf16" else _lib.K3_SPINE_MATRIX_INT8
+        d.hidden, d.routed_hidden = self.hidden, self.routed_hidden
+        d.shared_intermediate, d.experts, d.top_k = self.shared_intermediate, self.experts, self.top_k
+        d.router_bias = self.router_bias.data_ptr()
+        d.routed_norm = self.routed_norm.data_ptr()
+        for name in self.MATRICES:
+            setattr(d, name, getattr(self, name).data_ptr())
+            if self.kind == "int8":
+                setattr(d, name + "_scales", self.scales[name].data_ptr())
+        return d
+
+
+def moe_block_workspace(spine: MoeSpine, g, max_positions: int) -> torch.Tensor:
+    lib = _lib.load()
+    d = spine.descriptor()
+    n = lib.k3_hip_moe_block_workspace_bytes(C.byref(d), C.byref(g), max_positions)
+    if n == 0:
+        raise ValueError(f"invalid spine / geometry / positions: {_lib.last_error()}")
+    return torch.empty(n, dtype=torch.uint8, device="cuda")
+
+
+def moe_block(spine: MoeSpine, g, bank: torch.Tensor, stride: int, hidden: torch.Tensor,
+              workspace: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """The K3 MoE block on the device for hidden [P, H] fp32; returns (out,
+    route_ids [P, top_k], route_weights [P, top_k])."""
+    h2 = hidden if hidden.dim() == 2 else hidden.view(1, -1)
+    _dense(h2, torch.float32, "hidden")
+    P = h2.shape[0]
+    if workspace is None:
+        workspace = moe_block_workspace(spine, g, P)
+    if out is None:
+        out = torch.empty(P, spine.hidden, dtype=torch.float32, device=hidden.device)
+    ids = torch.empty(P, spine.top_k, dtype=torch.int32, device=hidden.device)
+    wts = torch.empty(P, spine.top_k, dtype=torch.float32, device=hidden.device)
+    lib = _lib.load()
+    d = spine.descriptor()
+    _lib.check(lib.k3_hip_moe_block_device(
+        C.byref(d), C.byref(g), bank.data_ptr(), stride, h2.data_ptr(), P, out.data_ptr(),
+        ids.data_ptr(), wts.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream()),
+        "k3_hip_moe_block_device")
+    return out, ids, wts

@@ -389,6 +389,70 @@ int k3_hip_synth_bank(const K3HipGeometryV1* g, uint8_t* bank,
 int k3_hip_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed,
                         uint64_t stream, void* stream_handle);
 
+/* ============================== the whole K3 MoE block on the device */
+/* The eight resident spine slots of one MoE layer (MoeSpineT1,
+ * native/provider_gate/provider_moe.h:66-100; shapes checked as
+ * validate_spine does, provider_moe.cpp:419-450), as device pointers.  Every
+ * matrix is row-major [rows, columns] in one storage form: BF16 bits
+ * (K3_SPINE_MATRIX_BF16; the *_scales pointers are ignored) or row-int8 with
+ * one fp32 scale per row (K3_SPINE_MATRIX_INT8; scales required).  The
+ * reference's geometry is hidden 7168, routed_hidden 3584, shared 6144,
+ * experts 896, top_k 16 (k3_moe_geometry, provider_moe.h:40-42). */
+#define K3_SPINE_MATRIX_BF16 0
+#define K3_SPINE_MATRIX_INT8 1
+#define K3_MOE_SPINE_ABI_V1 1
+typedef struct K3HipMoeSpineV1 {
+  uint32_t abi_version;          /* K3_MOE_SPINE_ABI_V1 */
+  uint32_t struct_bytes;         /* sizeof(K3HipMoeSpineV1) == 144 */
+  uint32_t matrix_kind;          /* K3_SPINE_MATRIX_* */
+  uint32_t hidden;               /* H: block input / output width */
+  uint32_t routed_hidden;        /* R: expert width (= expert geometry hidden) */
+  uint32_t shared_intermediate;  /* S */
+  uint32_t experts;              /* E: router rows = bank experts (<= 4096) */
+  uint32_t top_k;                /* routed experts per token (<= 32) */
+  const void* router;            /* [E, H] */
+  const float* router_scales;    /* [E] (int8) */
+  const float* router_bias;      /* [E] fp32 correction bias */
+  const void* routed_down;       /* [R, H] */
+  const float* routed_down_scales;
+  const float* routed_norm;      /* [R] fp32 RMS-norm weight */
+  const void* routed_up;         /* [H, R] */
+  const float* routed_up_scales;
+  const void* shared_gate;       /* [S, H] */
+  const float* shared_gate_scales;
+  const void* shared_up;         /* [S, H] */
+  const float* shared_up_scales;
+  const void* shared_down;       /* [H, S] */
+  const float* shared_down_scales;
+} K3HipMoeSpineV1;
+
+/* Workspace bytes of k3_hip_moe_block_device for up to max_positions. */
+uint64_t k3_hip_moe_block_workspace_bytes(const K3HipMoeSpineV1* spine,
+                                          const K3HipGeometryV1* experts,
+                                          int max_positions);
+
+/* The K3 MoE block for n_positions tokens (1..16) in one stream-ordered call,
+ * replacing prepare_moe_t1 / complete_moe_t1 and their position forms
+ * (provider_moe.cpp:1660-1700, :1970-2014) around the routed expert set:
+ *   logits   = router hidden;  scores = sigmoid(logits)
+ *   route    = top_k of scores + router_bias (descending, lower index on
+ *              ties), weights = scores[route] / (sum + 1e-20)
+ *   routed   = sum_{route order} w_e expert_e(routed_down hidden)
+ *              (the experts of `experts`, SiTU, from bank + id * stride)
+ *   out      = routed_up (routed_norm * rms_norm(routed, eps 1e-5))
+ *            + shared_down situ(shared_gate hidden, shared_up hidden)
+ * hidden, out: device fp32 [n_positions, H] (16-byte aligned); route_ids /
+ * route_weights (device, nullable): [n_positions, top_k].  Every product is
+ * fp32.  The experts of a batch go through the verify paths
+ * (k3_hip_set_verify_mode).  Returns a K3_HIP_* status. */
+int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine,
+                            const K3HipGeometryV1* experts,
+                            const uint8_t* bank, uint64_t expert_stride,
+                            const float* hidden, int n_positions, float* out,
+                            int32_t* route_ids, float* route_weights,
+                            void* workspace, uint64_t workspace_bytes,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,7 @@ enum {
 
 #define K3_SPINE_ABI_VERSION 1u
 #define K3_SPINE_MAX_POSITIONS 64
+#define K3_RMS_EPSILON 1.0e-5f /* the reference's kRmsEpsilon (provider_moe.cpp:87) */
 
 /* Replaces k3_cuda_spine_bf16_abi_version (provider_spine_bf16_cuda.cu:187-189). */
 uint32_t k3_hip_spine_bf16_abi_version(void);

@@ -17,12 +17,26 @@ Restates, in float64 numpy:
   rms_norm_f64       weight * (x / sqrt(mean(x^2) + eps)) (provider_moe.cpp:535-542)
   spine_fixture      the reference gate's deterministic matrix fixture
                      (provider_spine_bf16_cuda_test.cpp:235-276)
+  k3_router_f64      top-k of sigmoid(logits) + bias, weights = the selected
+                     sigmoids over their sum + 1e-20 (prepare_moe_t1,
+                     provider_moe.cpp:1673-1683); descending, lower index on ties
+  moe_block_f64      the whole K3 MoE block (prepare_moe_t1 + the routed expert
+                     set + complete_moe_t1, provider_moe.cpp:1660-1700,
+                     :1970-2014) in float64, the experts through oracle's
+                     moe_layer_f64 (SiTU)
+  tiny_fixture       the reference's tiny-geometry MoE fixture
+                     (provider_moe_test.cpp:50-191: make_row_int8, make_spine,
+                     test_code / encode_expert)
 
 Pins (tests/test_oracle_spine.py): the BF16 decode against the closed-form
 values of the sixteen fixture patterns and of IEEE special encodings; the GEMVs
 against pure-Python loops on small shapes, linearity in x, one-hot columns and
 the dense materialisation; the RMS norm against constant rows (closed form),
-scale invariance and a hand-computed row.
+scale invariance and a hand-computed row; the K3 router against the pinned
+top-k of the logits (zero bias: sigmoid is monotone), a pure-Python sort and
+forced selections; the block, on the reference's tiny fixture, against an
+independent dense float64 composition (the fixture's experts decoded with
+ldexp as provider_moe_test.cpp:132-153 does, every step a plain matmul).
 """
 from __future__ import annotations
 
@@ -51,19 +65,18 @@ def spine_bf16_f64(weights: np.ndarray, x: np.ndarray) -> np.ndarray:
     """weights uint16 [rows, cols], x float32 [positions, cols] -> float64
     [positions, rows]."""
     w = bf16_to_f32(weights).astype(np.float64)
-    return np.asarray(x, dtype=np.float32).astype(np.float64) @ w.T
+    return np.asarray(x, dtype=np.float64) @ w.T
 
 
 def spine_int8_f64(q: np.ndarray, scales: np.ndarray, x: np.ndarray) -> np.ndarray:
     """q int8 [rows, cols], scales float32 [rows], x float32 [positions, cols]
     -> float64 [positions, rows]."""
-    dots = np.asarray(x, dtype=np.float32).astype(np.float64) @ np.asarray(q, np.int8).astype(
-        np.float64).T
+    dots = np.asarray(x, dtype=np.float64) @ np.asarray(q, np.int8).astype(np.float64).T
     return dots * np.asarray(scales, dtype=np.float32).astype(np.float64)[None, :]
 
 
 def rms_norm_f64(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
-    x64 = np.asarray(x, dtype=np.float32).astype(np.float64)
+    x64 = np.asarray(x, dtype=np.float64)
     var = np.mean(x64 * x64, axis=-1, keepdims=True)
     return np.asarray(weight, np.float32).astype(np.float64) * (x64 / np.sqrt(var + np.float64(
         np.float32(eps))))
@@ -87,3 +100,132 @@ def spine_close(found: np.ndarray, expected: np.ndarray) -> bool:
     expected = np.asarray(expected, np.float64)
     tol = SPINE_TOLERANCE_ABS + SPINE_TOLERANCE_REL * np.abs(expected)
     return bool(np.all(np.isfinite(found)) and np.all(np.abs(found - expected) <= tol))
+
+
+# ------------------------------------------------------------ the K3 MoE block
+
+SITU_BETA = 4.0           # kSituBeta, provider_moe.cpp:85
+SITU_LINEAR_BETA = 25.0   # kSituLinearBeta, :86
+RMS_EPS = 1.0e-5          # kRmsEpsilon, :87
+
+
+def sigmoid_f64(v):
+    return 1.0 / (1.0 + np.exp(-np.asarray(v, np.float64)))
+
+
+def situ_f64(g, u):
+    """[4 tanh(g/4) sigmoid(g)] [25 tanh(u/25)] (provider_moe.cpp:524-533)."""
+    g = np.asarray(g, np.float64)
+    u = np.asarray(u, np.float64)
+    return (np.tanh(g / SITU_BETA) * SITU_BETA * sigmoid_f64(g)) * (
+        np.tanh(u / SITU_LINEAR_BETA) * SITU_LINEAR_BETA)
+
+
+def k3_router_f64(logits, bias, k: int):
+    """(ids int32 [k], weights float64 [k]) for one position."""
+    scores = sigmoid_f64(logits)
+    choice = scores + np.asarray(bias, np.float64)
+    order = np.lexsort((np.arange(choice.size), -choice))  # descending, lower index first
+    ids = order[:k].astype(np.int32)
+    sel = scores[ids]
+    return ids, sel / (sel.sum() + 1e-20)
+
+
+def _linear(kind: str, m: dict, name: str, x):
+    if kind == "bf16":
+        return spine_bf16_f64(m[name], x)
+    return spine_int8_f64(m[name], m[name + "_scales"], x)
+
+
+def moe_block_f64(kind: str, m: dict, expert_span, hidden, inter: int, k: int):
+    """The K3 block for hidden [P, H]; m holds the spine as numpy arrays
+    (router, router_bias, routed_down, routed_norm, routed_up, shared_gate,
+    shared_up, shared_down, and *_scales for kind "int8"); expert_span(id)
+    returns that expert's raw-v1 bytes.  Returns (out [P, H], ids [P, k],
+    weights [P, k], routed [P, R]) in float64."""
+    import oracle
+    x = np.atleast_2d(np.asarray(hidden, np.float64))
+    R = m["routed_down"].shape[0]
+    outs, all_ids, all_w, routed_all = [], [], [], []
+    for p in range(x.shape[0]):
+        xp = x[p:p + 1]
+        logits = _linear(kind, m, "router", xp)[0]
+        ids, w = k3_router_f64(logits, m["router_bias"], k)
+        routed_in = _linear(kind, m, "routed_down", xp)[0]
+        routed, _ = oracle.moe_layer_f64([expert_span(int(e)) for e in ids], w, R, inter,
+                                         oracle.ACT_SITU, routed_in)
+        norm = rms_norm_f64(routed[None, :], m["routed_norm"], RMS_EPS)
+        routed_full = _linear(kind, m, "routed_up", norm)[0]
+        h = situ_f64(_linear(kind, m, "shared_gate", xp), _linear(kind, m, "shared_up", xp))
+        shared = _linear(kind, m, "shared_down", h)[0]
+        outs.append(routed_full + shared)
+        all_ids.append(ids)
+        all_w.append(w)
+        routed_all.append(routed)
+    return np.array(outs), np.array(all_ids), np.array(all_w), np.array(routed_all)
+
+
+# The reference's tiny MoE geometry (kTestGeometry, provider_moe_test.cpp:50):
+# hidden, routed_hidden, intermediate, experts, shared_intermediate.
+TINY = dict(hidden=32, routed_hidden=32, intermediate=32, experts=16, shared_intermediate=64)
+
+
+def row_int8_fixture(rows: int, cols: int, seed: int):
+    """make_row_int8 (provider_moe_test.cpp:155-174): (q int8, scales float32)."""
+    r = np.arange(rows, dtype=np.int64)[:, None]
+    c = np.arange(cols, dtype=np.int64)[None, :]
+    q = (((r * 3 + c * 5 + seed * 7) % 9) - 4).astype(np.int8)
+    s = ((1 + (np.arange(rows) + seed) % 3).astype(np.float32) / np.float32(64.0))
+    return q, s
+
+
+def tiny_spine() -> dict:
+    """make_spine (provider_moe_test.cpp:176-191) as numpy arrays."""
+    m = {}
+    for name, (rows, cols, seed) in {
+            "router": (16, 32, 1), "routed_down": (32, 32, 2), "routed_up": (32, 32, 3),
+            "shared_gate": (64, 32, 4), "shared_up": (64, 32, 5),
+            "shared_down": (32, 64, 6)}.items():
+        m[name], m[name + "_scales"] = row_int8_fixture(rows, cols, seed)
+    m["router_bias"] = (np.arange(16, dtype=np.float32) * np.float32(1.0 / 4096.0))
+    m["routed_norm"] = np.linspace(0.75, 1.25, 32, dtype=np.float64).astype(np.float32)
+    return m
+
+
+def tiny_test_code(expert: int, matrix: int, row: int, column: int) -> int:
+    """test_code (provider_moe_test.cpp:98-106)."""
+    mag = 1 + ((expert * 3 + matrix * 5 + row * 7 + column * 11) % 4)
+    if (expert + matrix + row + column) & 1:
+        mag |= 8
+    return mag
+
+
+def tiny_expert_span(expert: int, hidden: int = 32, inter: int = 32) -> np.ndarray:
+    """encode_expert (provider_moe_test.cpp:108-130) over the raw-v1 layout of
+    (routed_hidden, intermediate) = (hidden, inter): w1 [I, H], w2 [H, I],
+    w3 [I, H], each packed (low nibble = even column) then its E8M0 scales."""
+    p13, s13 = inter * hidden // 2, inter * hidden // 32
+    p2, s2 = hidden * inter // 2, hidden * inter // 32
+    layouts = [(0, p13, inter, hidden), (p13 + s13, p13 + s13 + p2, hidden, inter),
+               (p13 + s13 + p2 + s2, p13 + s13 + p2 + s2 + p13, inter, hidden)]
+    span = np.zeros(2 * (p13 + s13) + p2 + s2, np.uint8)
+    for mat, (po, so, rows, cols) in enumerate(layouts):
+        for r in range(rows):
+            for c in range(0, cols, 2):
+                lo = tiny_test_code(expert, mat, r, c)
+                hi = tiny_test_code(expert, mat, r, c + 1)
+                span[po + r * (cols // 2) + c // 2] = lo | (hi << 4)
+            for gi in range(cols // 32):
+                span[so + r * (cols // 32) + gi] = 123 + ((expert + mat + r + gi) % 4)
+    return span
+
+
+def tiny_hidden(positions: int) -> np.ndarray:
+    """The fixture's hidden rows: linspace(-0.25, 0.375, 32) for one position
+    (parity_test, :275-277), linspace(-0.375, 0.625, 3 * 32) for three
+    (position_prepare_complete_parity_test, :299-302)."""
+    if positions == 1:
+        return np.linspace(-0.25, 0.375, 32, dtype=np.float64).astype(np.float32)[None, :]
+    if positions == 3:
+        return np.linspace(-0.375, 0.625, 96, dtype=np.float64).astype(np.float32).reshape(3, 32)
+    raise ValueError("the reference fixture has 1 or 3 positions")

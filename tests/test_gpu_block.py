@@ -1,0 +1,174 @@
+"""GPU parity of the whole K3 MoE block (k3_hip_moe_block_device): router,
+sigmoid + bias top-16, routed_down, the routed experts, RMS norm, routed_up
+and the shared SiTU expert, against the float64 oracle (oracle/spine.py
+moe_block_f64):
+
+* the reference's own tiny-geometry fixture (provider_moe_test.cpp:50-191:
+  row-int8 spine, 16 closed-form experts, hidden 32 / routed 32 /
+  intermediate 32 / shared 64) at one and three positions, under the
+  reference's bound max |out - expected| <= 2e-4 (:291);
+* the K3 geometry (hidden 7168, routed 3584, intermediate 3072, shared 6144,
+  896 experts in a device bank) with BF16 and row-int8 spines at 1, 2 and 4
+  positions, normwise error <= 1e-3 and route ids identical;
+* 16 positions, where AUTO takes the union path: outputs equal the
+  one-decode-layer-per-position path's within 1e-4 normwise, same routes.
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+from oracle import spine as S
+
+pytestmark = pytest.mark.gpu
+
+K3 = dict(hidden=7168, routed=3584, inter=3072, shared=6144, experts=896, top_k=16)
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _spine_from(kind, m):
+    from deltafin_amd import spine
+    mats = {}
+    scales = {}
+    for name in spine.MoeSpine.MATRICES:
+        a = m[name]
+        mats[name] = _dev(a.view(np.int16) if kind == "bf16" else a)
+        if kind == "int8":
+            scales[name] = _dev(m[name + "_scales"].astype(np.float32))
+    return spine.MoeSpine(kind, mats["router"], _dev(m["router_bias"].astype(np.float32)),
+                          mats["routed_down"], _dev(m["routed_norm"].astype(np.float32)),
+                          mats["routed_up"], mats["shared_gate"], mats["shared_up"],
+                          mats["shared_down"], scales=scales if kind == "int8" else None)
+
+
+@pytest.mark.parametrize("positions", [1, 3])
+def test_block_reference_tiny_fixture(gpu, positions):
+    import torch
+    from deltafin_amd import _lib, spine
+    say(f"block: reference tiny fixture, positions {positions}")
+    m = S.tiny_spine()
+    g = _lib.geometry(32, 32, _lib.K3_ACT_SITU)
+    spans = np.concatenate([S.tiny_expert_span(e) for e in range(16)])
+    stride = g.expert_span
+    bank = _dev(spans)
+    hidden = S.tiny_hidden(positions)
+    sp = _spine_from("int8", m)
+    out, ids, wts = spine.moe_block(sp, g, bank, stride, _dev(hidden))
+    torch.cuda.synchronize()
+    want, want_ids, want_w, _ = S.moe_block_f64("int8", m, S.tiny_expert_span, hidden, 32, 16)
+    assert ids.cpu().numpy().tolist() == want_ids.tolist()
+    assert np.max(np.abs(wts.cpu().numpy() - want_w)) <= 1e-6
+    err = np.max(np.abs(out.cpu().numpy().astype(np.float64) - want))
+    assert err <= 2.0e-4, f"max abs error {err:.3e} above the reference's 2e-4"
+
+
+def _k3_spine(kind, seed):
+    rng = np.random.default_rng(seed)
+    H, R, Sh, E = K3["hidden"], K3["routed"], K3["shared"], K3["experts"]
+    shapes = {"router": (E, H), "routed_down": (R, H), "routed_up": (H, R),
+              "shared_gate": (Sh, H), "shared_up": (Sh, H), "shared_down": (H, Sh)}
+    m = {}
+    for name, (rows, cols) in shapes.items():
+        if kind == "bf16":
+            v = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+            m[name] = (v.view(np.uint32) >> 16).astype(np.uint16)
+        else:
+            m[name] = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
+            m[name + "_scales"] = (rng.uniform(0.5, 1.5, rows) * 0.02 / 64).astype(np.float32)
+    m["router_bias"] = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    m["routed_norm"] = (1.0 + 0.1 * rng.standard_normal(R)).astype(np.float32)
+    return m
+
+
+@pytest.fixture(scope="module")
+def k3_bank(gpu):
+    import torch
+    from deltafin_amd import _lib, moe
+    g = _lib.preset(1)
+    stride = g.expert_span
+    bank = torch.empty(K3["experts"] * stride, dtype=torch.uint8, device="cuda")
+    moe.synth_bank(g, bank, stride, K3["experts"], 0, 4242)
+    torch.cuda.synchronize()
+    cache = {}
+
+    def span(e):
+        if e not in cache:
+            cache[e] = bank[e * stride:(e + 1) * stride].cpu().numpy()
+        return cache[e]
+    return g, bank, stride, span
+
+
+def _normwise(got, want):
+    return float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+
+
+@pytest.mark.parametrize("kind,positions", [("bf16", 1), ("bf16", 4), ("int8", 2)])
+def test_block_k3_geometry(gpu, k3_bank, kind, positions):
+    import torch
+    from deltafin_amd import spine
+    g, bank, stride, span = k3_bank
+    say(f"block: K3 geometry, {kind} spine, positions {positions}")
+    m = _k3_spine(kind, zlib.crc32(f"{kind}{positions}".encode()))
+    hidden = np.random.default_rng(positions).standard_normal(
+        (positions, K3["hidden"]), dtype=np.float32)
+    sp = _spine_from(kind, m)
+    out, ids, wts = spine.moe_block(sp, g, bank, stride, _dev(hidden))
+    torch.cuda.synchronize()
+    want, want_ids, want_w, _ = S.moe_block_f64(kind, m, span, hidden, K3["inter"], 16)
+    assert ids.cpu().numpy().tolist() == want_ids.tolist(), "route ids differ"
+    assert np.max(np.abs(wts.cpu().numpy() - want_w)) <= 1e-6
+    got = out.cpu().numpy().astype(np.float64)
+    for p in range(positions):
+        err = _normwise(got[p], want[p])
+        assert err <= 1e-3, f"position {p}: normwise error {err:.3e}"
+
+
+def test_block_union_matches_positions(gpu, k3_bank):
+    import torch
+    from deltafin_amd import _lib, spine
+    g, bank, stride, _ = k3_bank
+    say("block: 16 positions, union path vs one decode layer per position")
+    m = _k3_spine("bf16", 99)
+    hidden = _dev(np.random.default_rng(16).standard_normal((16, K3["hidden"]), dtype=np.float32))
+    sp = _spine_from("bf16", m)
+    ws = spine.moe_block_workspace(sp, g, 16)
+    out_auto, ids_auto, _ = spine.moe_block(sp, g, bank, stride, hidden, workspace=ws)
+    prev = _lib.set_verify_mode(_lib.VERIFY_POSITIONS)
+    try:
+        out_pos, ids_pos, _ = spine.moe_block(sp, g, bank, stride, hidden, workspace=ws)
+    finally:
+        _lib.set_verify_mode(prev)
+    torch.cuda.synchronize()
+    assert torch.equal(ids_auto, ids_pos)
+    a = out_auto.cpu().numpy().astype(np.float64)
+    b = out_pos.cpu().numpy().astype(np.float64)
+    for p in range(16):
+        assert _normwise(a[p], b[p]) <= 1e-4, f"position {p}"
+
+
+def test_block_rejects_bad_calls(gpu, k3_bank):
+    import ctypes as C
+    from deltafin_amd import _lib, spine
+    g, bank, stride, _ = k3_bank
+    say("block: argument checks")
+    m = S.tiny_spine()
+    sp = _spine_from("int8", m)
+    d = sp.descriptor()
+    lib = _lib.load()
+    # the tiny spine's routed width (32) differs from the K3 expert geometry
+    assert lib.k3_hip_moe_block_workspace_bytes(C.byref(d), C.byref(g), 1) == 0
+    d.struct_bytes = 100
+    g32 = _lib.geometry(32, 32, _lib.K3_ACT_SITU)
+    assert lib.k3_hip_moe_block_workspace_bytes(C.byref(d), C.byref(g32), 1) == 0
+    with pytest.raises(_lib.K3HipError) as e:
+        spine.moe_block(sp, g, bank, stride, _dev(np.zeros((1, 32), np.float32)),
+                        workspace=_dev(np.zeros(1 << 20, np.uint8)))
+    assert e.value.status == _lib.K3_HIP_E_INVALID

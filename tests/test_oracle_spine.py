@@ -141,3 +141,104 @@ def test_spine_available_without_device():
     from deltafin_amd import _lib
     lib = _lib.load()
     assert lib.k3_hip_spine_bf16_available(0, None, None) < 0
+
+
+# ----------------------------------------------------------- K3 router and block
+
+
+def test_k3_router_zero_bias_is_topk_of_logits():
+    import oracle
+    rng = np.random.default_rng(11)
+    logits = rng.standard_normal(896).astype(np.float32)
+    ids, w = S.k3_router_f64(logits, np.zeros(896, np.float32), 16)
+    ref_ids, _ = oracle.topk_softmax(logits, 16)  # sigmoid is monotone
+    assert ids.tolist() == ref_ids.tolist()
+    s = 1 / (1 + np.exp(-logits[ids].astype(np.float64)))
+    assert np.allclose(w, s / s.sum(), rtol=1e-14)
+
+
+def test_k3_router_python_sort_and_forced():
+    rng = np.random.default_rng(12)
+    logits = rng.standard_normal(40).astype(np.float32)
+    bias = (rng.standard_normal(40) * 0.3).astype(np.float32)
+    ids, w = S.k3_router_f64(logits, bias, 7)
+    sc = [1 / (1 + math.exp(-float(v))) for v in logits]
+    order = sorted(range(40), key=lambda i: (-(sc[i] + float(bias[i])), i))[:7]
+    assert ids.tolist() == order
+    tot = sum(sc[i] for i in order)
+    assert np.allclose(w, [sc[i] / (tot + 1e-20) for i in order], rtol=1e-14)
+    forced = np.zeros(40, np.float32)
+    forced[[5, 33, 17]] = np.float32(10.0)  # dominates any sigmoid difference
+    ids, w = S.k3_router_f64(logits, forced, 3)
+    assert sorted(ids.tolist()) == [5, 17, 33]
+    assert np.isclose(w.sum(), 1.0, rtol=1e-14)
+    ties = np.zeros(8, np.float32)
+    ids, _ = S.k3_router_f64(ties, ties, 4)  # all equal: lower index first
+    assert ids.tolist() == [0, 1, 2, 3]
+
+
+def test_tiny_expert_layout_matches_raw_v1_offsets():
+    import oracle
+    span = S.tiny_expert_span(3)
+    off = oracle.expert_offsets(32, 32)  # w1p, w1s, w2p, w2s, w3p, w3s, span
+    assert span.size == off[-1]
+    # expert 3, matrix 0, row 0: columns 0 and 1 -> one byte, scale 123 + 3
+    assert span[off[0]] == S.tiny_test_code(3, 0, 0, 0) | (S.tiny_test_code(3, 0, 0, 1) << 4)
+    assert span[off[1]] == 123 + 3
+    assert span[off[3]] == 123 + (3 + 1) % 4 and span[off[5]] == 123 + (3 + 2) % 4
+
+
+def _dense_block(m, hidden):
+    """The fixture block as plain float64 matmuls, the experts decoded with
+    ldexp (provider_moe_test.cpp:132-153, :193-264) -- an independent path."""
+    e2m1 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+
+    def decode(span, po, so, rows, cols):
+        w = np.empty((rows, cols))
+        for r in range(rows):
+            for c in range(cols):
+                b = int(span[po + r * (cols // 2) + c // 2])
+                code = b & 15 if c % 2 == 0 else b >> 4
+                v = e2m1[code & 7] * (-1.0 if code & 8 else 1.0)
+                w[r, c] = math.ldexp(v, int(span[so + r * (cols // 32) + c // 32]) - 127)
+        return w
+
+    def dense(name):
+        return m[name].astype(np.float64) * m[name + "_scales"].astype(np.float64)[:, None]
+
+    def situ(g, u):
+        return (np.tanh(g / 4) * 4 / (1 + np.exp(-g))) * (np.tanh(u / 25) * 25)
+
+    p13, s13, p2, s2 = 512, 32, 512, 32
+    experts = {}
+    for e in range(16):
+        sp = S.tiny_expert_span(e)
+        experts[e] = (decode(sp, 0, p13, 32, 32), decode(sp, p13 + s13, p13 + s13 + p2, 32, 32),
+                      decode(sp, p13 + s13 + p2 + s2, 2 * p13 + s13 + p2 + s2, 32, 32))
+    outs = []
+    for x in np.atleast_2d(hidden).astype(np.float64):
+        scores = 1 / (1 + np.exp(-(dense("router") @ x)))
+        choice = scores + m["router_bias"].astype(np.float64)
+        ids = sorted(range(16), key=lambda i: (-choice[i], i))
+        w = scores[ids] / (scores[ids].sum() + 1e-20)
+        rin = dense("routed_down") @ x
+        routed = np.zeros(32)
+        for e, we in zip(ids, w):
+            w1, w2, w3 = experts[e]
+            routed += we * (w2 @ situ(w1 @ rin, w3 @ rin))
+        norm = m["routed_norm"].astype(np.float64) * (routed / np.sqrt(np.mean(routed ** 2) +
+                                                                     float(np.float32(1e-5))))
+        shared = dense("shared_down") @ situ(dense("shared_gate") @ x, dense("shared_up") @ x)
+        outs.append(dense("routed_up") @ norm + shared)
+    return np.array(outs)
+
+
+@pytest.mark.parametrize("positions", [1, 3])
+def test_block_oracle_on_reference_tiny_fixture(positions):
+    m = S.tiny_spine()
+    hidden = S.tiny_hidden(positions)
+    out, ids, w, _ = S.moe_block_f64("int8", m, S.tiny_expert_span, hidden, 32, 16)
+    want = _dense_block(m, hidden)
+    assert out.shape == (positions, 32) and ids.shape == (positions, 16)
+    assert np.max(np.abs(out - want)) <= 1e-10 * max(1.0, np.max(np.abs(want)))
+    assert sorted(ids[0].tolist()) == list(range(16))  # top 16 of 16: every expert
