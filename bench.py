@@ -94,6 +94,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--spine-only", action="store_true",
                     help="print only the spine-projection timings (K3 spine shapes)")
     ap.add_argument("--no-spine", action="store_true", help="skip the spine timings")
+    ap.add_argument("--block-only", action="store_true",
+                    help="print only the whole-K3-MoE-block timings")
+    ap.add_argument("--no-block", action="store_true", help="skip the K3 MoE block timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 4 plain device copies of 1 GiB (the known-size kernel "
                          "the HBM byte counters are scaled by) and exit")
@@ -474,10 +477,10 @@ def main() -> int:
         print(json.dumps(_verify_config3(moe, _lib, g, bank, stride, max(1, args.verify_batches))),
               flush=True)
         return 0
-    if args.spine_only:
+    if args.spine_only or args.block_only:
         del bank
         torch.cuda.empty_cache()
-        print(json.dumps(_spine_bench()), flush=True)
+        print(json.dumps(_spine_bench() if args.spine_only else _k3_block_bench()), flush=True)
         return 0
 
     fn = lib.k3_hip_moe_route_layer_device
@@ -601,6 +604,8 @@ def main() -> int:
         res["verify"] = _verify_config3(moe, _lib, g, bank, stride, args.verify_batches)
     if not args.no_spine:
         res["spine"] = _spine_bench()
+    if not args.no_block:
+        res["k3_block"] = _k3_block_bench()
     if args.streamed_line_tokens > 0:
         try:
             res["streamed"] = streamed_config4(args.streamed_line_tokens)
@@ -828,6 +833,75 @@ def _spine_bench(launches: int = 24) -> dict:
         log(f"spine {kind}: " + ", ".join(
             f"{n} {per_kind[n]['p1']['us']}us/{per_kind[n]['p1']['gbs']}GB/s" for n, _, _ in
             SPINE_SHAPES) + f"; all five p1 {per_kind['all_five']['p1']}")
+    return out
+
+
+K3_BLOCK_EXPERTS = 896
+K3_BLOCK_POSITIONS = (1, 4)
+
+
+def _k3_block_bench(calls: int = 20) -> dict:
+    """The whole K3 MoE block (k3_hip_moe_block_device) at the reference's
+    geometry: BF16 spine (router 896 x 7168, routed_down, routed_up, shared
+    gate / up / down; 380 MB) and a bank of 896 raw-v1 K3 experts (15.7 GB),
+    fresh N(0,1) hidden rows per call (so the routes move).  `device_us` sums
+    the kernels' dispatch stamps per call; `wall_us` is the host-timed call
+    rate.  Algorithmic bytes per position-batch = spine + unique routed
+    experts x 17,547,264 + activations."""
+    import torch
+
+    from deltafin_amd import _lib, moe, spine
+
+    g = _lib.preset(1)
+    stride = g.expert_span
+    bank = torch.empty(K3_BLOCK_EXPERTS * stride, dtype=torch.uint8, device="cuda")
+    moe.synth_bank(g, bank, stride, K3_BLOCK_EXPERTS, 0, SEED)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED + 1)
+    H, R, S = 7168, 3584, 6144
+
+    def mat(rows, cols):
+        return (torch.randn(rows, cols, device="cuda", generator=gen) * 0.02).to(
+            torch.bfloat16).view(torch.int16)
+
+    sp = spine.MoeSpine("bf16", mat(K3_BLOCK_EXPERTS, H),
+                        torch.randn(K3_BLOCK_EXPERTS, device="cuda", generator=gen) * 0.01,
+                        mat(R, H), 1 + 0.1 * torch.randn(R, device="cuda", generator=gen),
+                        mat(H, R), mat(S, H), mat(S, H), mat(H, S))
+    spine_bytes = 2 * (K3_BLOCK_EXPERTS * H + 2 * R * H + 3 * S * H)
+    out = {"experts": K3_BLOCK_EXPERTS, "spine_bytes": spine_bytes, "calls": calls,
+           "expert_span": stride}
+    for P in K3_BLOCK_POSITIONS:
+        ws = spine.moe_block_workspace(sp, g, P)
+        xs = torch.randn(calls + 3, P, H, device="cuda", generator=gen)
+        for i in range(3):
+            spine.moe_block(sp, g, bank, stride, xs[i], workspace=ws)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ids_all = []
+        for i in range(3, calls + 3):
+            _, ids, _ = spine.moe_block(sp, g, bank, stride, xs[i], workspace=ws)
+            ids_all.append(ids)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / calls
+        _lib.timing_begin(64 * calls)
+        for i in range(3, calls + 3):
+            spine.moe_block(sp, g, bank, stride, xs[i], workspace=ws)
+        torch.cuda.synchronize()
+        kern, _ = _lib.timing_end()
+        kus = {k: round(v["total_ms"] * 1e3 / calls, 2) for k, v in kern.items()}
+        dev = sum(kus.values())
+        union = float(np.mean([len(set(t.cpu().numpy().ravel().tolist())) for t in ids_all]))
+        alg = spine_bytes + union * stride + P * (2 * H + R) * 4
+        out[f"p{P}"] = {
+            "wall_us": round(wall * 1e6, 1), "device_us": round(dev, 1),
+            "token_layers_per_s": round(P / wall, 1), "union_experts": round(union, 1),
+            "algorithmic_bytes": int(alg), "achieved_gbs": round(alg / wall / 1e9, 1),
+            "hbm_frac": round(alg / wall / 1e9 / HBM_PEAK_GBS, 4), "kernels_us": kus}
+        log(f"k3 block P={P}: {wall * 1e6:.1f} us/call (device {dev:.1f}), "
+            f"{alg / wall / 1e9:.0f} GB/s, kernels {kus}")
+    del bank
+    torch.cuda.empty_cache()
     return out
 
 

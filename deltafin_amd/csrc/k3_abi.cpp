@@ -818,21 +818,56 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   if ((rc = experts_on_device_routes(g, bank, expert_stride, E, P, top_k, b.routed_in,
                                      b.routed_out, ws, st)))
     return rc;
-  // the shared expert: h = situ(gate, up) overwrites gate
-  if ((rc = from_spine(spine_gemv(kind, sp.shared_gate, sp.shared_gate_scales, hidden, b.gate, S,
-                                  H, P, false, st), "shared_gate")))
+  // the shared expert: h = situ(gate, up), one launch reading each gate row
+  // and its up row together (two launches and the activation where the shape
+  // has no fused form); h overwrites gate
+  SpineOp glu{};
+  glu.w = sp.shared_gate;
+  glu.scales = sp.shared_gate_scales;
+  glu.w2 = sp.shared_up;
+  glu.scales2 = sp.shared_up_scales;
+  glu.act = K3_ACT_SITU;
+  glu.x = hidden;
+  glu.y = b.gate;
+  glu.rows = S;
+  glu.cols = H;
+  glu.positions = P;
+  rc = spine_gemv_op(kind, glu, st);
+  if (rc == K3_SPINE_E_UNSUPPORTED) {
+    if ((rc = from_spine(spine_gemv(kind, sp.shared_gate, sp.shared_gate_scales, hidden, b.gate,
+                                    S, H, P, false, st), "shared_gate")))
+      return rc;
+    if ((rc = from_spine(spine_gemv(kind, sp.shared_up, sp.shared_up_scales, hidden, b.up, S, H,
+                                    P, false, st), "shared_up")))
+      return rc;
+    if ((rc = launch_activation(b.gate, b.up, b.gate, (int64_t)P * S, K3_ACT_SITU, st)))
+      return rc;
+  } else if ((rc = from_spine(rc, "shared gate/up"))) {
     return rc;
-  if ((rc = from_spine(spine_gemv(kind, sp.shared_up, sp.shared_up_scales, hidden, b.up, S, H, P,
-                                  false, st), "shared_up")))
+  }
+  // complete: routed_up over the routed RMS norm (staged normalised by the
+  // projection itself where the shape allows), + shared_down h (one fp32 add)
+  SpineOp up{};
+  up.w = sp.routed_up;
+  up.scales = sp.routed_up_scales;
+  up.x = b.routed_out;
+  up.y = out;
+  up.rows = H;
+  up.cols = R;
+  up.positions = P;
+  up.norm_w = sp.routed_norm;
+  up.eps = K3_RMS_EPSILON;
+  rc = spine_gemv_op(kind, up, st);
+  if (rc == K3_SPINE_E_UNSUPPORTED) {
+    if ((rc = from_spine(spine_rms_norm(b.routed_out, sp.routed_norm, b.routed_out, P, R,
+                                        K3_RMS_EPSILON, st), "routed RMS norm")))
+      return rc;
+    if ((rc = from_spine(spine_gemv(kind, sp.routed_up, sp.routed_up_scales, b.routed_out, out,
+                                    H, R, P, false, st), "routed_up")))
+      return rc;
+  } else if ((rc = from_spine(rc, "routed_up"))) {
     return rc;
-  if ((rc = launch_activation(b.gate, b.up, b.gate, (int64_t)P * S, K3_ACT_SITU, st))) return rc;
-  // complete: routed RMS norm, routed_up, + shared_down h (one fp32 add)
-  if ((rc = from_spine(spine_rms_norm(b.routed_out, sp.routed_norm, b.routed_out, P, R,
-                                      K3_RMS_EPSILON, st), "routed RMS norm")))
-    return rc;
-  if ((rc = from_spine(spine_gemv(kind, sp.routed_up, sp.routed_up_scales, b.routed_out, out, H,
-                                  R, P, false, st), "routed_up")))
-    return rc;
+  }
   return from_spine(spine_gemv(kind, sp.shared_down, sp.shared_down_scales, b.gate, out, H, S, P,
                                true, st), "shared_down");
 }

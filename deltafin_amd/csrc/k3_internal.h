@@ -203,6 +203,24 @@ int spine_fail(int status, const char* fmt, ...);
 // accumulate: y += W x instead of y = W x (one fp32 add per output).
 int spine_gemv(int kind, const void* weights, const float* row_scales, const float* x,
                float* y, int rows, int cols, int positions, bool accumulate, hipStream_t stream);
+// One spine projection with the fused forms: w2 (GLU): y = act(W x, W2 x) per
+// row (no accumulate); norm_w: x is first RMS-normed per position,
+// norm_w * (x * rsqrt(mean(x^2) + eps)).  A fused form the shape cannot take
+// returns K3_SPINE_E_UNSUPPORTED before enqueuing anything.
+struct SpineOp {
+  const void* w;
+  const float* scales;
+  const void* w2;
+  const float* scales2;
+  int act;
+  const float* x;
+  float* y;
+  int rows, cols, positions;
+  bool accumulate;
+  const float* norm_w;
+  float eps;
+};
+int spine_gemv_op(int kind, const SpineOp& op, hipStream_t stream);
 int spine_decode_bits(const uint16_t* in, uint32_t* out, int count, hipStream_t stream);
 int spine_rms_norm(const float* in, const float* weight, float* out, int rows, int cols,
                    float eps, hipStream_t stream);

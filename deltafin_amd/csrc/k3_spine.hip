@@ -82,27 +82,81 @@ __device__ __forceinline__ int lds_slot(int c) {
   return ((j * kQ + q) * 64 + l) * 4 + (c & 3);
 }
 
-template <int kKind, int NJ, int R, int PG>
-__global__ __launch_bounds__(kSpineThreads, 4) void k_spine_gemv(
+// Stages positions [p0, p0 + pg) of x into LDS (zero-padded to kPad columns)
+// and ends with a barrier; every thread of the workgroup calls it.  With
+// norm_w, each staged row is the routed RMS norm of x (rms_norm,
+// provider_moe.cpp:535-542): norm_w[c] * (x[c] * r), r = 1 / sqrt(mean(x^2) +
+// eps), the sum of squares taken in a fixed order (thread-strided partials,
+// wave sums, the waves in order).  x rows and norm_w are 16-byte aligned.
+template <int kKind, int kPad>
+__device__ __forceinline__ void stage_x(float* xs, const float* x, int cols, int p0, int pg,
+                                        const float* norm_w, float eps, float* red) {
+  for (int p = 0; p < pg; ++p) {
+    const float* xp = x + (uint64_t)(p0 + p) * cols;
+    float r = 1.f;
+    if (norm_w) {
+      float ss = 0.f;
+      for (int c = 4 * threadIdx.x; c < cols; c += 4 * kSpineThreads) {
+        const float4 v = *reinterpret_cast<const float4*>(xp + c);
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+      }
+      ss = wave_sum(ss);
+      if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+      __syncthreads();
+      float tot = red[0];
+#pragma unroll
+      for (int v = 1; v < kSpineWaves; ++v) tot += red[v];
+      r = 1.0f / sqrtf(tot / (float)cols + eps);
+      __syncthreads();  // red is reused by the next position
+    }
+    for (int c = 4 * threadIdx.x; c < kPad; c += 4 * kSpineThreads) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (c < cols) {
+        v = *reinterpret_cast<const float4*>(xp + c);
+        if (norm_w) {
+          const float4 nw = *reinterpret_cast<const float4*>(norm_w + c);
+          v.x = nw.x * (v.x * r);
+          v.y = nw.y * (v.y * r);
+          v.z = nw.z * (v.z * r);
+          v.w = nw.w * (v.w * r);
+        }
+      }
+      *reinterpret_cast<float4*>(xs + p * kPad + lds_slot<kKind>(c)) = v;
+    }
+  }
+  __syncthreads();
+}
+
+// kGlu: R = 2 and the wave's two rows are row i of w (gate) and row i of w2
+// (up); the output is act(gate . x, up . x) (the shared expert's SiTU, or
+// SiLU-GLU), one row per wave.
+template <int kKind, int NJ, int R, int PG, bool kGlu = false>
+__global__ __launch_bounds__(kSpineThreads, kGlu ? 2 : 4) void k_spine_gemv(
     const uint8_t* __restrict__ w, const float* __restrict__ row_scale,
     const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions,
-    int tail_lanes, int accumulate) {
+    int tail_lanes, int accumulate, const uint8_t* __restrict__ w2,
+    const float* __restrict__ row_scale2, int act, const float* __restrict__ norm_w, float eps) {
   using E = SpineElem<kKind>;
+  static_assert(!kGlu || R == 2, "a GLU wave holds one gate row and one up row");
   constexpr int kQ = E::kPerChunk / 4;
   constexpr int kPad = NJ * 64 * E::kPerChunk;  // columns per staged position
   extern __shared__ float4 xs4[];               // [PG][kPad / 4]
+  __shared__ float red[kSpineWaves];
   float* xs = reinterpret_cast<float*>(xs4);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const uint64_t row_bytes = (uint64_t)cols * E::kBytes;
-  const int row0 = (blockIdx.x * kSpineWaves + wave) * R;
+  const int row0 = (blockIdx.x * kSpineWaves + wave) * (kGlu ? 1 : R);
   const bool tail_ok = lane < tail_lanes;
 
   u32x4 wv[R][NJ];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, rows - 1);
-    const uint8_t* base = w + (uint64_t)row * row_bytes;
+    const int row = min(kGlu ? row0 : row0 + r, rows - 1);
+    const uint8_t* base = (kGlu && r == 1 ? w2 : w) + (uint64_t)row * row_bytes;
     const uint8_t* rp = base + 16 * lane;
 #pragma unroll
     for (int j = 0; j < NJ - 1; ++j) wv[r][j] = load_chunk(rp + 1024 * j);
@@ -112,15 +166,7 @@ __global__ __launch_bounds__(kSpineThreads, 4) void k_spine_gemv(
   for (int p0 = 0; p0 < positions; p0 += PG) {
     const int pg = min(PG, positions - p0);
     if (p0) __syncthreads();
-    for (int p = 0; p < pg; ++p) {
-      const float* xp = x + (uint64_t)(p0 + p) * cols;
-      for (int c = 4 * threadIdx.x; c < kPad; c += 4 * kSpineThreads) {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (c < cols) v = *reinterpret_cast<const float4*>(xp + c);
-        *reinterpret_cast<float4*>(xs + p * kPad + lds_slot<kKind>(c)) = v;
-      }
-    }
-    __syncthreads();
+    stage_x<kKind, kPad>(xs, x, cols, p0, pg, norm_w, eps, red);
 
     float acc[R][PG];
 #pragma unroll
@@ -164,18 +210,36 @@ __global__ __launch_bounds__(kSpineThreads, 4) void k_spine_gemv(
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = row0 + r;
-      const float scale = kKind == K3_SPINE_KIND_INT8 ? row_scale[min(row, rows - 1)] : 1.f;
+    if constexpr (kGlu) {
+      const int rr = min(row0, rows - 1);
+      const float sg = kKind == K3_SPINE_KIND_INT8 ? row_scale[rr] : 1.f;
+      const float su = kKind == K3_SPINE_KIND_INT8 ? row_scale2[rr] : 1.f;
 #pragma unroll
       for (int p = 0; p < PG; ++p) {
         if (p < pg) {
-          float s = wave_sum(acc[r][p]);
-          if (kKind == K3_SPINE_KIND_INT8) s *= scale;
-          if (lane == 0 && row < rows) {
-            float* yp = y + (uint64_t)(p0 + p) * rows + row;
-            *yp = accumulate ? *yp + s : s;
+          float gs = wave_sum(acc[0][p]);
+          float us = wave_sum(acc[1][p]);
+          if (kKind == K3_SPINE_KIND_INT8) {
+            gs *= sg;
+            us *= su;
+          }
+          if (lane == 0 && row0 < rows) y[(uint64_t)(p0 + p) * rows + row0] = activate(act, gs, us);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = row0 + r;
+        const float scale = kKind == K3_SPINE_KIND_INT8 ? row_scale[min(row, rows - 1)] : 1.f;
+#pragma unroll
+        for (int p = 0; p < PG; ++p) {
+          if (p < pg) {
+            float s = wave_sum(acc[r][p]);
+            if (kKind == K3_SPINE_KIND_INT8) s *= scale;
+            if (lane == 0 && row < rows) {
+              float* yp = y + (uint64_t)(p0 + p) * rows + row;
+              *yp = accumulate ? *yp + s : s;
+            }
           }
         }
       }
@@ -193,11 +257,12 @@ template <int kKind, int NJ, int PG>
 __global__ __launch_bounds__(kSpineThreads, 2) void k_spine_stream(
     const uint8_t* __restrict__ w, const float* __restrict__ row_scale,
     const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions,
-    int tail_lanes, int accumulate) {
+    int tail_lanes, int accumulate, const float* __restrict__ norm_w, float eps) {
   using E = SpineElem<kKind>;
   constexpr int kQ = E::kPerChunk / 4;
   constexpr int kPad = NJ * 64 * E::kPerChunk;
   extern __shared__ float4 xs4[];  // [PG][kPad / 4]
+  __shared__ float red[kSpineWaves];
   float* xs = reinterpret_cast<float*>(xs4);
   const int lane = threadIdx.x & (kWave - 1);
   const int stride = gridDim.x * kSpineWaves;
@@ -252,15 +317,7 @@ __global__ __launch_bounds__(kSpineThreads, 2) void k_spine_stream(
   int row = blockIdx.x * kSpineWaves + threadIdx.x / kWave;
   u32x4 a[NJ], b[NJ];
   load_row(a, row);
-  for (int p = 0; p < positions; ++p) {
-    const float* xp = x + (uint64_t)p * cols;
-    for (int c = 4 * threadIdx.x; c < kPad; c += 4 * kSpineThreads) {
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (c < cols) v = *reinterpret_cast<const float4*>(xp + c);
-      *reinterpret_cast<float4*>(xs + p * kPad + lds_slot<kKind>(c)) = v;
-    }
-  }
-  __syncthreads();
+  stage_x<kKind, kPad>(xs, x, cols, 0, positions, norm_w, eps, red);
   if (row >= rows) return;  // no barrier follows
   for (;;) {
     const int rb = row + stride;
@@ -337,50 +394,86 @@ __global__ __launch_bounds__(kSpineThreads) void k_rms_norm(const float* __restr
 }
 
 template <int kKind, int NJ>
-int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, float* y, int rows,
-                      int cols, int positions, int tail_lanes, int pg, int stream_waves,
-                      int accumulate, hipStream_t st) {
-  // Two rows per wave for short rows (int8 decodes twice the values per piece).
+int spine_fast_launch(const SpineOp& op, int tail_lanes, int pg, int stream_waves,
+                      hipStream_t st) {
+  // Two rows per wave for short rows (int8 decodes twice the values per
+  // piece); a GLU wave always holds its gate and its up row.
   constexpr int R = NJ <= (kKind == K3_SPINE_KIND_BF16 ? 4 : 2) ? 2 : 1;
   constexpr uint32_t kPadBytes = NJ * 64u * SpineElem<kKind>::kPerChunk * 4u;
+  const auto* w = static_cast<const uint8_t*>(op.w);
+  const auto* w2 = static_cast<const uint8_t*>(op.w2);
+  const int acc = op.accumulate ? 1 : 0;
   TimedLaunch tl(KC_SPINE, st);
-  if (positions <= pg && stream_waves > 0) {
+  bool launched_one = false;
+  if (op.w2) {
+    const dim3 grid((unsigned)((op.rows + kSpineWaves - 1) / kSpineWaves));
+    if constexpr (2 * kPadBytes <= kSpineLdsBudget) {
+      if (pg == 2) {
+        launch_timed(tl, (k_spine_gemv<kKind, NJ, 2, 2, true>), grid, dim3(kSpineThreads),
+                     2 * kPadBytes, st, w, op.scales, op.x, op.y, op.rows, op.cols, op.positions,
+                     tail_lanes, acc, w2, op.scales2, op.act, op.norm_w, op.eps);
+        launched_one = true;
+      }
+    }
+    if (pg == 1) {
+      launch_timed(tl, (k_spine_gemv<kKind, NJ, 2, 1, true>), grid, dim3(kSpineThreads),
+                   kPadBytes, st, w, op.scales, op.x, op.y, op.rows, op.cols, op.positions,
+                   tail_lanes, acc, w2, op.scales2, op.act, op.norm_w, op.eps);
+      launched_one = true;
+    }
+  } else if (op.positions <= pg && stream_waves > 0) {
     // One position group: persistent waves, each with the same row count.
     const dim3 sgrid((unsigned)(stream_waves / kSpineWaves));
     const uint32_t lds = (uint32_t)pg * kPadBytes;
     if constexpr (4 * kPadBytes <= kSpineLdsBudget) {
-      if (pg == 4)
+      if (pg == 4) {
         launch_timed(tl, (k_spine_stream<kKind, NJ, 4>), sgrid, dim3(kSpineThreads), lds, st, w,
-                     scales, x, y, rows, cols, positions, tail_lanes, accumulate);
+                     op.scales, op.x, op.y, op.rows, op.cols, op.positions, tail_lanes, acc,
+                     op.norm_w, op.eps);
+        launched_one = true;
+      }
     }
     if constexpr (2 * kPadBytes <= kSpineLdsBudget) {
-      if (pg == 2)
+      if (pg == 2) {
         launch_timed(tl, (k_spine_stream<kKind, NJ, 2>), sgrid, dim3(kSpineThreads), lds, st, w,
-                     scales, x, y, rows, cols, positions, tail_lanes, accumulate);
+                     op.scales, op.x, op.y, op.rows, op.cols, op.positions, tail_lanes, acc,
+                     op.norm_w, op.eps);
+        launched_one = true;
+      }
     }
-    if (pg == 1)
+    if (pg == 1) {
       launch_timed(tl, (k_spine_stream<kKind, NJ, 1>), sgrid, dim3(kSpineThreads), lds, st, w,
-                   scales, x, y, rows, cols, positions, tail_lanes, accumulate);
+                   op.scales, op.x, op.y, op.rows, op.cols, op.positions, tail_lanes, acc,
+                   op.norm_w, op.eps);
+      launched_one = true;
+    }
   } else {
     const int rows_per_group = kSpineWaves * R;
-    const dim3 grid((unsigned)((rows + rows_per_group - 1) / rows_per_group));
-  // Only the position groups whose activation fits the LDS budget exist.
-  if constexpr (4 * kPadBytes <= kSpineLdsBudget) {
-    if (pg == 4)
-      launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 4>), grid, dim3(kSpineThreads), 4 * kPadBytes,
-                   st, w, scales, x, y, rows, cols, positions, tail_lanes, accumulate);
+    const dim3 grid((unsigned)((op.rows + rows_per_group - 1) / rows_per_group));
+    // Only the position groups whose activation fits the LDS budget exist.
+    if constexpr (4 * kPadBytes <= kSpineLdsBudget) {
+      if (pg == 4) {
+        launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 4>), grid, dim3(kSpineThreads),
+                     4 * kPadBytes, st, w, op.scales, op.x, op.y, op.rows, op.cols, op.positions,
+                     tail_lanes, acc, w2, op.scales2, op.act, op.norm_w, op.eps);
+        launched_one = true;
+      }
+    }
+    if constexpr (2 * kPadBytes <= kSpineLdsBudget) {
+      if (pg == 2) {
+        launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 2>), grid, dim3(kSpineThreads),
+                     2 * kPadBytes, st, w, op.scales, op.x, op.y, op.rows, op.cols, op.positions,
+                     tail_lanes, acc, w2, op.scales2, op.act, op.norm_w, op.eps);
+        launched_one = true;
+      }
+    }
+    if (pg == 1) {
+      launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 1>), grid, dim3(kSpineThreads), kPadBytes, st,
+                   w, op.scales, op.x, op.y, op.rows, op.cols, op.positions, tail_lanes, acc,
+                   w2, op.scales2, op.act, op.norm_w, op.eps);
+      launched_one = true;
+    }
   }
-  if constexpr (2 * kPadBytes <= kSpineLdsBudget) {
-    if (pg == 2)
-      launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 2>), grid, dim3(kSpineThreads), 2 * kPadBytes,
-                   st, w, scales, x, y, rows, cols, positions, tail_lanes, accumulate);
-  }
-  if (pg == 1)
-    launch_timed(tl, (k_spine_gemv<kKind, NJ, R, 1>), grid, dim3(kSpineThreads), kPadBytes, st,
-                 w, scales, x, y, rows, cols, positions, tail_lanes, accumulate);
-  }
-  const bool launched_one = pg == 1 || (pg == 2 && 2 * kPadBytes <= kSpineLdsBudget) ||
-                            (pg == 4 && 4 * kPadBytes <= kSpineLdsBudget);
   if (!launched_one) {
     tl.failed();
     return spine_fail(K3_SPINE_E_INVALID, "spine GEMV: no kernel for %d positions per group", pg);
@@ -391,8 +484,7 @@ int spine_fast_launch(const uint8_t* w, const float* scales, const float* x, flo
   return spine_fail(K3_SPINE_E_RUNTIME, "spine GEMV launch: %s", hipGetErrorString(e));
 }
 
-typedef int (*SpineFastFn)(const uint8_t*, const float*, const float*, float*, int, int, int,
-                           int, int, int, int, hipStream_t);
+typedef int (*SpineFastFn)(const SpineOp&, int, int, int, hipStream_t);
 
 template <int kKind, int... NJ>
 constexpr SpineFastFn spine_fast_table(int nj, std::integer_sequence<int, NJ...>) {
@@ -408,62 +500,85 @@ int preflight(const char* what) {
 
 }  // namespace
 
-int spine_gemv(int kind, const void* weights, const float* row_scales, const float* x,
-               float* y, int rows, int cols, int positions, bool accumulate, hipStream_t st) {
+int spine_gemv_op(int kind, const SpineOp& op, hipStream_t st) {
   const char* what = kind == K3_SPINE_KIND_BF16 ? "RAW_BF16 GEMV" : "row-int8 GEMV";
-  if (!weights || !x || !y || (kind == K3_SPINE_KIND_INT8 && !row_scales))
+  if (!op.w || !op.x || !op.y || (kind == K3_SPINE_KIND_INT8 && !op.scales) ||
+      (op.w2 && kind == K3_SPINE_KIND_INT8 && !op.scales2))
     return spine_fail(K3_SPINE_E_INVALID, "%s: null input or output pointer", what);
-  if (rows <= 0 || cols <= 0 || positions <= 0 || positions > K3_SPINE_MAX_POSITIONS)
+  if (op.rows <= 0 || op.cols <= 0 || op.positions <= 0 ||
+      op.positions > K3_SPINE_MAX_POSITIONS)
     return spine_fail(K3_SPINE_E_INVALID,
                       "%s: rows/columns must be positive and positions must be 1..%d", what,
                       K3_SPINE_MAX_POSITIONS);
-  if ((uint64_t)rows > (uint64_t)INT32_MAX / 2)
+  if ((uint64_t)op.rows > (uint64_t)INT32_MAX / 2)
     return spine_fail(K3_SPINE_E_INVALID, "%s: too many rows", what);
+  if (op.w2 && op.accumulate)
+    return spine_fail(K3_SPINE_E_INVALID, "%s: a GLU projection does not accumulate", what);
   int rc = preflight(what);
   if (rc != K3_SPINE_OK) return rc;
-  const auto* w = static_cast<const uint8_t*>(weights);
+  const auto* w = static_cast<const uint8_t*>(op.w);
   const int esize = kind == K3_SPINE_KIND_BF16 ? 2 : 1;
-  const uint64_t row_bytes = (uint64_t)cols * esize;
+  const uint64_t row_bytes = (uint64_t)op.cols * esize;
   const int nj = (int)((row_bytes + 1023) / 1024);
   const int per_position = nj * 64 * (16 / esize) * 4;  // staged activation bytes
-  const bool aligned = (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
-                       (reinterpret_cast<uintptr_t>(x) & 15) == 0 && row_bytes % 16 == 0;
+  const bool aligned =
+      (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(op.x) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(op.w2) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(op.norm_w) & 15) == 0 && row_bytes % 16 == 0;
   if (aligned && nj <= kSpineMaxNj && (uint32_t)per_position <= kSpineLdsBudget) {
     // Positions per LDS group: 1, 2 or 4 (the instantiated kernels), at most
-    // what the budget holds; 3 positions take one group of 4.
+    // what the budget holds; 3 positions take one group of 4 (GLU: 1 or 2).
     const int fit = (int)(kSpineLdsBudget / (uint32_t)per_position);
-    const int want = positions >= 3 ? 4 : positions;
-    const int pg = std::min(want, fit >= 4 ? 4 : fit >= 2 ? 2 : 1);
+    const int want = op.positions >= 3 ? 4 : op.positions;
+    int pg = std::min(want, fit >= 4 ? 4 : fit >= 2 ? 2 : 1);
+    if (op.w2 && pg == 4) pg = 2;
     const uint64_t tail_bytes = row_bytes - 1024ull * (nj - 1);
     const int tail_lanes = (int)(tail_bytes / 16);
+    // Persistent waves for one position group: about kStreamWavesPerCu per
+    // CU, rounded so every wave gets ceil(rows / target) rows, in whole
+    // workgroups.
+    int stream_waves = 0;
+    if (op.positions <= pg && !op.w2) {
+      const int target = std::max(kSpineWaves, std::max(1, device_cu_count()) * kStreamWavesPerCu);
+      const int per_wave = (op.rows + target - 1) / target;
+      stream_waves = (op.rows + per_wave - 1) / per_wave;
+      stream_waves = (stream_waves + kSpineWaves - 1) / kSpineWaves * kSpineWaves;
+    }
     const auto seq = std::make_integer_sequence<int, kSpineMaxNj>{};
     const SpineFastFn fn = kind == K3_SPINE_KIND_BF16
                                ? spine_fast_table<K3_SPINE_KIND_BF16>(nj, seq)
                                : spine_fast_table<K3_SPINE_KIND_INT8>(nj, seq);
-    // Persistent waves for one position group: about kStreamWavesPerCu per CU,
-    // rounded so every wave gets ceil(rows / target) rows, in whole workgroups.
-    int stream_waves = 0;
-    if (positions <= pg) {
-      const int target = std::max(kSpineWaves, std::max(1, device_cu_count()) * kStreamWavesPerCu);
-      const int per_wave = (rows + target - 1) / target;
-      stream_waves = (rows + per_wave - 1) / per_wave;
-      stream_waves = (stream_waves + kSpineWaves - 1) / kSpineWaves * kSpineWaves;
-    }
-    return fn(w, row_scales, x, y, rows, cols, positions, tail_lanes, pg, stream_waves,
-              accumulate ? 1 : 0, st);
+    return fn(op, tail_lanes, pg, stream_waves, st);
   }
-  const dim3 grid((unsigned)((rows + kSpineWaves - 1) / kSpineWaves));
+  if (op.w2 || op.norm_w)
+    return spine_fail(K3_SPINE_E_UNSUPPORTED,
+                      "%s: fused GLU / RMS norm needs 16-byte aligned rows of at most 16 KB", what);
+  const dim3 grid((unsigned)((op.rows + kSpineWaves - 1) / kSpineWaves));
   TimedLaunch tl(KC_SPINE, st);
   if (kind == K3_SPINE_KIND_BF16)
     launch_timed(tl, k_spine_gemv_generic<K3_SPINE_KIND_BF16>, grid, dim3(kSpineThreads), 0, st,
-                 w, row_scales, x, y, rows, cols, positions, accumulate);
+                 w, op.scales, op.x, op.y, op.rows, op.cols, op.positions, op.accumulate ? 1 : 0);
   else
     launch_timed(tl, k_spine_gemv_generic<K3_SPINE_KIND_INT8>, grid, dim3(kSpineThreads), 0, st,
-                 w, row_scales, x, y, rows, cols, positions, accumulate);
+                 w, op.scales, op.x, op.y, op.rows, op.cols, op.positions, op.accumulate ? 1 : 0);
   const hipError_t e = hipGetLastError();
   if (e == hipSuccess) return K3_SPINE_OK;
   tl.failed();
   return spine_fail(K3_SPINE_E_RUNTIME, "%s launch: %s", what, hipGetErrorString(e));
+}
+
+int spine_gemv(int kind, const void* weights, const float* row_scales, const float* x,
+               float* y, int rows, int cols, int positions, bool accumulate, hipStream_t st) {
+  SpineOp op{};
+  op.w = weights;
+  op.scales = row_scales;
+  op.x = x;
+  op.y = y;
+  op.rows = rows;
+  op.cols = cols;
+  op.positions = positions;
+  op.accumulate = accumulate;
+  return spine_gemv_op(kind, op, st);
 }
 
 int spine_decode_bits(const uint16_t* in, uint32_t* out, int count, hipStream_t st) {
