@@ -805,9 +805,15 @@ constexpr int kDownMaxRows = 64;
 #ifndef K3_DOWN_THREADS
 #define K3_DOWN_THREADS 1024
 #endif
+#ifndef K3_DOWN_THREADS_WIDE
+#define K3_DOWN_THREADS_WIDE 512
+#endif
+#ifndef K3_DOWN_BATCH_CPL2
+#define K3_DOWN_BATCH_CPL2 2
+#endif
 template <int CPLB>
 constexpr int down_max_threads() {
-  return CPLB <= 1 ? K3_DOWN_THREADS : 512;
+  return CPLB <= 1 ? K3_DOWN_THREADS : K3_DOWN_THREADS_WIDE;
 }
 
 template <typename OT, int CPLB, int kB, bool kS4 = false>
@@ -1883,7 +1889,7 @@ int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace&
   if (GB == 64 && route.n <= 16) return down_g64_dispatch<OT>(g, route, ws.h, out, st);
   switch ((GB + 63) / 64) {
     case 1: return down_blocks_launch<OT, 1, kDownBlocksBatch>(g, route, ws.h, out, st);
-    case 2: return down_blocks_launch<OT, 2, 2>(g, route, ws.h, out, st);
+    case 2: return down_blocks_launch<OT, 2, K3_DOWN_BATCH_CPL2>(g, route, ws.h, out, st);
     case 3: return down_blocks_launch<OT, 3, 2>(g, route, ws.h, out, st);
     case 4: return down_blocks_launch<OT, 4, 1>(g, route, ws.h, out, st);
     default: return fail(K3_HIP_E_INVALID, "decode layer: intermediate %d exceeds 8192", g.inter);
