@@ -31,7 +31,10 @@ namespace {
 constexpr int kSpineThreads = 256;
 constexpr int kSpineWaves = kSpineThreads / kWave;
 constexpr int kSpineMaxNj = 16;                // pieces per row on the fast path
-constexpr uint32_t kSpineLdsBudget = 65536;    // activation bytes per workgroup
+#ifndef K3_SPINE_LDS_BUDGET
+#define K3_SPINE_LDS_BUDGET 65536
+#endif
+constexpr uint32_t kSpineLdsBudget = K3_SPINE_LDS_BUDGET;  // activation bytes per workgroup
 #ifndef K3_SPINE_STREAM_WAVES_PER_CU
 #define K3_SPINE_STREAM_WAVES_PER_CU 8
 #endif
