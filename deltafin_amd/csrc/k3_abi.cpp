@@ -804,15 +804,33 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   const int P = n_positions, H = (int)sp.hidden, R = (int)sp.routed_hidden;
   const int S = (int)sp.shared_intermediate, E = (int)sp.experts;
   int rc;
-  // prepare: router logits, the route, routed_down
-  if ((rc = from_spine(spine_gemv(kind, sp.router, sp.router_scales, hidden, b.logits, E, H, P,
-                                  false, st), "router")))
+  // prepare: router logits and routed_down (one launch over both matrices,
+  // which read the same hidden rows, where the shape allows), then the route
+  SpineOp pre{};
+  pre.w = sp.router;
+  pre.scales = sp.router_scales;
+  pre.x = hidden;
+  pre.y = b.logits;
+  pre.rows = E;
+  pre.cols = H;
+  pre.positions = P;
+  pre.wb = sp.routed_down;
+  pre.scales_b = sp.routed_down_scales;
+  pre.yb = b.routed_in;
+  pre.rows_b = R;
+  rc = spine_gemv_op(kind, pre, st);
+  if (rc == K3_SPINE_E_UNSUPPORTED) {
+    if ((rc = from_spine(spine_gemv(kind, sp.router, sp.router_scales, hidden, b.logits, E, H, P,
+                                    false, st), "router")))
+      return rc;
+    if ((rc = from_spine(spine_gemv(kind, sp.routed_down, sp.routed_down_scales, hidden,
+                                    b.routed_in, R, H, P, false, st), "routed_down")))
+      return rc;
+  } else if ((rc = from_spine(rc, "router + routed_down"))) {
     return rc;
+  }
   if ((rc = launch_route_sigmoid_bias(b.logits, sp.router_bias, E, top_k, P, ws.ids, ws.w,
                                       route_ids, route_weights, st)))
-    return rc;
-  if ((rc = from_spine(spine_gemv(kind, sp.routed_down, sp.routed_down_scales, hidden,
-                                  b.routed_in, R, H, P, false, st), "routed_down")))
     return rc;
   // the routed experts
   if ((rc = experts_on_device_routes(g, bank, expert_stride, E, P, top_k, b.routed_in,

@@ -204,7 +204,8 @@ int spine_fail(int status, const char* fmt, ...);
 int spine_gemv(int kind, const void* weights, const float* row_scales, const float* x,
                float* y, int rows, int cols, int positions, bool accumulate, hipStream_t stream);
 // One spine projection with the fused forms: w2 (GLU): y = act(W x, W2 x) per
-// row (no accumulate); norm_w: x is first RMS-normed per position,
+// row (no accumulate); wb: a second matrix's rows after W's (see below);
+// norm_w: x is first RMS-normed per position,
 // norm_w * (x * rsqrt(mean(x^2) + eps)).  A fused form the shape cannot take
 // returns K3_SPINE_E_UNSUPPORTED before enqueuing anything.
 struct SpineOp {
@@ -219,6 +220,12 @@ struct SpineOp {
   bool accumulate;
   const float* norm_w;
   float eps;
+  // A second matrix of the same width over the same x (wb, scales_b: rows_b
+  // rows into yb [P][rows_b]), in the same launch; single position group only.
+  const void* wb;
+  const float* scales_b;
+  float* yb;
+  int rows_b;
 };
 int spine_gemv_op(int kind, const SpineOp& op, hipStream_t stream);
 int spine_decode_bits(const uint16_t* in, uint32_t* out, int count, hipStream_t stream);

@@ -260,12 +260,18 @@ template <int kKind, int NJ, int PG>
 __global__ __launch_bounds__(kSpineThreads, 2) void k_spine_stream(
     const uint8_t* __restrict__ w, const float* __restrict__ row_scale,
     const float* __restrict__ x, float* __restrict__ y, int rows, int cols, int positions,
-    int tail_lanes, int accumulate, const float* __restrict__ norm_w, float eps) {
+    int tail_lanes, int accumulate, const float* __restrict__ norm_w, float eps,
+    const uint8_t* __restrict__ wb, const float* __restrict__ row_scale_b, float* __restrict__ yb,
+    int rows_a) {
+  // Rows [0, rows_a) are w's (output y [P][rows_a]); with wb, rows [rows_a,
+  // rows) are wb's (output yb [P][rows - rows_a]): two matrices of the same
+  // width over the same activation in one launch.  Without wb, rows_a = rows.
   using E = SpineElem<kKind>;
   constexpr int kQ = E::kPerChunk / 4;
   constexpr int kPad = NJ * 64 * E::kPerChunk;
   extern __shared__ float4 xs4[];  // [PG][kPad / 4]
   __shared__ float red[kSpineWaves];
+  const int rows_b = rows - rows_a;
   float* xs = reinterpret_cast<float*>(xs4);
   const int lane = threadIdx.x & (kWave - 1);
   const int stride = gridDim.x * kSpineWaves;
@@ -273,7 +279,9 @@ __global__ __launch_bounds__(kSpineThreads, 2) void k_spine_stream(
   const bool tail_ok = lane < tail_lanes;
 
   auto load_row = [&](u32x4* buf, int row) {
-    const uint8_t* base = w + (uint64_t)min(row, rows - 1) * row_bytes;
+    const int r = min(row, rows - 1);
+    const uint8_t* base =
+        r < rows_a ? w + (uint64_t)r * row_bytes : wb + (uint64_t)(r - rows_a) * row_bytes;
     const uint8_t* rp = base + 16 * lane;
 #pragma unroll
     for (int j = 0; j < NJ - 1; ++j) buf[j] = load_chunk(rp + 1024 * j);
@@ -303,14 +311,18 @@ __global__ __launch_bounds__(kSpineThreads, 2) void k_spine_stream(
         }
       }
     }
-    const float scale = kKind == K3_SPINE_KIND_INT8 ? row_scale[row] : 1.f;
+    const bool in_a = row < rows_a;
+    const float scale = kKind == K3_SPINE_KIND_INT8
+                            ? (in_a ? row_scale[row] : row_scale_b[row - rows_a])
+                            : 1.f;
 #pragma unroll
     for (int p = 0; p < PG; ++p) {
       if (p < positions) {
         float s = wave_sum(acc[p]);
         if (kKind == K3_SPINE_KIND_INT8) s *= scale;
         if (lane == 0) {
-          float* yp = y + (uint64_t)p * rows + row;
+          float* yp = in_a ? y + (uint64_t)p * rows_a + row
+                           : yb + (uint64_t)p * rows_b + (row - rows_a);
           *yp = accumulate ? *yp + s : s;
         }
       }
@@ -405,6 +417,8 @@ int spine_fast_launch(const SpineOp& op, int tail_lanes, int pg, int stream_wave
   constexpr uint32_t kPadBytes = NJ * 64u * SpineElem<kKind>::kPerChunk * 4u;
   const auto* w = static_cast<const uint8_t*>(op.w);
   const auto* w2 = static_cast<const uint8_t*>(op.w2);
+  const auto* wb = static_cast<const uint8_t*>(op.wb);
+  const int total_rows = op.rows + (op.wb ? op.rows_b : 0);
   const int acc = op.accumulate ? 1 : 0;
   TimedLaunch tl(KC_SPINE, st);
   bool launched_one = false;
@@ -431,23 +445,23 @@ int spine_fast_launch(const SpineOp& op, int tail_lanes, int pg, int stream_wave
     if constexpr (4 * kPadBytes <= kSpineLdsBudget) {
       if (pg == 4) {
         launch_timed(tl, (k_spine_stream<kKind, NJ, 4>), sgrid, dim3(kSpineThreads), lds, st, w,
-                     op.scales, op.x, op.y, op.rows, op.cols, op.positions, tail_lanes, acc,
-                     op.norm_w, op.eps);
+                     op.scales, op.x, op.y, total_rows, op.cols, op.positions, tail_lanes, acc,
+                     op.norm_w, op.eps, wb, op.scales_b, op.yb, op.rows);
         launched_one = true;
       }
     }
     if constexpr (2 * kPadBytes <= kSpineLdsBudget) {
       if (pg == 2) {
         launch_timed(tl, (k_spine_stream<kKind, NJ, 2>), sgrid, dim3(kSpineThreads), lds, st, w,
-                     op.scales, op.x, op.y, op.rows, op.cols, op.positions, tail_lanes, acc,
-                     op.norm_w, op.eps);
+                     op.scales, op.x, op.y, total_rows, op.cols, op.positions, tail_lanes, acc,
+                     op.norm_w, op.eps, wb, op.scales_b, op.yb, op.rows);
         launched_one = true;
       }
     }
     if (pg == 1) {
       launch_timed(tl, (k_spine_stream<kKind, NJ, 1>), sgrid, dim3(kSpineThreads), lds, st, w,
-                   op.scales, op.x, op.y, op.rows, op.cols, op.positions, tail_lanes, acc,
-                   op.norm_w, op.eps);
+                   op.scales, op.x, op.y, total_rows, op.cols, op.positions, tail_lanes, acc,
+                   op.norm_w, op.eps, wb, op.scales_b, op.yb, op.rows);
       launched_one = true;
     }
   } else {
@@ -517,6 +531,9 @@ int spine_gemv_op(int kind, const SpineOp& op, hipStream_t st) {
     return spine_fail(K3_SPINE_E_INVALID, "%s: too many rows", what);
   if (op.w2 && op.accumulate)
     return spine_fail(K3_SPINE_E_INVALID, "%s: a GLU projection does not accumulate", what);
+  if (op.wb && (op.w2 || !op.yb || op.rows_b <= 0 || (kind == K3_SPINE_KIND_INT8 && !op.scales_b) ||
+                (uint64_t)op.rows + op.rows_b > (uint64_t)INT32_MAX / 2))
+    return spine_fail(K3_SPINE_E_INVALID, "%s: invalid second matrix", what);
   int rc = preflight(what);
   if (rc != K3_SPINE_OK) return rc;
   const auto* w = static_cast<const uint8_t*>(op.w);
@@ -527,7 +544,8 @@ int spine_gemv_op(int kind, const SpineOp& op, hipStream_t st) {
   const bool aligned =
       (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(op.x) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(op.w2) & 15) == 0 &&
-      (reinterpret_cast<uintptr_t>(op.norm_w) & 15) == 0 && row_bytes % 16 == 0;
+      (reinterpret_cast<uintptr_t>(op.norm_w) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(op.wb) & 15) == 0 && row_bytes % 16 == 0;
   if (aligned && nj <= kSpineMaxNj && (uint32_t)per_position <= kSpineLdsBudget) {
     // Positions per LDS group: 1, 2 or 4 (the instantiated kernels), at most
     // what the budget holds; 3 positions take one group of 4 (GLU: 1 or 2).
@@ -541,11 +559,15 @@ int spine_gemv_op(int kind, const SpineOp& op, hipStream_t st) {
     // CU, rounded so every wave gets ceil(rows / target) rows, in whole
     // workgroups.
     int stream_waves = 0;
+    const int total = op.rows + (op.wb ? op.rows_b : 0);
     if (op.positions <= pg && !op.w2) {
       const int target = std::max(kSpineWaves, std::max(1, device_cu_count()) * kStreamWavesPerCu);
-      const int per_wave = (op.rows + target - 1) / target;
-      stream_waves = (op.rows + per_wave - 1) / per_wave;
+      const int per_wave = (total + target - 1) / target;
+      stream_waves = (total + per_wave - 1) / per_wave;
       stream_waves = (stream_waves + kSpineWaves - 1) / kSpineWaves * kSpineWaves;
+    } else if (op.wb) {
+      return spine_fail(K3_SPINE_E_UNSUPPORTED,
+                        "%s: two matrices in one launch need a single position group", what);
     }
     const auto seq = std::make_integer_sequence<int, kSpineMaxNj>{};
     const SpineFastFn fn = kind == K3_SPINE_KIND_BF16
@@ -553,7 +575,7 @@ int spine_gemv_op(int kind, const SpineOp& op, hipStream_t st) {
                                : spine_fast_table<K3_SPINE_KIND_INT8>(nj, seq);
     return fn(op, tail_lanes, pg, stream_waves, st);
   }
-  if (op.w2 || op.norm_w)
+  if (op.w2 || op.norm_w || op.wb)
     return spine_fail(K3_SPINE_E_UNSUPPORTED,
                       "%s: fused GLU / RMS norm needs 16-byte aligned rows of at most 16 KB", what);
   const dim3 grid((unsigned)((op.rows + kSpineWaves - 1) / kSpineWaves));
