@@ -837,7 +837,7 @@ def _spine_bench(launches: int = 24) -> dict:
 
 
 K3_BLOCK_EXPERTS = 896
-K3_BLOCK_POSITIONS = (1, 4)
+K3_BLOCK_POSITIONS = (1, 4, 8, 16)
 
 
 def _k3_block_bench(calls: int = 20) -> dict:

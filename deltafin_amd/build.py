@@ -49,7 +49,7 @@ CXX_FLAGS = [
     "-Wextra",
     "-Wno-unused-parameter",
 ]
-KERNEL_SOURCES = ["k3_kernels.hip", "k3_verify_mfma.hip", "k3_spine.hip"]
+KERNEL_SOURCES = ["k3_kernels.hip", "k3_verify_mfma.hip", "k3_spine.hip", "k3_spine_mfma.hip"]
 HOST_SOURCES = ["k3_abi.cpp", "k3_cache.cpp", "k3_timing.cpp", "k3_spine_abi.cpp"]
 
 
@@ -66,8 +66,9 @@ def _run(cmd: list[str]) -> None:
 
 
 def build(verbose: bool = True, defines: list[str] | None = None, out: Path | None = None) -> Path:
-    """Compile the library; `defines` (NAME=VALUE) override kernel tuning
-    constants and `out` redirects the library (both for tuning sweeps)."""
+    """Compile the library; `defines` (NAME=VALUE) override tuning constants in
+    every translation unit and `out` redirects the library (both for tuning
+    sweeps)."""
     hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
     target = Path(out) if out is not None else LIB
     target.parent.mkdir(parents=True, exist_ok=True)
@@ -80,7 +81,7 @@ def build(verbose: bool = True, defines: list[str] | None = None, out: Path | No
             objs.append(str(obj))
         for src in HOST_SOURCES:
             obj = Path(tmp) / (src + ".o")
-            _run(["g++", *CXX_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+            _run(["g++", *CXX_FLAGS, *dflags, "-c", str(CSRC / src), "-o", str(obj)])
             objs.append(str(obj))
         tmp_lib = Path(tmp) / LIB.name
         _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp_lib), *objs,

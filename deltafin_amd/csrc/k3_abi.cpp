@@ -650,6 +650,10 @@ double expected_union(int n_bank, int top_k, int n_positions) {
 }
 
 // ---------------------------------------------------------------- MoE block
+// Positions from which the block's BF16 spine runs on the matrix cores.
+#ifndef K3_SPINE_MFMA_MIN_POSITIONS
+#define K3_SPINE_MFMA_MIN_POSITIONS 3
+#endif
 static_assert(sizeof(K3HipMoeSpineV1) == 144, "K3HipMoeSpineV1 layout changed");
 
 // Block workspace: the expert workspace, then logits [P, E], routed_in and
@@ -663,6 +667,7 @@ struct BlockBufs {
   float* routed_out;
   float* gate;
   float* up;
+  uint8_t* terms;  // BF16 activation terms of the matrix-core spine (P >= 3)
 };
 
 uint64_t block_layout(const K3HipMoeSpineV1& sp, const Geo& g, int max_positions,
@@ -684,6 +689,9 @@ uint64_t block_layout(const K3HipMoeSpineV1& sp, const Geo& g, int max_positions
   take(b ? &b->routed_out : nullptr, P * sp.routed_hidden);
   take(b ? &b->gate : nullptr, P * sp.shared_intermediate);
   take(b ? &b->up : nullptr, P * sp.shared_intermediate);
+  const int wmax = (int)std::max(sp.hidden, std::max(sp.routed_hidden, sp.shared_intermediate));
+  if (b) b->terms = base + off;
+  off += align256(spine_mfma_terms_bytes(max_positions, wmax));
   return off;
 }
 
@@ -804,6 +812,39 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   const int P = n_positions, H = (int)sp.hidden, R = (int)sp.routed_hidden;
   const int S = (int)sp.shared_intermediate, E = (int)sp.experts;
   int rc;
+  // 3..16 positions of a BF16 spine: every projection on the matrix cores
+  // from BF16 activation terms (the fp32 kernels are bound by LDS and FMAs
+  // there); the steps and their order are the same.
+  if (P >= K3_SPINE_MFMA_MIN_POSITIONS && kind == K3_SPINE_KIND_BF16 &&
+      spine_mfma_supported(kind, P, E, H) &&
+      spine_mfma_supported(kind, P, H, R) && spine_mfma_supported(kind, P, H, S)) {
+    auto mm = [&](const void* w, float* y, int rows, int cols, bool acc, const char* step) {
+      return from_spine(spine_mfma_gemv(w, b.terms, y, rows, cols, P, acc, st), step);
+    };
+    auto split = [&](const float* x, int cols) {
+      return from_spine(spine_mfma_split(x, P, cols, b.terms, st), "term split");
+    };
+    if ((rc = split(hidden, H)) || (rc = mm(sp.router, b.logits, E, H, false, "router")) ||
+        (rc = mm(sp.routed_down, b.routed_in, R, H, false, "routed_down")) ||
+        (rc = mm(sp.shared_gate, b.gate, S, H, false, "shared_gate")) ||
+        (rc = mm(sp.shared_up, b.up, S, H, false, "shared_up")))
+      return rc;
+    if ((rc = launch_route_sigmoid_bias(b.logits, sp.router_bias, E, top_k, P, ws.ids, ws.w,
+                                        route_ids, route_weights, st)))
+      return rc;
+    if ((rc = experts_on_device_routes(g, bank, expert_stride, E, P, top_k, b.routed_in,
+                                       b.routed_out, ws, st)))
+      return rc;
+    if ((rc = launch_activation(b.gate, b.up, b.gate, (int64_t)P * S, K3_ACT_SITU, st)))
+      return rc;
+    if ((rc = from_spine(spine_rms_norm(b.routed_out, sp.routed_norm, b.routed_out, P, R,
+                                        K3_RMS_EPSILON, st), "routed RMS norm")))
+      return rc;
+    if ((rc = split(b.routed_out, R)) || (rc = mm(sp.routed_up, out, H, R, false, "routed_up")) ||
+        (rc = split(b.gate, S)) || (rc = mm(sp.shared_down, out, H, S, true, "shared_down")))
+      return rc;
+    return K3_HIP_OK;
+  }
   // prepare: router logits and routed_down (one launch over both matrices,
   // which read the same hidden rows, where the shape allows), then the route
   SpineOp pre{};

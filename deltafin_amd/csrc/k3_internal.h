@@ -176,6 +176,7 @@ enum KernelClass : int {
   KC_DOWN_MFMA,
   KC_SPINE,
   KC_RMS_NORM,
+  KC_SPINE_MFMA,
   KC_COUNT
 };
 
@@ -228,6 +229,14 @@ struct SpineOp {
   int rows_b;
 };
 int spine_gemv_op(int kind, const SpineOp& op, hipStream_t stream);
+// Matrix-core spine (k3_spine_mfma.hip, BF16 matrices, 1..16 positions, cols a
+// multiple of 64): split x [P, cols] into BF16 terms (spine_mfma_terms_bytes of
+// device memory, 16-byte aligned), then y = W x (+ y) from those terms.
+uint64_t spine_mfma_terms_bytes(int positions, int cols);
+bool spine_mfma_supported(int kind, int positions, int rows, int cols);
+int spine_mfma_split(const float* x, int positions, int cols, void* terms, hipStream_t stream);
+int spine_mfma_gemv(const void* w, const void* terms, float* y, int rows, int cols, int positions,
+                    bool accumulate, hipStream_t stream);
 int spine_decode_bits(const uint16_t* in, uint32_t* out, int count, hipStream_t stream);
 int spine_rms_norm(const float* in, const float* weight, float* out, int rows, int cols,
                    float eps, hipStream_t stream);

@@ -8,8 +8,10 @@ moe_block_f64):
   intermediate 32 / shared 64) at one and three positions, under the
   reference's bound max |out - expected| <= 2e-4 (:291);
 * the K3 geometry (hidden 7168, routed 3584, intermediate 3072, shared 6144,
-  896 experts in a device bank) with BF16 and row-int8 spines at 1, 2 and 4
-  positions, normwise error <= 1e-3 and route ids identical;
+  896 experts in a device bank) with BF16 spines at 1, 3, 4 and 8 positions
+  (from 3 positions the spine runs on the BF16 matrix cores from three-term
+  activation splits) and a row-int8 spine at 2, normwise error <= 1e-3 and
+  route ids identical;
 * 16 positions, where AUTO takes the union path: outputs equal the
   one-decode-layer-per-position path's within 1e-4 normwise, same routes.
 """
@@ -110,7 +112,7 @@ def _normwise(got, want):
     return float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
 
 
-@pytest.mark.parametrize("kind,positions", [("bf16", 1), ("bf16", 4), ("int8", 2)])
+@pytest.mark.parametrize("kind,positions", [("bf16", 1), ("bf16", 3), ("bf16", 4), ("bf16", 8), ("int8", 2)])
 def test_block_k3_geometry(gpu, k3_bank, kind, positions):
     import torch
     from deltafin_amd import spine
