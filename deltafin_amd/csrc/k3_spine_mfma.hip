@@ -39,7 +39,10 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kAhead = 8;           // weight steps in flight per wave
+#ifndef K3_SPINE_MFMA_TILES
+#define K3_SPINE_MFMA_TILES 2
+#endif
+constexpr int kAhead = 8;           // weight KB in flight per wave (steps x tiles)
 constexpr int kAheadB = 4;          // activation-term steps in flight per wave
 static_assert(kAhead % kAheadB == 0, "the term ring must index statically");
 
@@ -82,36 +85,50 @@ __global__ __launch_bounds__(256) void k_split_bf16_terms(const float* __restric
   terms[i] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-template <int NB>
+// TL tiles (8 TL rows) per workgroup: every wave applies each step's terms
+// to all TL tiles, so the term loads from L2 are shared by 8 TL weight rows.
+template <int NB, int TL>
 __global__ __launch_bounds__(256) void k_spine_mfma(const uint8_t* __restrict__ wmat,
                                                     const uint4* __restrict__ terms,
                                                     float* __restrict__ y, int rows, int cols,
                                                     int P, int S, int accumulate) {
-  __shared__ f32x4 part[4][NB][2][64];
+  constexpr int kA = kAhead / TL;  // steps of weights in flight (8 / TL KB per tile)
+  constexpr int kB = kA < kAheadB ? kA : kAheadB;
+  static_assert(kA % kB == 0, "the rings must index statically");
+  __shared__ f32x4 part[4][TL][NB][2][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int r0 = blockIdx.x * 8;
+  const int r0 = blockIdx.x * 8 * TL;
   const int steps = cols / 64;                   // 64-element steps of a row
   const int per = (steps + S - 1) / S;           // steps of this wave
   const int k0 = wave * per;
-  const int groups = (per + kAhead - 1) / kAhead;
+  const int groups = (per + kA - 1) / kA;
   const int tsteps = cols / 32 + 2;              // K32 steps of the term buffer
   const int m = lane & 15;
-  const int row = min(r0 + (m >> 1), rows - 1);
-  const uint8_t* arow = wmat + (uint64_t)row * cols * 2 + 64 * (m & 1) + 16 * (lane >> 4);
   const int last = steps - 1;
-
-  f32x4 d0[NB], d1[NB];
+  const uint8_t* arow[TL];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    d0[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    d1[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < TL; ++t) {
+    const int row = min(r0 + 8 * t + (m >> 1), rows - 1);
+    arow[t] = wmat + (uint64_t)row * cols * 2 + 64 * (m & 1) + 16 * (lane >> 4);
   }
-  // A ring: the pieces of steps k0 + g kAhead + j, clamped into the row; B
-  // ring: the terms of steps kAheadB ahead (the zero steps past the range).
-  u32x4 ring[kAhead];
-  u32x4 bring[kAheadB][NB][2];
-  auto a_load = [&](int ks) { return load_chunk(arow + 128 * (uint64_t)min(ks, last)); };
+
+  f32x4 d0[TL][NB], d1[TL][NB];
+#pragma unroll
+  for (int t = 0; t < TL; ++t)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      d0[t][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      d1[t][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  // A ring: the pieces of steps kA ahead, clamped into the row; B ring: the
+  // terms of steps kB ahead (the zero steps past the wave's range).
+  u32x4 ring[kA][TL];
+  u32x4 bring[kB][NB][2];
+  auto a_load = [&](u32x4 (&dst)[TL], int ks) {
+#pragma unroll
+    for (int t = 0; t < TL; ++t) dst[t] = load_chunk(arow[t] + 128 * (uint64_t)min(ks, last));
+  };
   auto b_load = [&](u32x4 (&dst)[NB][2], int idx) {
     const int ks = k0 + idx;
     const int s0 = (idx < per && ks < steps) ? 2 * ks : tsteps - 2;
@@ -124,44 +141,51 @@ __global__ __launch_bounds__(256) void k_spine_mfma(const uint8_t* __restrict__ 
   };
   if (wave < S) {
 #pragma unroll
-    for (int j = 0; j < kAhead; ++j) ring[j] = a_load(k0 + j);
+    for (int j = 0; j < kA; ++j) a_load(ring[j], k0 + j);
 #pragma unroll
-    for (int j = 0; j < kAheadB; ++j) b_load(bring[j], j);
+    for (int j = 0; j < kB; ++j) b_load(bring[j], j);
     for (int gi = 0; gi < groups; ++gi) {
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j) {
-        const int idx = gi * kAhead + j;          // step index within the wave
+      for (int j = 0; j < kA; ++j) {
+        const int idx = gi * kA + j;              // step index within the wave
         const int ks = k0 + idx;
-        const u32x4 a = ring[j];
+        u32x4 a[TL];
+#pragma unroll
+        for (int t = 0; t < TL; ++t) a[t] = ring[j][t];
         u32x4 b[NB][2];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          b[nb][0] = bring[j % kAheadB][nb][0];
-          b[nb][1] = bring[j % kAheadB][nb][1];
+          b[nb][0] = bring[j % kB][nb][0];
+          b[nb][1] = bring[j % kB][nb][1];
         }
-        ring[j] = a_load(ks + kAhead);            // refill kAhead steps ahead
-        b_load(bring[j % kAheadB], idx + kAheadB);
-        const bf16x8 av = __builtin_bit_cast(bf16x8, a);
+        a_load(ring[j], ks + kA);                 // refill kA steps ahead
+        b_load(bring[j % kB], idx + kB);
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          d0[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              av, __builtin_bit_cast(bf16x8, b[nb][0]), d0[nb], 0, 0, 0);
-          d1[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              av, __builtin_bit_cast(bf16x8, b[nb][1]), d1[nb], 0, 0, 0);
+        for (int t = 0; t < TL; ++t) {
+          const bf16x8 av = __builtin_bit_cast(bf16x8, a[t]);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            d0[t][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                av, __builtin_bit_cast(bf16x8, b[nb][0]), d0[t][nb], 0, 0, 0);
+            d1[t][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                av, __builtin_bit_cast(bf16x8, b[nb][1]), d1[t][nb], 0, 0, 0);
+          }
         }
       }
     }
   }
   // valid rows: weight row 2q from d0[0] + d1[1], row 2q + 1 from d0[2] + d1[3]
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    part[wave][nb][0][lane] = d0[nb];
-    part[wave][nb][1][lane] = d1[nb];
-  }
+  for (int t = 0; t < TL; ++t)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      part[wave][t][nb][0][lane] = d0[t][nb];
+      part[wave][t][nb][1][lane] = d1[t][nb];
+    }
   __syncthreads();
-  const int t = threadIdx.x;
-  if (t < 8 * P) {
-    const int r = t / P, p = t % P;               // output row r of the tile, position p
+  for (int o = threadIdx.x; o < 8 * TL * P; o += 256) {
+    const int rt = o / P, p = o % P;              // output row rt of the workgroup, position p
+    const int t = rt >> 3, r = rt & 7;
     const int q = r >> 1, hi = r & 1;
     float acc = 0.f;
     for (int w = 0; w < S; ++w) {
@@ -171,12 +195,12 @@ __global__ __launch_bounds__(256) void k_spine_mfma(const uint8_t* __restrict__ 
         const int nb = n >> 4;
         const int ln = 16 * q + (n & 15);
         if (nb < NB) {
-          const f32x4 e0 = part[w][nb][0][ln], e1 = part[w][nb][1][ln];
+          const f32x4 e0 = part[w][t][nb][0][ln], e1 = part[w][t][nb][1][ln];
           acc += hi ? e0[2] + e1[3] : e0[0] + e1[1];
         }
       }
     }
-    const int orow = r0 + r;
+    const int orow = r0 + rt;
     if (orow < rows) {
       float* yp = y + (int64_t)p * rows + orow;
       *yp = accumulate ? *yp + acc : acc;
@@ -216,16 +240,17 @@ int spine_mfma_gemv(const void* w, const void* terms, float* y, int rows, int co
   const int steps = cols / 64;
   const int S = steps >= 64 ? 4 : steps >= 16 ? 2 : 1;  // waves splitting K
   const int nb = (3 * positions + 15) / 16;
-  const dim3 grid((unsigned)((rows + 7) / 8));
+  constexpr int TL = K3_SPINE_MFMA_TILES;
+  const dim3 grid((unsigned)((rows + 8 * TL - 1) / (8 * TL)));
   const auto* wm = static_cast<const uint8_t*>(w);
   const auto* tb = static_cast<const uint4*>(terms);
   TimedLaunch tl(KC_SPINE_MFMA, st);
   switch (nb) {
-    case 1: launch_timed(tl, k_spine_mfma<1>, grid, dim3(256), 0, st, wm, tb, y, rows, cols,
+    case 1: launch_timed(tl, (k_spine_mfma<1, TL>), grid, dim3(256), 0, st, wm, tb, y, rows, cols,
                          positions, S, accumulate ? 1 : 0); break;
-    case 2: launch_timed(tl, k_spine_mfma<2>, grid, dim3(256), 0, st, wm, tb, y, rows, cols,
+    case 2: launch_timed(tl, (k_spine_mfma<2, TL>), grid, dim3(256), 0, st, wm, tb, y, rows, cols,
                          positions, S, accumulate ? 1 : 0); break;
-    default: launch_timed(tl, k_spine_mfma<3>, grid, dim3(256), 0, st, wm, tb, y, rows, cols,
+    default: launch_timed(tl, (k_spine_mfma<3, TL>), grid, dim3(256), 0, st, wm, tb, y, rows, cols,
                           positions, S, accumulate ? 1 : 0); break;
   }
   const hipError_t e = hipGetLastError();
