@@ -815,7 +815,12 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   // 3..16 positions of a BF16 spine: every projection on the matrix cores
   // from BF16 activation terms (the fp32 kernels are bound by LDS and FMAs
   // there); the steps and their order are the same.
-  if (P >= K3_SPINE_MFMA_MIN_POSITIONS && kind == K3_SPINE_KIND_BF16 &&
+  const bool matrices_aligned =
+      ((reinterpret_cast<uintptr_t>(sp.router) | reinterpret_cast<uintptr_t>(sp.routed_down) |
+        reinterpret_cast<uintptr_t>(sp.routed_up) | reinterpret_cast<uintptr_t>(sp.shared_gate) |
+        reinterpret_cast<uintptr_t>(sp.shared_up) | reinterpret_cast<uintptr_t>(sp.shared_down)) &
+       15u) == 0;
+  if (P >= K3_SPINE_MFMA_MIN_POSITIONS && kind == K3_SPINE_KIND_BF16 && matrices_aligned &&
       spine_mfma_supported(kind, P, E, H) &&
       spine_mfma_supported(kind, P, H, R) && spine_mfma_supported(kind, P, H, S)) {
     auto mm = [&](const void* w, float* y, int rows, int cols, bool acc, const char* step) {

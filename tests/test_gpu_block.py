@@ -174,3 +174,36 @@ def test_block_rejects_bad_calls(gpu, k3_bank):
         spine.moe_block(sp, g, bank, stride, _dev(np.zeros((1, 32), np.float32)),
                         workspace=_dev(np.zeros(1 << 20, np.uint8)))
     assert e.value.status == _lib.K3_HIP_E_INVALID
+
+
+@pytest.mark.parametrize("positions", [1, 4])
+def test_block_unaligned_spine_falls_back(gpu, k3_bank, positions):
+    """Spine matrices 2 bytes off a 16-byte boundary and a norm weight 4 bytes
+    off: the fused and matrix-core forms do not apply, and the block runs the
+    separate launches and the any-shape kernel with the same result."""
+    import torch
+    from deltafin_amd import spine
+    g, bank, stride, span = k3_bank
+    say(f"block: unaligned BF16 spine, positions {positions}")
+    m = _k3_spine("bf16", 7 + positions)
+
+    def off(a, elems):
+        flat = np.zeros(a.size + elems, a.dtype)
+        flat[elems:] = a.ravel()
+        t = _dev(flat.view(np.int16) if a.dtype == np.uint16 else flat)
+        return t[elems:].view(*a.shape)
+
+    mats = {n: off(m[n], 1) for n in spine.MoeSpine.MATRICES}
+    sp = spine.MoeSpine("bf16", mats["router"], _dev(m["router_bias"]), mats["routed_down"],
+                        off(m["routed_norm"], 1), mats["routed_up"], mats["shared_gate"],
+                        mats["shared_up"], mats["shared_down"])
+    assert sp.routed_norm.data_ptr() % 16 == 4 and sp.router.data_ptr() % 16 == 2
+    hidden = np.random.default_rng(40 + positions).standard_normal(
+        (positions, K3["hidden"]), dtype=np.float32)
+    out, ids, _ = spine.moe_block(sp, g, bank, stride, _dev(hidden))
+    torch.cuda.synchronize()
+    want, want_ids, _, _ = S.moe_block_f64("bf16", m, span, hidden, K3["inter"], 16)
+    assert ids.cpu().numpy().tolist() == want_ids.tolist()
+    got = out.cpu().numpy().astype(np.float64)
+    for p in range(positions):
+        assert _normwise(got[p], want[p]) <= 1e-3, f"position {p}"
