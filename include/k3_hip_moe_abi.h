@@ -443,7 +443,9 @@ uint64_t k3_hip_moe_block_workspace_bytes(const K3HipMoeSpineV1* spine,
  *            + shared_down situ(shared_gate hidden, shared_up hidden)
  * hidden, out: device fp32 [n_positions, H] (16-byte aligned); route_ids /
  * route_weights (device, nullable): [n_positions, top_k].  Every product is
- * fp32.  The experts of a batch go through the verify paths
+ * fp32 (from 3 positions a 16-byte-aligned BF16 spine runs on the BF16 matrix
+ * cores from a three-term BF16 split of each activation, whose products are
+ * exact in fp32).  The experts of a batch go through the verify paths
  * (k3_hip_set_verify_mode).  Returns a K3_HIP_* status. */
 int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine,
                             const K3HipGeometryV1* experts,
