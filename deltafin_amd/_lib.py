@@ -38,6 +38,7 @@ K3_DTYPE_BF16 = 1
 K3_HIP_MAX_TOKEN_EXPERTS = 32
 K3_HIP_MAX_POSITIONS = 16
 K3_HIP_MAX_EDGES = 256
+K3_HIP_NOALLOC_SCRATCH_BYTES = 1 << 20
 
 
 class K3HipExpertDescriptorV1(C.Structure):
@@ -147,6 +148,8 @@ SIGNATURES = {
     "k3_hip_moe_layer_device": (_i32, [_GP, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _u64, _vp]),
     "k3_hip_moe_route_layer_device": (
         _i32, [_GP, _vp, _u64, _i32, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _u64, _vp]),
+    "k3_hip_moe_route_layer_device_noalloc": (
+        _i32, [_GP, _vp, _u64, _i32, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp]),
     "k3_hip_moe_verify_route_device": (
         _i32, [_GP, _vp, _u64, _i32, _vp, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _u64, _vp]),
     "k3_hip_moe_verify_device": (

@@ -49,7 +49,8 @@ CXX_FLAGS = [
     "-Wextra",
     "-Wno-unused-parameter",
 ]
-KERNEL_SOURCES = ["k3_kernels.hip", "k3_verify_mfma.hip", "k3_spine.hip", "k3_spine_mfma.hip"]
+KERNEL_SOURCES = ["k3_kernels.hip", "k3_verify_mfma.hip", "k3_spine.hip", "k3_spine_mfma.hip",
+                  "k3_noalloc.hip"]
 HOST_SOURCES = ["k3_abi.cpp", "k3_cache.cpp", "k3_timing.cpp", "k3_spine_abi.cpp"]
 
 

@@ -235,6 +235,27 @@ int k3_hip_moe_route_layer_device(const K3HipGeometryV1* g,
                                   float* route_weights, void* workspace,
                                   uint64_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): k3_hip_moe_route_layer_device with the same arguments
+ * and results, minus the workspace, which comes from a library-owned static
+ * device array of K3_HIP_NOALLOC_SCRATCH_BYTES per GPU (held until the process
+ * ends).  Allocates nothing.  A geometry / top_k whose workspace
+ * (k3_hip_moe_workspace_bytes(g, top_k, 1)) exceeds that size returns
+ * K3_HIP_E_INVALID (1 MiB holds top_k 16 at both presets; the benchmark
+ * geometry at top_k 32 needs about 1.4 MB and is refused).  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, or two threads) race and must be ordered
+ * by the caller. */
+#define K3_HIP_NOALLOC_SCRATCH_BYTES (UINT64_C(1) << 20)
+int k3_hip_moe_route_layer_device_noalloc(const K3HipGeometryV1* g,
+                                          const uint8_t* bank,
+                                          uint64_t expert_stride, int n_bank,
+                                          const float* logits, int top_k,
+                                          const void* x, int x_dtype,
+                                          void* out, int out_dtype,
+                                          int32_t* route_ids,
+                                          float* route_weights, void* stream);
+
 /* Batched speculative verify with device routing: positions p < n_positions
  * each route top_k of logits[p, n_bank]; experts are grouped so each routed
  * expert's bytes are read once for all positions that chose it (no reference
