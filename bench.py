@@ -97,6 +97,16 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--block-only", action="store_true",
                     help="print only the whole-K3-MoE-block timings")
     ap.add_argument("--no-block", action="store_true", help="skip the K3 MoE block timings")
+    ap.add_argument("--settle-ms", type=float, default=100.0,
+                    help="untimed back-to-back decode steps for this long before the warm-up "
+                         "steps (0 disables)")
+    ap.add_argument("--transient-probe", action="store_true",
+                    help="print per-phase decode step times from idle (the load-onset "
+                         "transient the settle phase waits out) and exit")
+    ap.add_argument("--no-single", action="store_true",
+                    help="skip the config-0 (one GEMV) and config-1 (one expert) legs")
+    ap.add_argument("--single-only", action="store_true",
+                    help="print only the config-0 and config-1 objects")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 4 plain device copies of 1 GiB (the known-size kernel "
                          "the HBM byte counters are scaled by) and exit")
@@ -123,22 +133,30 @@ def copy_calibration() -> int:
     return 0
 
 
-def cpu_threads() -> int:
+def cpu_nproc() -> int:
+    """CPUs this process may run on (what `nproc` prints)."""
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    # The reference pool caps at 32 threads (tools/fused_gemv_batch.c:36); one
-    # GPU's share of the box is 16 CPUs.
-    return max(1, min(n, 16))
+        return os.cpu_count() or 1
 
 
-def cpu_baseline(bank_host: np.ndarray, logits: np.ndarray, x_f32: np.ndarray,
-                 seconds: float, threads: int) -> tuple[dict, np.ndarray, int]:
-    """The reference CPU composition for config 2 (provider_moe.cpp:867-971 with
-    SiLU-GLU in place of SiTU): mxfp4_moe_layer over the 32 gate/up matrices with
-    the shared x, fp32 SiLU-GLU, mxfp4_gemv_batch over the 16 down matrices, then
-    the ordered combine.  Tokens are run in order until `seconds` of CPU work."""
+def cpu_threads() -> int:
+    """Pool threads of the reference CPU path: min(nproc, 32), the reference
+    pool's own cap (K3_MAX_THREADS, tools/fused_gemv_batch.c:36)."""
+    return max(1, min(cpu_nproc(), 32))
+
+
+MT_THREADS_CAP = 16  # mxfp4_gemv_mt splits rows over at most 16 threads (tools/fused_gemv.c:734)
+
+
+def cpu_token_fn(bank_host_base: int, threads: int):
+    """The reference CPU composition of one token-layer (provider_moe.cpp:867-971
+    with SiLU-GLU in place of SiTU): mxfp4_moe_layer over the routed experts'
+    gate/up matrices with the shared x, fp32 SiLU-GLU, mxfp4_gemv_batch over
+    their down matrices, then the route-ordered combine.  Returns
+    token(ids, weights, x_f32, stride) -> fp32 output, reading expert e's span
+    at bank_host_base + e * stride (host memory)."""
     import oracle
 
     ref = oracle.ref()
@@ -146,44 +164,59 @@ def cpu_baseline(bank_host: np.ndarray, logits: np.ndarray, x_f32: np.ndarray,
     u8p = C.POINTER(C.c_uint8)
     f32p = C.POINTER(C.c_float)
     off = oracle.expert_offsets(HIDDEN, INTER)
-    base = bank_host.ctypes.data
     rows13 = (C.c_int * (2 * TOP_K))(*([INTER] * (2 * TOP_K)))
     cols13 = (C.c_int * (2 * TOP_K))(*([HIDDEN] * (2 * TOP_K)))
     rows2 = (C.c_int * TOP_K)(*([HIDDEN] * TOP_K))
     cols2 = (C.c_int * TOP_K)(*([INTER] * TOP_K))
     gu = np.empty(2 * TOP_K * INTER, np.float32)
     yb = np.empty((TOP_K, HIDDEN), np.float32)
-    outs = []
 
-    def token(t: int) -> np.ndarray:
-        ids, w64 = oracle.topk_softmax(logits[t], TOP_K)
-        w = w64.astype(np.float32)
+    def token(ids, w, x_f32: np.ndarray, stride: int = SPAN, base: int | None = None) -> np.ndarray:
+        b0 = bank_host_base if base is None else base
+        k = len(ids)
         p13 = (u8p * (2 * TOP_K))()
         s13 = (u8p * (2 * TOP_K))()
         p2 = (u8p * TOP_K)()
         s2 = (u8p * TOP_K)()
         for j, e in enumerate(ids):
-            b = base + int(e) * SPAN
+            b = b0 + int(e) * stride
             p13[2 * j] = C.cast(b + off[0], u8p)
             s13[2 * j] = C.cast(b + off[1], u8p)
             p13[2 * j + 1] = C.cast(b + off[4], u8p)
             s13[2 * j + 1] = C.cast(b + off[5], u8p)
             p2[j] = C.cast(b + off[2], u8p)
             s2[j] = C.cast(b + off[3], u8p)
-        xt = np.ascontiguousarray(x_f32[t])
-        ref.mxfp4_moe_layer(p13, s13, rows13, cols13, 2 * TOP_K, xt.ctypes.data_as(f32p),
+        xt = np.ascontiguousarray(x_f32, dtype=np.float32)
+        ref.mxfp4_moe_layer(p13, s13, rows13, cols13, 2 * k, xt.ctypes.data_as(f32p),
                             gu.ctypes.data_as(f32p), threads)
-        g = gu.reshape(TOP_K, 2, INTER)[:, 0, :]
-        u = gu.reshape(TOP_K, 2, INTER)[:, 1, :]
+        g = gu[:2 * k * INTER].reshape(k, 2, INTER)[:, 0, :]
+        u = gu[:2 * k * INTER].reshape(k, 2, INTER)[:, 1, :]
         with np.errstate(over="ignore"):
             h = np.ascontiguousarray(g / (np.float32(1.0) + np.exp(-g)) * u, dtype=np.float32)
-        xs = (f32p * TOP_K)(*[h[j].ctypes.data_as(f32p) for j in range(TOP_K)])
-        ys = (f32p * TOP_K)(*[yb[j].ctypes.data_as(f32p) for j in range(TOP_K)])
-        ref.mxfp4_gemv_batch(p2, s2, xs, ys, rows2, cols2, TOP_K, threads)
+        xs = (f32p * TOP_K)(*[h[j].ctypes.data_as(f32p) for j in range(k)])
+        ys = (f32p * TOP_K)(*[yb[j].ctypes.data_as(f32p) for j in range(k)])
+        ref.mxfp4_gemv_batch(p2, s2, xs, ys, rows2, cols2, k, threads)
         out = np.zeros(HIDDEN, np.float32)
-        for j in range(TOP_K):
-            out += w[j] * yb[j]
+        for j in range(k):
+            out += np.float32(w[j]) * yb[j]
         return out
+
+    return token
+
+
+def cpu_baseline(bank_host: np.ndarray, logits: np.ndarray, x_f32: np.ndarray,
+                 seconds: float, threads: int) -> tuple[dict, np.ndarray, int]:
+    """The reference CPU composition for config 2 (cpu_token_fn) on the same
+    tokens and bank.  Tokens are run in order until `seconds` of CPU work."""
+    import oracle
+
+    ref = oracle.ref()
+    run = cpu_token_fn(bank_host.ctypes.data, threads)
+    outs = []
+
+    def token(t: int) -> np.ndarray:
+        ids, w64 = oracle.topk_softmax(logits[t], TOP_K)
+        return run(ids, w64.astype(np.float32), x_f32[t])
 
     token(0)  # warm the pool and the pages of the first token's experts
     n = 0
@@ -198,14 +231,13 @@ def cpu_baseline(bank_host: np.ndarray, logits: np.ndarray, x_f32: np.ndarray,
     res = {
         "value": rate,
         "unit": "token-layers/s",
-        "cores": threads,
+        **_cpu_env(threads),
         "kind": "reference",
         "sample": (f"first {n} of the {logits.shape[0]} tokens of the same workload, "
                    f"384-expert bank copied to host DRAM; mxfp4_moe_layer + fp32 SiLU-GLU + "
                    f"mxfp4_gemv_batch + ordered combine per token ({el:.1f} s)"),
         "achieved_gbs": rate * LAYER_BYTES / 1e9,
         "avx2": int(ref.mxfp4_have_avx2()),
-        "cpu_model": _cpu_model(),
     }
     return res, np.stack(outs), n
 
@@ -214,22 +246,50 @@ STREAM_LAYERS = 8
 STREAM_SLOTS = 1025          # 24e9 B of HBM / 23,396,352 B per expert
 STREAM_ZIPF = 1.1
 STREAM_WARMUP_TOKENS = 200
+STREAM_STAGING_SLOTS = 4     # pinned staging slots for layers held in pageable memory
+STREAM_CHECK_TOKENS = 2      # tokens whose 8 layer outputs are checked against the oracle
+STREAM_CPU_TOKENS = 4        # tokens of the CPU per-token compute figure
 
 
-def streamed_config4(n_tokens: int) -> dict:
-    """8 layers x 384 experts (71.87 GB) in pinned host
-    memory (as many 8.98 GB layer banks as the host will pin; the rest alias
-    them), a 1,025-slot (24 GB) HBM LRU cache, 16 distinct experts per layer
-    per token drawn Zipf(1.1) over a per-layer rank permutation (seeded).  Per
-    layer: plan -> fetch the misses (side-stream copies) -> resolve (the
-    compute stream waits per expert) -> layer kernels -> release, with no host
-    synchronisation, x chained layer to layer in bf16.  Reports tokens/s, the
-    PCIe rate of the uploads, the hit rate, and the copy/compute overlap
-    1 - (wall - max(copy, compute)) / min(copy, compute), where compute is the
-    same token sequence over resident experts and copy the same plan/fetch
-    sequence with no kernels."""
+def stream_routes(n_layers: int, n_bank: int, total: int, seed: int) -> tuple[np.ndarray, np.ndarray]:
+    """Per layer a seeded rank permutation of the experts; per token and layer
+    16 distinct ranks drawn Zipf(STREAM_ZIPF) without replacement, returned as
+    canonical ascending expert ids [total, layers, 16] and weights summing to 1."""
+    rng = np.random.default_rng(seed)
+    perms = [rng.permutation(n_bank) for _ in range(n_layers)]
+    pz = np.arange(1, n_bank + 1, dtype=np.float64) ** -STREAM_ZIPF
+    pz /= pz.sum()
+    routes = np.empty((total, n_layers, TOP_K), dtype=np.int64)
+    for t in range(total):
+        for layer in range(n_layers):
+            routes[t, layer] = np.sort(perms[layer][rng.choice(n_bank, TOP_K, replace=False, p=pz)])
+    weights = rng.random((total, n_layers, TOP_K)).astype(np.float32)
+    weights /= weights.sum(axis=2, keepdims=True)
+    return routes, weights
+
+
+def streamed_config4(n_tokens: int, cpu: bool = True) -> dict:
+    """8 distinct layers x 384 experts (71.87 GB) in host
+    memory, a 1,025-slot (24 GB) HBM LRU cache, 16 distinct experts per layer
+    per token drawn Zipf(1.1) over a per-layer rank permutation (seeded).
+    Each layer's 8.98 GB bank is pinned host memory where the host grants it;
+    layers it refuses to pin are held in pageable memory, distinct bytes, and
+    their misses go through the cache's pinned staging slots (a threaded host
+    copy, then the DMA).  Per layer: plan -> fetch the misses (side-stream
+    copies) -> resolve (the compute stream waits per expert) -> layer kernels
+    -> RMS norm of the layer output (k3_hip_rms_norm; it is the next layer's
+    fp32 x, as a model normalises between layers, so activations stay O(1))
+    -> release, with no host synchronisation.  Reports tokens/s, the PCIe rate of the uploads, the hit rate, the
+    misses served from pinned and from pageable layers, and the copy/compute
+    overlap 1 - (wall - max(copy, compute)) / min(copy, compute), where compute
+    is the same token sequence over resident experts and copy the same
+    plan/fetch sequence with no kernels.  Then STREAM_CHECK_TOKENS tokens run
+    through all 8 layers again with each layer's output checked against the
+    fp64 oracle on that layer's host bytes, and the reference CPU path's
+    per-token compute time (8 layers, cpu_token_fn on the host banks)."""
     import torch
 
+    import oracle
     from deltafin_amd import _lib, moe
 
     torch.cuda.set_device(0)
@@ -238,22 +298,24 @@ def streamed_config4(n_tokens: int) -> dict:
         raise _lib.K3HipError(lib.k3_hip_moe_available(0), "k3_hip_moe_available")
     g = moe.preset(2)
     L, NB = STREAM_LAYERS, N_BANK
-    # One pinned 8.98 GB bank per layer, as many as the host grants; logical
-    # layers past that read the bytes of pinned layer (layer % pinned) (the
-    # cache still keys every logical layer separately, so misses and uploads
-    # are those of 8 distinct layers).
     t0 = time.perf_counter()
-    hosts = []
+    hosts, pinned = [], []
     for layer in range(L):
-        try:
-            hosts.append(torch.empty(NB * SPAN, dtype=torch.uint8, pin_memory=True))
-        except Exception as e:  # torch raises its accelerator error (a RuntimeError) on OOM
-            log(f"streamed: pinned allocation of layer {layer} refused ({str(e).splitlines()[0]})")
-            break
-    if not hosts:
-        raise RuntimeError("streamed: no pinned host memory for even one layer")
+        h = None
+        if all(pinned):
+            try:
+                h = torch.empty(NB * SPAN, dtype=torch.uint8, pin_memory=True)
+            except Exception as e:  # torch raises its accelerator error (a RuntimeError) on OOM
+                log(f"streamed: pinning layer {layer} refused ({str(e).splitlines()[0]}); "
+                    f"layers {layer}..{L - 1} go to pageable memory")
+        if h is None:
+            h = torch.empty(NB * SPAN, dtype=torch.uint8)
+        hosts.append(h)
+        pinned.append(bool(h.is_pinned()))
     t_alloc = time.perf_counter() - t0
-    log(f"streamed: {len(hosts)} x {NB * SPAN / 1e9:.2f} GB pinned host banks in {t_alloc:.1f} s")
+    n_pinned = sum(pinned)
+    log(f"streamed: {n_pinned} pinned + {L - n_pinned} pageable x {NB * SPAN / 1e9:.2f} GB "
+        f"host banks in {t_alloc:.1f} s")
     bank = torch.empty(NB * SPAN, dtype=torch.uint8, device="cuda")
     for layer, h in enumerate(hosts):
         moe.synth_bank(g, bank, SPAN, NB, layer * NB, SEED)
@@ -261,79 +323,103 @@ def streamed_config4(n_tokens: int) -> dict:
     torch.cuda.synchronize()
     log(f"streamed: host banks filled ({time.perf_counter() - t0:.1f} s)")
 
-    # Routes: per layer a rank permutation, 16 distinct ranks per token ~ Zipf(1.1).
-    rng = np.random.default_rng(SEED + 4)
-    perms = [rng.permutation(NB) for _ in range(L)]
-    pz = np.arange(1, NB + 1, dtype=np.float64) ** -STREAM_ZIPF
-    pz /= pz.sum()
     total = STREAM_WARMUP_TOKENS + n_tokens
-    routes = np.empty((total, L, TOP_K), dtype=np.int64)
-    for t in range(total):
-        for layer in range(L):
-            routes[t, layer] = np.sort(perms[layer][rng.choice(NB, TOP_K, replace=False, p=pz)])
-    weights = rng.random((total, L, TOP_K)).astype(np.float32)
-    weights /= weights.sum(axis=2, keepdims=True)
+    routes, weights = stream_routes(L, NB, total + STREAM_CHECK_TOKENS, SEED + 4)
 
-    cache = lib.k3_hip_cache_create(0, SPAN, STREAM_SLOTS, L, 0)
+    cache = lib.k3_hip_cache_create(0, SPAN, STREAM_SLOTS, L, STREAM_STAGING_SLOTS)
     if not cache:
         raise _lib.K3HipError(-3, f"k3_hip_cache_create: {_lib.last_error()}")
-    xs = [moe.synth_normal(HIDDEN, torch.bfloat16, SEED + 5, 0),
-          torch.empty(HIDDEN, dtype=torch.bfloat16, device="cuda")]
+    xs = [moe.synth_normal(HIDDEN, torch.float32, SEED + 5, 0),
+          torch.empty(HIDDEN, dtype=torch.float32, device="cuda")]
+    x_first = xs[0].clone()
+    norm_w = torch.ones(HIDDEN, dtype=torch.float32, device="cuda")
     ws = moe.workspace(g, TOP_K)
     wsb, wsn = moe._ws_args(ws)
     st = moe.stream_handle()
     gref = C.byref(g)
-    host_base = [hosts[layer % len(hosts)].data_ptr() for layer in range(L)]
+    host_base = [hosts[layer].data_ptr() for layer in range(L)]
     u16 = C.c_uint16 * TOP_K
     missing = u16()
     n_missing = C.c_int(0)
     spans = (C.c_void_p * TOP_K)()
     srcs = (C.c_void_p * TOP_K)()
     plan_id = [0]
+    miss_by_kind = [0, 0]  # misses served from pageable / pinned layers
 
-    def layer_step(t: int, layer: int, cur: int) -> None:
+    def layer_kernels(spans_arr, w, x_in, y_out, x_next) -> None:
+        rc = lib.k3_hip_moe_layer_device(gref, spans_arr, w, TOP_K, x_in.data_ptr(),
+                                         _lib.K3_DTYPE_F32, y_out.data_ptr(), _lib.K3_DTYPE_F32,
+                                         wsb, wsn, st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_moe_layer_device")
+        rc = lib.k3_hip_rms_norm(y_out.data_ptr(), norm_w.data_ptr(), x_next.data_ptr(), 1,
+                                 HIDDEN, C.c_float(1e-5), st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_rms_norm")
+
+    def layer_step(c, t: int, layer: int, x_in, y_out, x_next=None) -> None:
         ids = u16(*routes[t, layer].tolist())
         plan_id[0] += 1
         pid = plan_id[0]
-        rc = lib.k3_hip_cache_plan(cache, pid, layer, ids, TOP_K, missing, C.byref(n_missing))
+        rc = lib.k3_hip_cache_plan(c, pid, layer, ids, TOP_K, missing, C.byref(n_missing))
         if rc != 0:
             raise _lib.K3HipError(rc, "k3_hip_cache_plan")
         for i in range(n_missing.value):
             srcs[i] = host_base[layer] + missing[i] * SPAN
-        rc = lib.k3_hip_cache_fetch(cache, pid, srcs, n_missing.value)
+        miss_by_kind[int(pinned[layer])] += n_missing.value
+        rc = lib.k3_hip_cache_fetch(c, pid, srcs, n_missing.value)
         if rc != 0:
             raise _lib.K3HipError(rc, "k3_hip_cache_fetch")
-        rc = lib.k3_hip_cache_resolve(cache, pid, ids, TOP_K, spans, st)
+        rc = lib.k3_hip_cache_resolve(c, pid, ids, TOP_K, spans, st)
         if rc != 0:
             raise _lib.K3HipError(rc, "k3_hip_cache_resolve")
-        w = (C.c_float * TOP_K)(*weights[t, layer].tolist())
-        rc = lib.k3_hip_moe_layer_device(gref, spans, w, TOP_K, xs[cur].data_ptr(),
-                                         _lib.K3_DTYPE_BF16, xs[1 - cur].data_ptr(),
-                                         _lib.K3_DTYPE_BF16, wsb, wsn, st)
-        if rc != 0:
-            raise _lib.K3HipError(rc, "k3_hip_moe_layer_device")
-        lib.k3_hip_cache_release(cache, pid)
+        if x_in is not None:
+            w = (C.c_float * TOP_K)(*weights[t, layer].tolist())
+            layer_kernels(spans, w, x_in, y_out, y_out if x_next is None else x_next)
+        lib.k3_hip_cache_release(c, pid)
 
-    def run(first: int, count: int) -> float:
+    def run(c, first: int, count: int, kernels: bool = True) -> float:
         cur = 0
         torch.cuda.synchronize()
         t_start = time.perf_counter()
         for t in range(first, first + count):
             for layer in range(L):
-                layer_step(t, layer, cur)
+                layer_step(c, t, layer, xs[cur] if kernels else None, xs[1 - cur])
                 cur = 1 - cur
         torch.cuda.synchronize()
         return time.perf_counter() - t_start
 
     six = (C.c_longlong * 6)()
-    run(0, STREAM_WARMUP_TOKENS)
+    run(cache, 0, STREAM_WARMUP_TOKENS)
     lib.k3_hip_cache_stats(cache, six)
     before = list(six)
-    wall = run(STREAM_WARMUP_TOKENS, n_tokens)
+    miss_by_kind[:] = [0, 0]
+    wall = run(cache, STREAM_WARMUP_TOKENS, n_tokens)
     lib.k3_hip_cache_stats(cache, six)
     hits, misses = six[0] - before[0], six[1] - before[1]
     uploaded = six[5] - before[5]
+    miss_pageable, miss_pinned = miss_by_kind
+
+    # Sampled outputs: tokens past the timed ones, each through all 8 layers,
+    # every layer's output (before the norm) checked against the fp64 oracle
+    # on the host bank's bytes, with the exact x the layer consumed.
+    worst = 0.0
+    x_cur = x_first.clone()
+    y32 = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    x_nxt = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    for t in range(total, total + STREAM_CHECK_TOKENS):
+        for layer in range(L):
+            layer_step(cache, t, layer, x_cur, y32, x_nxt)
+            torch.cuda.synchronize()
+            hb = hosts[layer].numpy()
+            sp = [hb[int(e) * SPAN:(int(e) + 1) * SPAN] for e in routes[t, layer]]
+            xin = x_cur.cpu().numpy()
+            ref, mag = oracle.moe_layer_f64(sp, weights[t, layer].astype(np.float64), HIDDEN,
+                                            INTER, oracle.ACT_SILU, xin)
+            worst = max(worst, oracle.cond_rel_err(y32.cpu().numpy(), ref, mag, INTER))
+            x_cur, x_nxt = x_nxt, x_cur
     lib.k3_hip_cache_destroy(cache)
+    log(f"streamed: checked {STREAM_CHECK_TOKENS} tokens x {L} layers, max cond rel err {worst:.2e}")
 
     # Compute alone: the same routes over experts resident in the device bank.
     ptrs = [[(C.c_void_p * TOP_K)(*[bank.data_ptr() + int(e) * SPAN for e in routes[t, layer]])
@@ -344,56 +430,35 @@ def streamed_config4(n_tokens: int) -> dict:
     for i, t in enumerate(range(STREAM_WARMUP_TOKENS, total)):
         for layer in range(L):
             w = (C.c_float * TOP_K)(*weights[t, layer].tolist())
-            rc = lib.k3_hip_moe_layer_device(gref, ptrs[i][layer], w, TOP_K, xs[cur].data_ptr(),
-                                             _lib.K3_DTYPE_BF16, xs[1 - cur].data_ptr(),
-                                             _lib.K3_DTYPE_BF16, wsb, wsn, st)
-            if rc != 0:
-                raise _lib.K3HipError(rc, "k3_hip_moe_layer_device")
+            layer_kernels(ptrs[i][layer], w, xs[cur], xs[1 - cur], xs[1 - cur])
             cur = 1 - cur
     torch.cuda.synchronize()
     compute = time.perf_counter() - t_start
     # Copy alone: the same plan/fetch/release sequence on a fresh cache with
     # no layer kernels (the side stream carries exactly the streamed run's
     # uploads), warm-up tokens included and then timed like the run.
-    cache2 = lib.k3_hip_cache_create(0, SPAN, STREAM_SLOTS, L, 0)
+    cache2 = lib.k3_hip_cache_create(0, SPAN, STREAM_SLOTS, L, STREAM_STAGING_SLOTS)
     if not cache2:
         raise _lib.K3HipError(-3, f"k3_hip_cache_create: {_lib.last_error()}")
-
-    def fetch_only(first: int, count: int) -> float:
-        torch.cuda.synchronize()
-        t_start = time.perf_counter()
-        for t in range(first, first + count):
-            for layer in range(L):
-                ids = u16(*routes[t, layer].tolist())
-                plan_id[0] += 1
-                pid = plan_id[0]
-                if lib.k3_hip_cache_plan(cache2, pid, layer, ids, TOP_K, missing,
-                                         C.byref(n_missing)) != 0:
-                    raise _lib.K3HipError(-2, "k3_hip_cache_plan")
-                for i in range(n_missing.value):
-                    srcs[i] = host_base[layer] + missing[i] * SPAN
-                if lib.k3_hip_cache_fetch(cache2, pid, srcs, n_missing.value) != 0:
-                    raise _lib.K3HipError(-4, "k3_hip_cache_fetch")
-                if lib.k3_hip_cache_resolve(cache2, pid, ids, TOP_K, spans, st) != 0:
-                    raise _lib.K3HipError(-2, "k3_hip_cache_resolve")
-                lib.k3_hip_cache_release(cache2, pid)
-        torch.cuda.synchronize()
-        return time.perf_counter() - t_start
-
-    fetch_only(0, STREAM_WARMUP_TOKENS)
-    copy = fetch_only(STREAM_WARMUP_TOKENS, n_tokens)
+    run(cache2, 0, STREAM_WARMUP_TOKENS, kernels=False)
+    copy = run(cache2, STREAM_WARMUP_TOKENS, n_tokens, kernels=False)
     lib.k3_hip_cache_destroy(cache2)
-    # Context: pinned H2D rate of one 1.5 GB copy.
+    # Context: H2D rate of one 1.5 GB copy from a pinned and from a pageable bank.
     probe = 64 * SPAN
     dst = torch.empty(probe, dtype=torch.uint8, device="cuda")
-    src = hosts[0][:probe]
-    dst.copy_(src, non_blocking=True)
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    for _ in range(3):
+    rates = {}
+    for kind, layer in (("pinned", pinned.index(True) if any(pinned) else None),
+                        ("pageable", pinned.index(False) if not all(pinned) else None)):
+        if layer is None:
+            continue
+        src = hosts[layer][:probe]
         dst.copy_(src, non_blocking=True)
-    torch.cuda.synchronize()
-    h2d_gbs = 3 * probe / (time.perf_counter() - t_start) / 1e9
+        torch.cuda.synchronize()
+        t_start = time.perf_counter()
+        for _ in range(3):
+            dst.copy_(src, non_blocking=True)
+        torch.cuda.synchronize()
+        rates[kind] = round(3 * probe / (time.perf_counter() - t_start) / 1e9, 2)
     overlap = 1.0 - (wall - max(copy, compute)) / min(copy, compute) if min(copy, compute) > 0 else None
     res = {
         "metric": "streamed-expert MoE tokens/s (8 layers, 16-of-384 per layer, host -> 24 GB HBM cache)",
@@ -405,34 +470,83 @@ def streamed_config4(n_tokens: int) -> dict:
         "ms_per_token": round(wall * 1e3 / n_tokens, 3),
         "data": "synthetic",
         "config": {
-            "workload": "BASELINE configs[4]: 8 layers x 384 MXFP4 experts (71.87 GB) in pinned "
-                        "host memory, 1,025-slot (24 GB) HBM LRU, Zipf(1.1) routes of 16 distinct "
-                        "experts per layer, bf16 x chained through the layers",
+            "workload": (f"BASELINE configs[4]: 8 distinct layers x 384 MXFP4 experts (71.87 GB) "
+                         f"in host memory, {n_pinned} layer banks pinned and {L - n_pinned} "
+                         f"pageable (the host refused to pin more; their misses go through "
+                         f"{STREAM_STAGING_SLOTS} pinned staging slots), 1,025-slot (24 GB) HBM "
+                         f"LRU, Zipf(1.1) routes of 16 distinct experts per layer, fp32 x "
+                         f"RMS-normalised between layers"),
             "layers": L, "experts_per_layer": NB, "top_k": TOP_K, "cache_slots": STREAM_SLOTS,
-            "zipf": STREAM_ZIPF, "pinned_layers": len(hosts),
-            "host_bank_bytes_pinned": len(hosts) * NB * SPAN,
+            "zipf": STREAM_ZIPF, "pinned_layers": n_pinned, "pageable_layers": L - n_pinned,
+            "host_bank_bytes_pinned": n_pinned * NB * SPAN,
+            "host_bank_bytes_pageable": (L - n_pinned) * NB * SPAN,
+            "staging_slots": STREAM_STAGING_SLOTS,
         },
         "hit_rate": round(hits / max(hits + misses, 1), 4),
         "misses_per_token": round(misses / n_tokens, 2),
+        "misses_per_token_pinned_layers": round(miss_pinned / n_tokens, 2),
+        "misses_per_token_pageable_layers": round(miss_pageable / n_tokens, 2),
         "pcie_gbs": round(uploaded / wall / 1e9, 2),
-        "h2d_probe_gbs": round(h2d_gbs, 2),
+        "h2d_probe_gbs": rates,
         "compute_only_ms_per_token": round(compute * 1e3 / n_tokens, 3),
         "copy_only_ms_per_token": round(copy * 1e3 / n_tokens, 3),
         "overlap": None if overlap is None else round(overlap, 3),
         "host_alloc_s": round(t_alloc, 1),
+        "parity": {"tokens_checked": STREAM_CHECK_TOKENS, "layers_each": L,
+                   "max_cond_rel_err_fp32": worst, "tolerance": 1e-3, "pass": bool(worst <= 1e-3)},
     }
+    if cpu:
+        # The reference CPU path's compute per token (8 layers) on the host
+        # banks; it has no streaming analog.
+        threads = cpu_threads()
+        run_cpu = cpu_token_fn(host_base[0], threads)
+        xh = x_first.cpu().numpy()
+        run_cpu(routes[0, 0], weights[0, 0], xh, SPAN, host_base[0])  # warm the pool
+        t_start = time.perf_counter()
+        for t in range(STREAM_WARMUP_TOKENS, STREAM_WARMUP_TOKENS + STREAM_CPU_TOKENS):
+            xt = xh
+            for layer in range(L):
+                y = run_cpu(routes[t, layer], weights[t, layer], xt, SPAN, host_base[layer])
+                xt = (y / np.sqrt(np.mean(y * y) + np.float32(1e-5))).astype(np.float32)
+        per_tok = (time.perf_counter() - t_start) / STREAM_CPU_TOKENS
+        res["cpu_baseline"] = {"value": round(1.0 / per_tok, 3), "unit": "tokens/s",
+                               "ms_per_token": round(per_tok * 1e3, 1), **_cpu_env(threads),
+                               "kind": "reference",
+                               "sample": (f"{STREAM_CPU_TOKENS} tokens x {L} layers of the same "
+                                          "routes, compute only (the host banks are the CPU's "
+                                          "resident weights): mxfp4_moe_layer + fp32 SiLU-GLU + "
+                                          "mxfp4_gemv_batch + ordered combine per layer")}
     del hosts, bank, dst
     return res
 
 
 def _cpu_model() -> str:
+    """The first CPU's /proc/cpuinfo identity: model name, vendor, family /
+    model / stepping, and the number of packages and logical CPUs listed."""
+    info: dict[str, str] = {}
+    packages: set[str] = set()
+    logical = 0
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" not in line:
+                continue
+            k, v = (s.strip() for s in line.split(":", 1))
+            if k == "processor":
+                logical += 1
+            elif k == "physical id":
+                packages.add(v)
+            elif k in ("model name", "vendor_id", "cpu family", "model", "stepping") and k not in info:
+                info[k] = v
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    return (f"{name} ({info.get('vendor_id', '?')} family {info.get('cpu family', '?')} model "
+            f"{info.get('model', '?')} stepping {info.get('stepping', '?')}; "
+            f"{max(len(packages), 1)} package(s), {logical} logical CPUs listed)")
+
+
+def _cpu_env(threads: int) -> dict:
+    return {"cores": threads, "nproc": cpu_nproc(), "cpu_model": _cpu_model()}
 
 
 def main() -> int:
@@ -440,7 +554,7 @@ def main() -> int:
     if args.copy_calibration:
         return copy_calibration()
     if args.streamed:
-        print(json.dumps(streamed_config4(args.streamed_tokens)), flush=True)
+        print(json.dumps(streamed_config4(args.streamed_tokens, not args.no_cpu)), flush=True)
         return 0
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: the routed-expert path is built and measured "
@@ -477,6 +591,10 @@ def main() -> int:
         print(json.dumps(_verify_config3(moe, _lib, g, bank, stride, max(1, args.verify_batches))),
               flush=True)
         return 0
+    if args.single_only:
+        print(json.dumps(_single_configs(moe, _lib, oracle, g, bank, stride, args.cpu_seconds,
+                                         args.no_cpu)), flush=True)
+        return 0
     if args.spine_only or args.block_only:
         del bank
         torch.cuda.empty_cache()
@@ -497,10 +615,30 @@ def main() -> int:
         if rc != 0:
             raise _lib.K3HipError(rc, "k3_hip_moe_route_layer_device")
 
+    if args.transient_probe:
+        print(json.dumps(_transient_probe(step)), flush=True)
+        return 0
+
+    # ---- settle (untimed): back-to-back decode steps until the GPU has run
+    # them for --settle-ms.  From idle, the first ~1.5 ms of this load run at
+    # full speed, the next ~10-20 ms at ~15 % lower throughput in both decode
+    # kernels, then the rate holds steady (bench.py --transient-probe; the
+    # same token can take 51 us in that window and 42.5 us after it).  The
+    # timed window starts in the steady state.
+    settle_steps = 0
+    t_settle = time.perf_counter()
+    while args.settle_ms > 0:
+        for i in range(100):
+            step(settle_steps + i)
+        settle_steps += 100
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t_settle) * 1e3 >= args.settle_ms:
+            break
+    settle_ms = (time.perf_counter() - t_settle) * 1e3
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    log(f"warmup {args.warmup} steps done")
+    log(f"settle {settle_steps} steps ({settle_ms:.1f} ms), warmup {args.warmup} steps done")
 
     # ---- timed region: exactly K steps, synchronised on both sides
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -535,6 +673,10 @@ def main() -> int:
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic,
+        "traffic_source": (f"not measured in this run: read from "
+                           f"{TRAFFIC_FILE.relative_to(ROOT)} (rocprofv3 --pmc FETCH_SIZE and "
+                           f"WRITE_SIZE per dispatch, each scaled by its reading for a 1 GiB "
+                           f"device copy)") if traffic is not None else None,
         "algorithmic_bytes_per_launch": KERNEL_BYTES[dom],
         "avg_launch_us": round(dom_s * 1e6, 3),
     }
@@ -577,6 +719,10 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"steps": settle_steps, "ms": round(settle_ms, 1),
+                   "note": "untimed decode steps run back to back before the warm-up steps, "
+                           "so the timed window starts after the GPU's load-onset transient "
+                           "(bench.py --transient-probe; profiles/decode_config2_load_transient.md)"},
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -600,37 +746,300 @@ def main() -> int:
         "other_decode_path": alt,
         "parity": parity,
     }
+    if not args.no_single:
+        res.update(_single_configs(moe, _lib, oracle, g, bank, stride, args.cpu_seconds,
+                                   args.no_cpu))
     if args.verify_batches > 0:
-        res["verify"] = _verify_config3(moe, _lib, g, bank, stride, args.verify_batches)
+        res["verify"] = _verify_config3(moe, _lib, g, bank, stride, args.verify_batches,
+                                        None if args.no_cpu else args.cpu_seconds)
     if not args.no_spine:
         res["spine"] = _spine_bench()
     if not args.no_block:
         res["k3_block"] = _k3_block_bench()
     if args.streamed_line_tokens > 0:
         try:
-            res["streamed"] = streamed_config4(args.streamed_line_tokens)
+            res["streamed"] = streamed_config4(args.streamed_line_tokens, not args.no_cpu)
         except Exception as e:  # reported in the line rather than losing the decode result
             log(f"streamed run failed: {e}")
             res["streamed"] = {"error": str(e).splitlines()[0]}
     if not args.no_cpu:
         log("cpu baseline: copying the bank to host DRAM")
-        bank_host = bank.cpu().numpy()
+        bank_host = host_bank(bank)
         lg_host = logits.cpu().numpy()
         x_host = x.float().cpu().numpy()  # bf16 -> fp32 widening outside the timed region
         threads = cpu_threads()
         cpu, cpu_out, n_cpu = cpu_baseline(bank_host, lg_host, x_host, args.cpu_seconds, threads)
-        # The GPU rows are bf16-rounded (relative step 2^-8): the difference is
-        # reported per token against the token's largest |output|.
+        # Cross-check on exactly the tokens the CPU ran: the GPU path computes
+        # them again, untimed, into their output rows.  The GPU rows are
+        # bf16-rounded (relative step 2^-8): the difference is reported per
+        # token against the token's largest |output|.
+        for t in range(n_cpu):
+            step(t)
+        torch.cuda.synchronize()
         gpu_out = out[:n_cpu].float().cpu().numpy()
         scale = np.max(np.abs(cpu_out), axis=1)
         cpu["gpu_bf16_vs_cpu_max_diff_over_max_abs"] = float(
             np.max(np.max(np.abs(gpu_out - cpu_out), axis=1) / scale))
+        cpu["cross_check_rows"] = n_cpu
         res["cpu_baseline"] = cpu
         log(f"cpu baseline {cpu['value']:.2f} tok/s with {threads} threads")
     else:
         res["cpu_baseline"] = None
     print(json.dumps(res), flush=True)
     return 0
+
+
+CFG0_BYTES = MAT_BYTES + HIDDEN * 4 + INTER * 4    # 7,835,648: W + fp32 x + fp32 y
+CFG1_BYTES = SPAN + X_BYTES + HIDDEN * 4           # 23,439,360: 3 matrices + bf16 x + fp32 out
+SINGLE_ROTATE = 64                                 # distinct matrices / experts per rotation
+
+
+def _roofline(nbytes: float, seconds: float) -> dict:
+    gbs = nbytes / seconds / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+
+
+def _single_configs(moe, _lib, oracle, g, bank, stride, cpu_seconds: float, no_cpu: bool,
+                    launches: int = 640) -> dict:
+    """BASELINE configs[0] and [1] on the resident bank.
+
+    Config 0: one 2048 x 7168 MXFP4 GEMV, fp32 x ~N(0,1), fp32 y, batch 1
+    (k3_hip_mxfp4_gemv, the k3_cuda_mxfp4_gemv counterpart).  The matrices
+    are the gate matrices of SINGLE_ROTATE distinct experts of the bank (501
+    MB, above the 256 MB Infinity Cache), launched round-robin back to back so
+    no launch finds its matrix in a cache.  Config 1: one expert's SwiGLU FFN,
+    y = down(silu(gate x) * (up x)), bf16 x, fp32 y, with fp32 accumulation
+    (k3_hip_moe_layer_device with one expert of weight 1.0, exact), over
+    SINGLE_ROTATE distinct experts (1.5 GB).  Each leg reports the host-timed
+    rate of the back-to-back calls and the kernels' device time per call
+    (dispatch stamps), GB/s over the algorithmic bytes, one call checked
+    against the fp64 oracle, and the reference CPU path on the same matrices
+    copied to host memory: config 0 through mxfp4_gemv_mt (threads created per
+    call, at most 16) and the pooled mxfp4_gemv_batch with one matrix; config 1
+    through mxfp4_moe_layer (gate and up) -> fp32 SiLU-GLU -> mxfp4_gemv_batch
+    (down), the reference CPU composition (provider_moe.cpp:867-971)."""
+    import torch
+
+    lib = _lib.load()
+    st = moe.stream_handle()
+    off = moe.span_offsets(g)
+    base = bank.data_ptr()
+    n_rot = SINGLE_ROTATE
+    res: dict = {}
+
+    # ---------------- config 0
+    x0 = moe.synth_normal(HIDDEN, torch.float32, SEED + 70, 1)
+    y0 = torch.empty(INTER, dtype=torch.float32, device="cuda")
+    mats = [(base + e * stride + off["w1p"], base + e * stride + off["w1s"]) for e in range(n_rot)]
+
+    def gemv(i: int) -> None:
+        p, s = mats[i % n_rot]
+        rc = lib.k3_hip_mxfp4_gemv(p, s, x0.data_ptr(), y0.data_ptr(), INTER, HIDDEN, 1, st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_mxfp4_gemv")
+
+    def timed_calls(fn, cls: list[str]) -> tuple[float, float]:
+        for i in range(n_rot):
+            fn(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(launches):
+            fn(i)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / launches
+        _lib.timing_begin(4 * launches)
+        for i in range(launches):
+            fn(i)
+        torch.cuda.synchronize()
+        kern, _ = _lib.timing_end()
+        dev = sum(kern[k]["total_ms"] for k in cls if k in kern) / 1e3 / launches
+        return wall, dev
+
+    wall0, dev0 = timed_calls(gemv, ["gemv"])
+    gemv(0)
+    torch.cuda.synchronize()
+    h_p = bank[off["w1p"]: off["w1p"] + INTER * HIDDEN // 2].cpu().numpy()
+    h_s = bank[off["w1s"]: off["w1s"] + INTER * HIDDEN // 32].cpu().numpy()
+    x0h = x0.cpu().numpy()
+    ref0, mag0 = oracle.gemv_f64(h_p, h_s, x0h, INTER, HIDDEN, with_mag=True)
+    err0 = oracle.cond_rel_err(y0.cpu().numpy(), ref0, mag0, HIDDEN)
+    c0 = {
+        "workload": ("BASELINE configs[0]: one 2048x7168 MXFP4 GEMV, fp32 x ~N(0,1), fp32 y, "
+                     f"batch 1, round-robin over {n_rot} distinct matrices "
+                     f"({n_rot * MAT_BYTES / 1e6:.0f} MB) so every launch streams HBM"),
+        "algorithmic_bytes": CFG0_BYTES,
+        "launches": launches,
+        "us_per_call_wall": round(wall0 * 1e6, 3),
+        "us_per_call_device": round(dev0 * 1e6, 3),
+        "gemvs_per_s": round(1 / wall0, 1),
+        "achieved_gbs_wall": round(CFG0_BYTES / wall0 / 1e9, 1),
+        "roofline": _roofline(CFG0_BYTES, dev0),
+        "parity": {"max_cond_rel_err": err0, "tolerance": 1e-3, "pass": bool(err0 <= 1e-3)},
+    }
+    log(f"config 0: {wall0 * 1e6:.2f} us/GEMV wall, {dev0 * 1e6:.2f} us device "
+        f"({CFG0_BYTES / dev0 / 1e9:.0f} GB/s), parity {err0:.2e}")
+
+    # ---------------- config 1
+    x1 = moe.synth_normal(HIDDEN, torch.bfloat16, SEED + 71, 1)
+    y1 = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    ws = moe.workspace(g, 1)
+    wsb, wsn = moe._ws_args(ws)
+    one = (C.c_float * 1)(1.0)
+    experts = [(C.c_void_p * 1)(base + e * stride) for e in range(n_rot)]
+    gref = C.byref(g)
+
+    def expert(i: int) -> None:
+        rc = lib.k3_hip_moe_layer_device(gref, experts[i % n_rot], one, 1, x1.data_ptr(),
+                                         _lib.K3_DTYPE_BF16, y1.data_ptr(), _lib.K3_DTYPE_F32,
+                                         wsb, wsn, st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_moe_layer_device")
+
+    wall1, dev1 = timed_calls(expert, ["glu_decode", "down_decode", "decode_fused"])
+    expert(0)
+    torch.cuda.synchronize()
+    span0 = bank[:SPAN].cpu().numpy()
+    x1h = x1.float().cpu().numpy()
+    ref1, _, mag1 = oracle.expert_f64(span0, HIDDEN, INTER, oracle.ACT_SILU, x1h)
+    err1 = oracle.cond_rel_err(y1.cpu().numpy(), ref1, mag1, INTER)
+    c1 = {
+        "workload": ("BASELINE configs[1]: one expert SwiGLU FFN at batch 1, gate/up 2048x7168 "
+                     "and down 7168x2048 MXFP4, bf16 x ~N(0,1), fp32 y, fp32 accumulation, "
+                     f"round-robin over {n_rot} distinct experts ({n_rot * SPAN / 1e9:.2f} GB)"),
+        "algorithmic_bytes": CFG1_BYTES,
+        "launches": launches,
+        "us_per_call_wall": round(wall1 * 1e6, 3),
+        "us_per_call_device": round(dev1 * 1e6, 3),
+        "experts_per_s": round(1 / wall1, 1),
+        "achieved_gbs_wall": round(CFG1_BYTES / wall1 / 1e9, 1),
+        "roofline": _roofline(CFG1_BYTES, dev1),
+        "parity": {"max_cond_rel_err": err1, "tolerance": 1e-3, "pass": bool(err1 <= 1e-3)},
+    }
+    log(f"config 1: {wall1 * 1e6:.2f} us/expert wall, {dev1 * 1e6:.2f} us device "
+        f"({CFG1_BYTES / dev1 / 1e9:.0f} GB/s), parity {err1:.2e}")
+
+    if not no_cpu:
+        c0["cpu_baseline"], c1["cpu_baseline"] = _single_cpu(
+            oracle, bank, stride, off, x0h, x1h, cpu_seconds)
+    res["config0"] = c0
+    res["config1"] = c1
+    return res
+
+
+def _single_cpu(oracle, bank, stride, off, x0h: np.ndarray, x1h: np.ndarray,
+                seconds: float) -> tuple[dict, dict]:
+    """The reference CPU kernels on the config-0 matrices and config-1 experts
+    (host copies of the same bytes), each timed for about seconds / 3."""
+    ref = oracle.ref()
+    u8p, f32p = C.POINTER(C.c_uint8), C.POINTER(C.c_float)
+    threads = cpu_threads()
+    mt = min(cpu_nproc(), MT_THREADS_CAP)
+    ref.mxfp4_pool_init(threads)
+    n_rot = SINGLE_ROTATE
+    hb = host_bank(bank)
+    host = [hb[e * stride: e * stride + SPAN] for e in range(n_rot)]
+    y0 = np.empty(INTER, np.float32)
+    x0 = np.ascontiguousarray(x0h, dtype=np.float32)
+
+    def rate(fn, budget: float) -> tuple[float, int]:
+        fn(0)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn(n)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return el / n, n
+
+    def gemv_mt(i: int) -> None:
+        h = host[i % n_rot]
+        ref.mxfp4_gemv_mt(h[off["w1p"]:].ctypes.data_as(u8p), h[off["w1s"]:].ctypes.data_as(u8p),
+                          x0.ctypes.data_as(f32p), y0.ctypes.data_as(f32p), INTER, HIDDEN, mt)
+
+    rows1 = (C.c_int * 1)(INTER)
+    cols1 = (C.c_int * 1)(HIDDEN)
+    ys = (f32p * 1)(y0.ctypes.data_as(f32p))
+    xs = (f32p * 1)(x0.ctypes.data_as(f32p))
+
+    def gemv_pool(i: int) -> None:
+        h = host[i % n_rot]
+        ps = (u8p * 1)(h[off["w1p"]:].ctypes.data_as(u8p))
+        ss = (u8p * 1)(h[off["w1s"]:].ctypes.data_as(u8p))
+        ref.mxfp4_gemv_batch(ps, ss, xs, ys, rows1, cols1, 1, threads)
+
+    t_mt, n_mt = rate(gemv_mt, seconds / 3)
+    t_pool, n_pool = rate(gemv_pool, seconds / 6)
+    env = _cpu_env(threads)
+    c0 = {"value": round(CFG0_BYTES / t_mt / 1e9, 2), "unit": "GB/s", **env, "mt_threads": mt,
+          "kind": "reference",
+          "sample": (f"{n_mt} mxfp4_gemv_mt calls ({mt} threads, created per call) round-robin "
+                     f"over the same {n_rot} matrices in host DRAM"),
+          "us_per_call": round(t_mt * 1e6, 1),
+          "pool_batch1": {"us_per_call": round(t_pool * 1e6, 1),
+                          "gbs": round(CFG0_BYTES / t_pool / 1e9, 2), "threads": threads,
+                          "calls": n_pool},
+          "avx2": int(ref.mxfp4_have_avx2())}
+
+    x1 = np.ascontiguousarray(x1h, dtype=np.float32)  # bf16 -> fp32 outside the timed region
+    gu = np.empty(2 * INTER, np.float32)
+    y1 = np.empty(HIDDEN, np.float32)
+    rows13 = (C.c_int * 2)(INTER, INTER)
+    cols13 = (C.c_int * 2)(HIDDEN, HIDDEN)
+    rows2 = (C.c_int * 1)(HIDDEN)
+    cols2 = (C.c_int * 1)(INTER)
+    y1s = (f32p * 1)(y1.ctypes.data_as(f32p))
+
+    def expert(i: int) -> None:
+        h = host[i % n_rot]
+        p13 = (u8p * 2)(h[off["w1p"]:].ctypes.data_as(u8p), h[off["w3p"]:].ctypes.data_as(u8p))
+        s13 = (u8p * 2)(h[off["w1s"]:].ctypes.data_as(u8p), h[off["w3s"]:].ctypes.data_as(u8p))
+        ref.mxfp4_moe_layer(p13, s13, rows13, cols13, 2, x1.ctypes.data_as(f32p),
+                            gu.ctypes.data_as(f32p), threads)
+        g_, u_ = gu[:INTER], gu[INTER:]
+        with np.errstate(over="ignore"):
+            hh = np.ascontiguousarray(g_ / (np.float32(1.0) + np.exp(-g_)) * u_, dtype=np.float32)
+        p2 = (u8p * 1)(h[off["w2p"]:].ctypes.data_as(u8p))
+        s2 = (u8p * 1)(h[off["w2s"]:].ctypes.data_as(u8p))
+        hs = (f32p * 1)(hh.ctypes.data_as(f32p))
+        ref.mxfp4_gemv_batch(p2, s2, hs, y1s, rows2, cols2, 1, threads)
+
+    t_e, n_e = rate(expert, seconds / 2)
+    c1 = {"value": round(CFG1_BYTES / t_e / 1e9, 2), "unit": "GB/s", **env, "kind": "reference",
+          "sample": (f"{n_e} experts round-robin over the same {n_rot} experts in host DRAM: "
+                     f"mxfp4_moe_layer (gate, up) + fp32 SiLU-GLU + mxfp4_gemv_batch (down)"),
+          "us_per_call": round(t_e * 1e6, 1), "avx2": int(ref.mxfp4_have_avx2())}
+    log(f"config 0/1 cpu: gemv_mt {t_mt * 1e6:.0f} us, pool {t_pool * 1e6:.0f} us, "
+        f"expert {t_e * 1e6:.0f} us")
+    return c0, c1
+
+
+def _transient_probe(step) -> dict:
+    """Decode step rates in phases from a cold start, to show the GPU's
+    load-onset transient: host-timed µs per step of each phase (the per-launch
+    kernel durations come from running this under rocprofv3 --kernel-trace).
+    Tokens are those of the config-2 workload; `same` phases repeat tokens 5-24,
+    `new` ones take tokens never run before in the process."""
+    import torch
+
+    phases = (("warm5", 0, 5, 0.0), ("first20", 5, 20, 0.0), ("same20", 5, 20, 0.0),
+              ("same20_after_idle_0.5s", 5, 20, 0.5), ("new20", 500, 20, 0.0),
+              ("run1000", 0, 1000, 0.0), ("same20_after_run", 5, 20, 0.0),
+              ("same20_after_idle_1s", 5, 20, 1.0), ("new20_after_idle_1s", 300, 20, 1.0))
+    out = []
+    for name, first, n, idle in phases:
+        if idle:
+            time.sleep(idle)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(n):
+            step(first + i)
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) * 1e6 / n
+        log(f"transient probe {name}: {us:.2f} us/step")
+        out.append({"phase": name, "first_token": first, "steps": n, "idle_before_s": idle,
+                    "us_per_step": round(us, 2)})
+    return {"transient_probe": out}
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_decode_config2.txt"
@@ -750,8 +1159,15 @@ def _verify_batches(moe, _lib, g, bank, stride, logits, x, batches: int) -> dict
         if kus.get("glu_mfma") else None,
         "down_mfma_gbs": round(union * MAT_BYTES / (kus["down_mfma"] * 1e-6) / 1e9, 1)
         if kus.get("down_mfma") else None,
+        # Useful = the layer's own multiply-adds (2 flops per weight and real
+        # token) over the two matrix-core kernels' time; issued = every MFMA
+        # the kernels issue (16 token columns each, padding and parity split
+        # included), which is what keeps the matrix cores busy.
+        "mfma_util": round(useful / mfma_s / (MFMA_PEAK_FP8_TFLOPS * 1e12), 5) if mfma_s else None,
+        "mfma_useful_tflops": round(useful / mfma_s / 1e12, 2) if mfma_s else None,
         "mfma_issued_tflops": round(issued / mfma_s / 1e12, 1) if mfma_s else None,
-        "mfma_util": round(issued / mfma_s / (MFMA_PEAK_FP8_TFLOPS * 1e12), 4) if mfma_s else None,
+        "mfma_issued_util": round(issued / mfma_s / (MFMA_PEAK_FP8_TFLOPS * 1e12), 4)
+        if mfma_s else None,
         "useful_tflops_union_mfma": round(useful / usec / 1e12, 2),
     }
     log(f"verify M={m}: auto -> {auto_path} {sec * 1e6:.1f} us/batch (union {union:.1f} of "
@@ -905,7 +1321,8 @@ def _k3_block_bench(calls: int = 20) -> dict:
     return out
 
 
-def _verify_config3(moe, _lib, g, bank, stride, batches: int) -> dict:
+def _verify_config3(moe, _lib, g, bank, stride, batches: int,
+                    cpu_seconds: float | None = None) -> dict:
     """batched speculative verify over the same resident
     bank: M positions, each with its own top-16 of 384 N(0,1) logits and bf16
     x.  Each M is timed on the library's default path (AUTO: the matrix-core
@@ -914,7 +1331,14 @@ def _verify_config3(moe, _lib, g, bank, stride, batches: int) -> dict:
     `shared_M16`, gives 16 positions logits with a common N(0,1) component
     (logits = z_common + 0.5 z_position, as consecutive draft tokens of one
     sequence share much of their routing): there the union is small and the
-    matrix cores carry a real small-M contraction."""
+    matrix cores carry a real small-M contraction.
+
+    With cpu_seconds, each M also carries `cpu_per_row`: the reference CPU
+    path as the reference runs a verify tile, one token's expert-set
+    composition per position with no union amortisation (provider_moe.cpp:
+    1092-1105; cpu_token_fn), timed on the same batches (about cpu_seconds / 4
+    per M), beside the bytes that composition reads (M x 16 experts) and the
+    union bytes the GPU reads."""
     import torch
 
     out = {}
@@ -923,6 +1347,9 @@ def _verify_config3(moe, _lib, g, bank, stride, batches: int) -> dict:
         logits = moe.synth_normal(n * m * N_BANK, torch.float32, SEED + 30 + m, 1).view(n, m, N_BANK)
         x = moe.synth_normal(n * m * HIDDEN, torch.bfloat16, SEED + 30 + m, 2).view(n, m, HIDDEN)
         out[f"M{m}"] = _verify_batches(moe, _lib, g, bank, stride, logits, x, batches)
+        if cpu_seconds:
+            out[f"M{m}"]["cpu_per_row"] = _verify_cpu(bank, logits, x, out[f"M{m}"],
+                                                      cpu_seconds / 4)
     m = 16
     n = batches + 3
     common = moe.synth_normal(n * N_BANK, torch.float32, SEED + 60, 1).view(n, 1, N_BANK)
@@ -932,10 +1359,61 @@ def _verify_config3(moe, _lib, g, bank, stride, batches: int) -> dict:
     out["shared_M16"] = _verify_batches(moe, _lib, g, bank, stride, logits, x, batches)
     return {"config": "BASELINE configs[3]: M positions each routing top-16 of 384, bf16 x/out; "
                       "us_per_batch on the default path; union_mfma_* on the matrix-core union "
-                      "kernels (every routed expert read once per batch); mfma_util = issued "
-                      "block-scaled MFMA flops (16 token columns each) / (gate/up + down kernel "
-                      "time x 5.0 PFLOP/s dense fp8)",
+                      "kernels (every routed expert read once per batch); mfma_util = the "
+                      "layer's useful flops (2 per weight and routed token) / (gate/up + down "
+                      "matrix-core kernel time x 5.0 PFLOP/s dense fp8); mfma_issued_util counts "
+                      "every issued block-scaled MFMA (16 token columns each, padding and the "
+                      "parity split included)",
             **out}
+
+
+_HOST_BANK: dict = {}
+
+
+def host_bank(bank) -> np.ndarray:
+    """Host copy of the resident bank (made once per process)."""
+    key = (bank.data_ptr(), bank.numel())
+    if key not in _HOST_BANK:
+        log("copying the bank to host DRAM for the CPU legs")
+        _HOST_BANK.clear()
+        _HOST_BANK[key] = bank.cpu().numpy()
+    return _HOST_BANK[key]
+
+
+def _verify_cpu(bank, logits, x, gpu: dict, seconds: float) -> dict:
+    """The reference CPU composition of a verify tile: per position, that
+    position's own top-16 through cpu_token_fn, batches in order (from batch 3,
+    the GPU's first timed batch) until `seconds` of work."""
+    import oracle
+
+    threads = cpu_threads()
+    hb = host_bank(bank)
+    run = cpu_token_fn(hb.ctypes.data, threads)
+    lg = logits.cpu().numpy()
+    xf = x.float().cpu().numpy()  # bf16 -> fp32 widening outside the timed region
+    n, m = lg.shape[0], lg.shape[1]
+    routes = [[oracle.topk_softmax(lg[i, p], TOP_K) for p in range(m)] for i in range(n)]
+    run(routes[0][0][0], routes[0][0][1].astype(np.float32), xf[0, 0])  # warm the pool
+    done, t0 = 0, time.perf_counter()
+    while True:
+        i = 3 + done % max(n - 3, 1)
+        for p in range(m):
+            ids, w = routes[i][p]
+            run(ids, w.astype(np.float32), xf[i, p])
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per_batch = el / done
+    nbytes = m * LAYER_BYTES
+    return {"ms_per_batch": round(per_batch * 1e3, 2), "token_layers_per_s": round(m / per_batch, 1),
+            "bytes_read_per_batch": nbytes, "achieved_gbs": round(nbytes / per_batch / 1e9, 1),
+            "union_bytes_per_batch_gpu": gpu["algorithmic_bytes"],
+            "gpu_speedup": round(per_batch * 1e6 / gpu["us_per_batch"], 1),
+            "batches": done, **_cpu_env(threads), "kind": "reference",
+            "sample": (f"{done} verify batches of {m} positions: per position "
+                       "mxfp4_moe_layer + fp32 SiLU-GLU + mxfp4_gemv_batch + ordered combine "
+                       "(no union amortisation, as the reference CPU path)")}
 
 
 def _parity(moe, oracle, synth, g, bank, stride, logits, x, ws, n_tokens: int) -> dict:

@@ -105,6 +105,22 @@ K3_SPINE_MATRIX_BF16 = 0
 K3_SPINE_MATRIX_INT8 = 1
 K3_MOE_SPINE_ABI_V1 = 1
 
+
+class K3HipCachePolicyV1(C.Structure):
+    _fields_ = [
+        ("abi_version", C.c_uint32),
+        ("struct_bytes", C.c_uint32),
+        ("automatic_capacity", C.c_uint32),
+        ("reserve_kind", C.c_uint32),
+        ("capacity_experts", C.c_uint64),
+        ("reserve_value", C.c_uint64),
+    ]
+
+
+K3_CACHE_RESERVE_AUTO, K3_CACHE_RESERVE_BYTES, K3_CACHE_RESERVE_RATIO_PPM = 0, 1, 2
+K3_HIP_CACHE_MAX_EXPERTS = 65536
+assert C.sizeof(K3HipCachePolicyV1) == 32
+
 assert C.sizeof(K3HipMoeSpineV1) == 144
 assert C.sizeof(K3HipKernelTimingV1) == 64
 assert C.sizeof(K3HipExpertDescriptorV1) == 32
@@ -159,8 +175,12 @@ SIGNATURES = {
     "k3_hip_cache_plan": (_i32, [_vp, _u64, _i32, _vp, _i32, _vp, C.POINTER(_i32)]),
     "k3_hip_cache_fetch": (_i32, [_vp, _u64, _vp, _i32]),
     "k3_hip_cache_resolve": (_i32, [_vp, _u64, _vp, _i32, _vp, _vp]),
-    "k3_hip_cache_ready_subset": (_i32, [_vp, _u64, _vp, _i32, _vp]),
+    "k3_hip_cache_ready_subset": (_i32, [_vp, _u64, _vp, _i32, _vp, _vp]),
     "k3_hip_cache_release": (None, [_vp, _u64]),
+    "k3_hip_cache_configure": (_i32, [_vp, C.POINTER(K3HipCachePolicyV1)]),
+    "k3_hip_cache_budget": (_i32, [_vp, C.POINTER(C.c_longlong)]),
+    "k3_hip_cache_materialize_plan": (_i32, [_vp, _u64, _vp, _i32, _vp, _u64, C.POINTER(_i32)]),
+    "k3_hip_cache_fail_allocations": (_i32, [_vp, _i32]),
     "k3_hip_cache_stats": (None, [_vp, C.POINTER(C.c_longlong)]),
     "k3_hip_cache_read_back": (_i32, [_vp, _i32, C.c_uint16, _vp, _u64]),
     "k3_hip_cache_state": (_i32, [_vp, C.c_char_p, _u64]),

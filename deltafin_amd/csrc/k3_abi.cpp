@@ -237,6 +237,8 @@ bool lds_fits(const void* kernel, int block, size_t dynamic_lds) {
 namespace {
 
 bool geometry_from(const K3HipGeometryV1* g, Geo* out);
+int verify_table(const Geo& g, const EdgeTable& tbl, const void* x, int x_dtype, void* out,
+                 int out_dtype, const Workspace& ws, hipStream_t st);
 
 // ---------------------------------------------------------------- presets
 void fill_geometry(uint32_t hidden, uint32_t inter, uint32_t act, K3HipGeometryV1* out) {
@@ -581,34 +583,10 @@ int positions_locked(Context& c, const Geo& lg, const uint8_t* const* blobs, int
     return finish_call_locked(c, temps, fail(K3_HIP_E_COPY, "positions input copy: %s", hipGetErrorString(e)));
   Workspace ws;
   carve_workspace(c.ws, c.ws_bytes, c.geo, K3_HIP_MAX_EDGES, K3_HIP_MAX_POSITIONS, &ws);
-  int rc = K3_HIP_OK;
-  if (lg.layout == K3_LAYOUT_SCALE4_V2) {
-    // scale4-v2 runs through the decode kernels: one layer per position (a
-    // position with no edges gets a zero row).
-    for (int p = 0; p < n_pos && rc == K3_HIP_OK; ++p) {
-      float* op = c.dout + (size_t)p * c.geo.hidden;
-      const int n = offs[p + 1] - offs[p];
-      if (n == 0) {
-        e = hipMemsetAsync(op, 0, (size_t)c.geo.hidden * 4, c.stream);
-        if (e != hipSuccess) rc = hip_fail("positions zero row", e);
-        continue;
-      }
-      TokenRoute route;
-      memset(&route, 0, sizeof(route));
-      route.n = n;
-      for (int j = 0; j < n; ++j) {
-        route.ptr[j] = tbl.ptr[offs[p] + j];
-        route.w[j] = tbl.w[offs[p] + j];
-      }
-      rc = launch_decode_layer(lg, route, c.dx + (size_t)p * c.geo.hidden, K3_DTYPE_F32, op,
-                               K3_DTYPE_F32, ws, c.stream);
-    }
-  } else {
-    rc = launch_verify_plan_table(tbl, ws, c.stream);
-    if (rc == K3_HIP_OK)
-      rc = launch_verify_layer(c.geo, n_edges, n_pos, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws,
-                               c.stream);
-  }
+  // The same path selection as the device surface (k3_hip_set_verify_mode):
+  // raw-v1 spans take the matrix-core union path where it applies and pays,
+  // scale4-v2 spans run one decode layer per position.
+  int rc = verify_table(lg, tbl, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws, c.stream);
   if (rc == K3_HIP_OK &&
       (e = hipMemcpyAsync(c.hout, c.dout, bytes, hipMemcpyDeviceToHost, c.stream)) != hipSuccess)
     rc = fail(K3_HIP_E_COPY, "positions output copy: %s", hipGetErrorString(e));
@@ -647,6 +625,76 @@ double expected_union(int n_bank, int top_k, int n_positions) {
   double miss = 1.0;
   for (int i = 0; i < n_positions; ++i) miss *= 1.0 - p;
   return (double)n_bank * (1.0 - miss);
+}
+
+// Verify over a caller route table, shared by k3_hip_moe_verify_device and
+// the descriptor surface's positions call: the matrix-core union path, the
+// VALU union kernels or one decode layer per position, as the verify mode and
+// the route's sharing say (k3_hip_set_verify_mode).  The union paths read
+// raw-v1 spans; other layouts run per position.  Positions without edges get
+// zero rows.
+int verify_table(const Geo& g, const EdgeTable& tbl, const void* x, int x_dtype, void* out,
+                 int out_dtype, const Workspace& ws, hipStream_t st) {
+  const int n_edges = tbl.n_edges, n_positions = tbl.n_positions;
+  const size_t xb = x_dtype == K3_DTYPE_BF16 ? 2 : 4, ob = out_dtype == K3_DTYPE_BF16 ? 2 : 4;
+  if (n_edges == 0) return launch_zero(out, (uint64_t)n_positions * g.hidden * ob, st);
+  // Distinct experts and the most edges any one of them carries (the
+  // matrix-core path takes up to 16 edges, one token column each).
+  int n_unique = 0, max_edges_per_expert = 0;
+  for (int i = 0; i < n_edges; ++i) {
+    bool seen = false;
+    for (int j = 0; j < i && !seen; ++j) seen = tbl.ptr[j] == tbl.ptr[i];
+    if (seen) continue;
+    ++n_unique;
+    int c = 0;
+    for (int j = i; j < n_edges; ++j) c += tbl.ptr[j] == tbl.ptr[i];
+    max_edges_per_expert = std::max(max_edges_per_expert, c);
+  }
+  const int mode = g_verify_mode.load();
+  const bool raw = g.layout == K3_LAYOUT_RAW_V1;
+  const bool mfma_ok = raw && verify_mfma_supported(g) && max_edges_per_expert <= 16;
+  if (mode == K3_VERIFY_UNION_MFMA && !mfma_ok)
+    return fail(K3_HIP_E_CAPABILITY,
+                "verify: no matrix-core path (geometry/layout, or an expert with %d > 16 edges)",
+                max_edges_per_expert);
+  const bool mfma = mode == K3_VERIFY_UNION_MFMA ||
+                    (mode == K3_VERIFY_AUTO && n_positions >= 2 && mfma_ok &&
+                     n_unique <= kUnionFraction * n_edges);
+  // Without the matrix-core path, positions that share most of their experts
+  // take the VALU union kernels (each shared expert read once); otherwise one
+  // decode layer per position (about twice the streaming rate of the VALU
+  // union kernels, so they win unless the union is under half the edges).
+  const bool valu = raw && (mode == K3_VERIFY_UNION_VALU ||
+                            (mode == K3_VERIFY_AUTO && !mfma && !mfma_ok && 2 * n_unique <= n_edges));
+  if (mfma || valu) {
+    int rc = launch_verify_plan_table(tbl, ws, st);
+    if (rc != K3_HIP_OK) return rc;
+    return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
+                : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
+  }
+  for (int p = 0; p < n_positions; ++p) {
+    const int e0 = tbl.pos_off[p], n = tbl.pos_off[p + 1] - e0;
+    uint8_t* outp = static_cast<uint8_t*>(out) + (size_t)p * g.hidden * ob;
+    if (n == 0) {  // no routed expert: a zero row
+      const int rc = launch_zero(outp, (uint64_t)g.hidden * ob, st);
+      if (rc != K3_HIP_OK) return rc;
+      continue;
+    }
+    if (n > K3_HIP_MAX_TOKEN_EXPERTS)
+      return fail(K3_HIP_E_INVALID, "verify: position %d has %d edges (at most %d)", p, n,
+                  K3_HIP_MAX_TOKEN_EXPERTS);
+    TokenRoute route;
+    memset(&route, 0, sizeof(route));
+    route.n = n;
+    for (int i = 0; i < n; ++i) {
+      route.ptr[i] = tbl.ptr[e0 + i];
+      route.w[i] = tbl.w[e0 + i];
+    }
+    const int rc = launch_decode_layer(g, route, static_cast<const uint8_t*>(x) + (size_t)p * g.hidden * xb,
+                                       x_dtype, outp, out_dtype, ws, st);
+    if (rc != K3_HIP_OK) return rc;
+  }
+  return K3_HIP_OK;
 }
 
 // ---------------------------------------------------------------- MoE block
@@ -821,7 +869,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
         reinterpret_cast<uintptr_t>(sp.shared_up) | reinterpret_cast<uintptr_t>(sp.shared_down)) &
        15u) == 0;
   if (P >= K3_SPINE_MFMA_MIN_POSITIONS && kind == K3_SPINE_KIND_BF16 && matrices_aligned &&
-      spine_mfma_supported(kind, P, E, H) &&
+      spine_mfma_supported(kind, P, R, H) && spine_mfma_supported(kind, P, S, H) &&
       spine_mfma_supported(kind, P, H, R) && spine_mfma_supported(kind, P, H, S)) {
     auto mm = [&](const void* w, float* y, int rows, int cols, bool acc, const char* step) {
       return from_spine(spine_mfma_gemv(w, b.terms, y, rows, cols, P, acc, st), step);
@@ -829,7 +877,13 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
     auto split = [&](const float* x, int cols) {
       return from_spine(spine_mfma_split(x, P, cols, b.terms, st), "term split");
     };
-    if ((rc = split(hidden, H)) || (rc = mm(sp.router, b.logits, E, H, false, "router")) ||
+    // The router logits stay on the fp32 kernels at every P: each position's
+    // logit is then summed in the same order whatever the batch (the fp32
+    // spine kernels reduce every (row, position) identically), so a hidden row
+    // routes to the same experts in a 1-token decode and in a verify batch.
+    if ((rc = from_spine(spine_gemv(kind, sp.router, sp.router_scales, hidden, b.logits, E, H, P,
+                                    false, st), "router")) ||
+        (rc = split(hidden, H)) ||
         (rc = mm(sp.routed_down, b.routed_in, R, H, false, "routed_down")) ||
         (rc = mm(sp.shared_gate, b.gate, S, H, false, "shared_gate")) ||
         (rc = mm(sp.shared_up, b.up, S, H, false, "shared_up")))
@@ -1339,11 +1393,6 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
   if (!carve_workspace(workspace, workspace_bytes, g, std::max(n_edges, 1), n_positions, &ws))
     return fail(K3_HIP_E_INVALID, "verify: workspace missing, misaligned or too small");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (n_edges == 0) {
-    const size_t bytes = (size_t)n_positions * g.hidden * (out_dtype == K3_DTYPE_BF16 ? 2 : 4);
-    const hipError_t e = hipMemsetAsync(out, 0, bytes, st);
-    return e == hipSuccess ? K3_HIP_OK : hip_fail("verify: zero output", e);
-  }
   EdgeTable tbl;
   memset(&tbl, 0, sizeof(tbl));
   tbl.n_edges = n_edges;
@@ -1355,63 +1404,7 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
     tbl.ptr[i] = edge_experts[i];
     tbl.w[i] = edge_weights[i];
   }
-  // Distinct experts and the most edges any one of them carries (the
-  // matrix-core path takes up to 16 edges, one token column each).
-  int n_unique = 0, max_edges_per_expert = 0;
-  for (int i = 0; i < n_edges; ++i) {
-    bool seen = false;
-    for (int j = 0; j < i && !seen; ++j) seen = tbl.ptr[j] == tbl.ptr[i];
-    if (seen) continue;
-    ++n_unique;
-    int c = 0;
-    for (int j = i; j < n_edges; ++j) c += tbl.ptr[j] == tbl.ptr[i];
-    max_edges_per_expert = std::max(max_edges_per_expert, c);
-  }
-  const int mode = g_verify_mode.load();
-  const bool mfma_ok = verify_mfma_supported(g) && max_edges_per_expert <= 16;
-  if (mode == K3_VERIFY_UNION_MFMA && !mfma_ok)
-    return fail(K3_HIP_E_CAPABILITY,
-                "verify: no matrix-core path (geometry/layout, or an expert with %d > 16 edges)",
-                max_edges_per_expert);
-  const bool mfma = mode == K3_VERIFY_UNION_MFMA ||
-                    (mode == K3_VERIFY_AUTO && n_positions >= 2 && mfma_ok &&
-                     n_unique <= kUnionFraction * n_edges);
-  // Without the matrix-core path, positions that share most of their experts
-  // take the VALU union kernels (each shared expert read once); otherwise one
-  // decode layer per position (about twice the streaming rate of the VALU
-  // union kernels, so they win unless the union is under half the edges).
-  const bool valu = mode == K3_VERIFY_UNION_VALU ||
-                    (mode == K3_VERIFY_AUTO && !mfma && !mfma_ok && 2 * n_unique <= n_edges);
-  if (mfma || valu) {
-    int rc = launch_verify_plan_table(tbl, ws, st);
-    if (rc != K3_HIP_OK) return rc;
-    return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
-                : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
-  }
-  const size_t xb = x_dtype == K3_DTYPE_BF16 ? 2 : 4, ob = out_dtype == K3_DTYPE_BF16 ? 2 : 4;
-  for (int p = 0; p < n_positions; ++p) {
-    const int e0 = position_offsets[p], n = position_offsets[p + 1] - e0;
-    uint8_t* outp = static_cast<uint8_t*>(out) + p * g.hidden * ob;
-    if (n == 0) {  // no routed expert: a zero row
-      const hipError_t e = hipMemsetAsync(outp, 0, g.hidden * ob, st);
-      if (e != hipSuccess) return hip_fail("verify: zero row", e);
-      continue;
-    }
-    if (n > K3_HIP_MAX_TOKEN_EXPERTS)
-      return fail(K3_HIP_E_INVALID, "verify: position %d has %d edges (at most %d)", p, n,
-                  K3_HIP_MAX_TOKEN_EXPERTS);
-    TokenRoute route;
-    memset(&route, 0, sizeof(route));
-    route.n = n;
-    for (int i = 0; i < n; ++i) {
-      route.ptr[i] = tbl.ptr[e0 + i];
-      route.w[i] = tbl.w[e0 + i];
-    }
-    const int rc = launch_decode_layer(g, route, static_cast<const uint8_t*>(x) + p * g.hidden * xb,
-                                       x_dtype, outp, out_dtype, ws, st);
-    if (rc != K3_HIP_OK) return rc;
-  }
-  return K3_HIP_OK;
+  return verify_table(g, tbl, x, x_dtype, out, out_dtype, ws, st);
 }
 
 int k3_hip_set_fused_decode(int enabled) { return set_fused_decode(enabled); }

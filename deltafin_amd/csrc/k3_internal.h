@@ -151,6 +151,9 @@ int launch_synth_bank(const Geo& g, uint8_t* bank, uint64_t stride,
                       int lo, int hi, hipStream_t stream);
 int launch_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed,
                         uint64_t stream_id, hipStream_t stream);
+// Zero `bytes` (a multiple of 4) at a 4-byte aligned device pointer with a
+// kernel (graph-capturable, unlike a memset node).
+int launch_zero(void* p, uint64_t bytes, hipStream_t stream);
 
 int device_cu_count();
 // Whether one workgroup of `kernel` at `block` threads with `dynamic_lds`

@@ -1587,6 +1587,15 @@ __global__ void k_combine_positions(const Workspace ws, int hidden, int n_positi
   store_out(out + i, acc);
 }
 
+// Zero n 32-bit words (rows of positions with no routed expert).  A kernel
+// rather than hipMemsetAsync, so a caller capturing the call into a HIP graph
+// records a kernel node.
+__global__ void k_zero_words(uint32_t* __restrict__ p, uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
 // ======================================================================
 // synthetic inputs
 // ======================================================================
@@ -2132,6 +2141,18 @@ int launch_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed, uint64_
   launch_timed(tl, k_synth_normal, dim3((unsigned)blocks), dim3(256), 0, st, out, dtype, n, seed,
                      stream_id);
   return launched(tl, "synth normal launch");
+}
+
+int launch_zero(void* p, uint64_t bytes, hipStream_t st) {
+  if (!p || bytes % 4 != 0 || ((uintptr_t)p & 3u) != 0)
+    return fail(K3_HIP_E_INVALID, "zero fill: needs a 4-byte aligned pointer and size");
+  if (bytes == 0) return K3_HIP_OK;
+  const uint64_t n = bytes / 4;
+  const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 1024);
+  TimedLaunch tl(KC_COMBINE, st);
+  launch_timed(tl, k_zero_words, dim3((unsigned)blocks), dim3(256), 0, st,
+               static_cast<uint32_t*>(p), n);
+  return launched(tl, "zero fill launch");
 }
 
 }  // namespace k3

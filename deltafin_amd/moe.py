@@ -297,14 +297,54 @@ class ExpertCache:
               "k3_hip_cache_resolve")
         return [int(out[i]) for i in range(n)]
 
-    def ready_subset(self, plan_id: int, ids: Sequence[int]) -> list[int | None]:
+    def ready_subset(self, plan_id: int, ids: Sequence[int],
+                     stream: int | None = None) -> list[int | None]:
         n = len(ids)
         a = (C.c_uint16 * n)(*ids)
         out = (C.c_void_p * n)()
-        rc = self._lib.k3_hip_cache_ready_subset(self.handle, plan_id, a, n, out)
+        rc = self._lib.k3_hip_cache_ready_subset(self.handle, plan_id, a, n, out,
+                                                 stream if stream is not None else stream_handle())
         if rc < 0:
             raise K3HipError(rc, "k3_hip_cache_ready_subset")
         return [int(out[i]) if out[i] else None for i in range(n)]
+
+    def configure(self, automatic: bool, capacity: int = 0,
+                  reserve_kind: int = _lib.K3_CACHE_RESERVE_AUTO, reserve_value: int = 0) -> None:
+        """CudaMoeExpertCache::configure (provider_cuda_moe.h:97-98); before the first plan."""
+        p = _lib.K3HipCachePolicyV1(1, C.sizeof(_lib.K3HipCachePolicyV1), int(automatic),
+                                    reserve_kind, capacity, reserve_value)
+        check(self._lib.k3_hip_cache_configure(self.handle, C.byref(p)), "k3_hip_cache_configure")
+
+    def budget(self) -> dict[str, int]:
+        """The budget (measured: False before the first plan and after a
+        recovery, until the next plan measures it again)."""
+        s = (C.c_longlong * 5)()
+        rc = self._lib.k3_hip_cache_budget(self.handle, s)
+        if rc < 0:
+            raise K3HipError(rc, "k3_hip_cache_budget")
+        return dict(zip(["capacity", "allocated_slots", "free_bytes", "reserve_bytes",
+                         "rebuilds_left"], list(s)), measured=rc == 1)
+
+    def materialize_plan(self, plan_id: int, max_hits: int) -> dict[int, np.ndarray]:
+        """Host copies of the plan's pinned hits (materialize_plan_for_cpu,
+        provider_cuda_moe.cpp:1170-1196): {expert id: span bytes}."""
+        ids = (C.c_uint16 * max(max_hits, 1))()
+        host = np.empty(max(max_hits, 1) * self.span, dtype=np.uint8)
+        n = C.c_int()
+        check(self._lib.k3_hip_cache_materialize_plan(self.handle, plan_id, ids, max_hits,
+                                                      host.ctypes.data, host.nbytes, C.byref(n)),
+              "k3_hip_cache_materialize_plan")
+        return {int(ids[i]): host[i * self.span:(i + 1) * self.span] for i in range(n.value)}
+
+    def fail_allocations(self, count: int) -> None:
+        """Test hook: the next `count` device allocations report out-of-memory."""
+        check(self._lib.k3_hip_cache_fail_allocations(self.handle, count),
+              "k3_hip_cache_fail_allocations")
+
+    def state(self) -> tuple[int, str]:
+        buf = C.create_string_buffer(512)
+        rc = self._lib.k3_hip_cache_state(self.handle, buf, 512)
+        return rc, buf.value.decode(errors="replace")
 
     def release(self, plan_id: int) -> None:
         self._lib.k3_hip_cache_release(self.handle, plan_id)

@@ -121,12 +121,43 @@ class MoeSpine:
         self.shared_gate, self.shared_up, self.shared_down = shared_gate, shared_up, shared_down
         self.scales = dict(scales or {})
         self.top_k = top_k
+        if router.dim() != 2 or routed_down.dim() != 2 or shared_gate.dim() != 2:
+            raise ValueError("router, routed_down and shared_gate must be 2-D [rows, columns]")
         self.hidden = router.shape[1]
         self.routed_hidden = routed_down.shape[0]
         self.shared_intermediate = shared_gate.shape[0]
         self.experts = router.shape[0]
         if kind == "int8" and set(self.scales) != set(self.MATRICES):
             raise ValueError("row-int8 spines need a scale vector for every matrix")
+        # Every shape, element type and layout is checked here, before a
+        # pointer reaches the library (a wrong one would be an out-of-bounds
+        # device read).
+        H, R, S, E = self.hidden, self.routed_hidden, self.shared_intermediate, self.experts
+        want = {"router": (E, H), "routed_down": (R, H), "routed_up": (H, R),
+                "shared_gate": (S, H), "shared_up": (S, H), "shared_down": (H, S)}
+        mdt = (torch.int16, torch.uint16, torch.bfloat16) if kind == "bf16" else (torch.int8,)
+        for name, shape in want.items():
+            t = getattr(self, name)
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{name} must be {list(shape)}, got {list(t.shape)}")
+        if tuple(router_bias.shape) != (E,):
+            raise ValueError(f"router_bias must hold {E} values")
+        if tuple(routed_norm.shape) != (R,):
+            raise ValueError(f"routed_norm must hold {R} values")
+        for name, shape in want.items():
+            t = getattr(self, name)
+            if t.dtype not in mdt or t.device.type != "cuda" or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous device tensor of "
+                                 f"{'BF16 bits' if kind == 'bf16' else 'int8'}")
+            if kind == "int8":
+                sc = self.scales[name]
+                if tuple(sc.shape) != (shape[0],):
+                    raise ValueError(f"{name} scales must hold {shape[0]} values")
+                _dense(sc, torch.float32, f"{name} scales")
+        _dense(router_bias, torch.float32, "router_bias")
+        _dense(routed_norm, torch.float32, "routed_norm")
+        if not 1 <= top_k <= min(E, 32):
+            raise ValueError(f"top_k must be in [1, min(experts, 32)], got {top_k}")
 
     def descriptor(self) -> _lib.K3HipMoeSpineV1:
         d = _lib.K3HipMoeSpineV1()
@@ -160,6 +191,16 @@ def moe_block(spine: MoeSpine, g, bank: torch.Tensor, stride: int, hidden: torch
     h2 = hidden if hidden.dim() == 2 else hidden.view(1, -1)
     _dense(h2, torch.float32, "hidden")
     P = h2.shape[0]
+    if h2.shape[1] != spine.hidden:
+        raise ValueError(f"hidden rows must hold {spine.hidden} values, got {h2.shape[1]}")
+    if g.hidden != spine.routed_hidden:
+        raise ValueError(f"the expert geometry's hidden ({g.hidden}) must equal the spine's "
+                         f"routed width ({spine.routed_hidden})")
+    if bank.dtype != torch.uint8 or bank.device.type != "cuda" or not bank.is_contiguous():
+        raise ValueError("bank must be a contiguous uint8 device tensor")
+    if stride < g.expert_span or bank.numel() < (spine.experts - 1) * stride + g.expert_span:
+        raise ValueError(f"bank holds {bank.numel()} bytes; {spine.experts} experts at stride "
+                         f"{stride} need {(spine.experts - 1) * stride + g.expert_span}")
     if workspace is None:
         workspace = moe_block_workspace(spine, g, P)
     if out is None:

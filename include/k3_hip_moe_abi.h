@@ -292,13 +292,45 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* g,
 
 typedef struct K3HipCache K3HipCache;
 
-/* capacity_experts slots of span_bytes each in HBM; n_layers strata.  staging
- * slots = pinned host staging buffers used for pageable sources.
+/* A cache over n_layers strata of span_bytes experts.  capacity_experts = 0
+ * sizes it from the budget alone (automatic capacity); > 0 requests that many
+ * slots, clamped to the budget (CudaMoeCachePolicy, provider_cuda_moe.h:16-28;
+ * at most K3_HIP_CACHE_MAX_EXPERTS).  HBM is taken in segments of slots as
+ * the cache fills, after the budget is measured at the first plan.
+ * staging_slots = pinned host staging buffers used for pageable sources.
  * Returns NULL on failure (see k3_hip_last_error). */
+#define K3_HIP_CACHE_MAX_EXPERTS 65536
 K3HipCache* k3_hip_cache_create(int device, uint64_t span_bytes,
                                 int capacity_experts, int n_layers,
                                 int staging_slots);
 void k3_hip_cache_destroy(K3HipCache* cache);
+
+/* Capacity policy (CudaMoeCachePolicy, provider_cuda_moe.h:16-28).  The
+ * budget is free device memory at the first plan minus a reserve:
+ * K3_CACHE_RESERVE_AUTO max(2 GiB, free / 5), _BYTES reserve_value bytes,
+ * _RATIO_PPM free x reserve_value / 1e6 (provider_cuda_moe.cpp:668-705). */
+enum { K3_CACHE_RESERVE_AUTO = 0, K3_CACHE_RESERVE_BYTES = 1,
+       K3_CACHE_RESERVE_RATIO_PPM = 2 };
+typedef struct K3HipCachePolicyV1 {
+  uint32_t abi_version;        /* 1 */
+  uint32_t struct_bytes;       /* sizeof(K3HipCachePolicyV1) == 32 */
+  uint32_t automatic_capacity; /* 1: what the budget holds; 0: capacity_experts */
+  uint32_t reserve_kind;       /* K3_CACHE_RESERVE_* */
+  uint64_t capacity_experts;   /* 0 when automatic, else <= K3_HIP_CACHE_MAX_EXPERTS */
+  uint64_t reserve_value;      /* 0 for AUTO; bytes; or ppm (<= 1,000,000) */
+} K3HipCachePolicyV1;
+#ifdef __cplusplus
+static_assert(sizeof(K3HipCachePolicyV1) == 32, "cache policy ABI drift");
+#endif
+/* Replaces CudaMoeExpertCache::configure (provider_cuda_moe.h:97-98,
+ * validate_cache_policy provider_cuda_moe.cpp:60-74): K3_HIP_E_INVALID for a
+ * policy out of bounds, or once the policy is frozen (from the first plan). */
+int k3_hip_cache_configure(K3HipCache* cache, const K3HipCachePolicyV1* policy);
+/* The budget (CudaMoeResidencyPlanReport::capacity_experts,
+ * provider_cuda_moe.h:30-34): five = [capacity in experts (-1 before the
+ * first plan), slots allocated, free bytes measured, reserve bytes, rebuilds
+ * left].  Returns 1 once measured, 0 before, or K3_HIP_E_INVALID. */
+int k3_hip_cache_budget(const K3HipCache* cache, long long* five);
 /* Plan (provider_cuda_moe.cpp:963-1008): snapshot hits for `ids` of `layer`
  * (canonical ascending, unique), LRU-promoting them; misses are written to
  * missing_ids (capacity n) and *n_missing.  plan_id must be non-zero and not
@@ -309,7 +341,14 @@ int k3_hip_cache_plan(K3HipCache* cache, uint64_t plan_id, int layer,
 /* Admit the plan's misses from host memory: sources[i] holds the span of
  * missing_ids[i] (pinned memory is copied directly, pageable memory through
  * a staging slot).  Copies run on the cache's side stream; per-expert ready
- * events are recorded.  Non-blocking for pinned sources. */
+ * events are recorded.  Non-blocking for pinned sources.  All or nothing:
+ * K3_HIP_E_ALLOC when every slot is pinned by live plans, or on a
+ * recoverable device allocation failure (the reference's
+ * CudaMoeRecoverableError, provider_cuda_moe.cpp:630-653: the fetch is
+ * undone, unpinned entries are dropped and the budget is re-measured at the
+ * next plan; after two such rebuilds the cache disables itself).  The plan
+ * stays live with its hits pinned: the caller takes its CPU path through
+ * k3_hip_cache_materialize_plan, then releases the plan. */
 int k3_hip_cache_fetch(K3HipCache* cache, uint64_t plan_id,
                        const uint8_t* const* sources, int n_sources);
 /* Device pointers of the plan's experts in `ids` order, and make `stream`
@@ -318,12 +357,30 @@ int k3_hip_cache_resolve(K3HipCache* cache, uint64_t plan_id,
                          const uint16_t* ids, int n,
                          const uint8_t** device_spans, void* stream);
 /* Device pointers for the subset of `ids` already resident and ready (no
- * wait); others get NULL.  Returns the number resident. */
+ * wait); others get NULL.  `stream` is where the caller will read them:
+ * release orders the slots' reuse after the work queued there.  Returns the
+ * number resident. */
 int k3_hip_cache_ready_subset(K3HipCache* cache, uint64_t plan_id,
                               const uint16_t* ids, int n,
-                              const uint8_t** device_spans);
-/* Finish or cancel a plan (provider_cuda_moe.cpp:1166-1168). */
+                              const uint8_t** device_spans, void* stream);
+/* Finish or cancel a plan (provider_cuda_moe.cpp:1166-1168).  Slots the plan
+ * pinned are reused only after the work queued so far on every stream the
+ * plan resolved on (resolve / ready_subset). */
 void k3_hip_cache_release(K3HipCache* cache, uint64_t plan_id);
+/* Bounded device-to-host copy of the plan's pinned hits only, for the
+ * caller's exact CPU reconstruction of the tile
+ * (CudaMoeExpertCache::materialize_plan_for_cpu, provider_cuda_moe.cpp:1170-1196;
+ * used by provider_moe.cpp:1117-1206): ids_out receives their expert ids in
+ * canonical order, host_out their spans back to back, *n_out their count.
+ * Works on a disabled cache while the plan is live. */
+int k3_hip_cache_materialize_plan(K3HipCache* cache, uint64_t plan_id,
+                                  uint16_t* ids_out, int ids_capacity,
+                                  uint8_t* host_out, uint64_t host_bytes,
+                                  int* n_out);
+/* Test hook, no reference counterpart: the next `count` device allocations of
+ * the cache report out-of-memory without reaching the allocator, so the
+ * recoverable path can be exercised on demand. */
+int k3_hip_cache_fail_allocations(K3HipCache* cache, int count);
 /* [hits, misses, evictions, resident, capacity, bytes_uploaded]. */
 void k3_hip_cache_stats(const K3HipCache* cache, long long* six);
 /* Qualification and fail-closed state (CudaMoeExpertCache::available / detail,

@@ -137,16 +137,29 @@ def _linear(kind: str, m: dict, name: str, x):
     return spine_int8_f64(m[name], m[name + "_scales"], x)
 
 
-def moe_block_f64(kind: str, m: dict, expert_span, hidden, inter: int, k: int):
+def _linear_abs(kind: str, m: dict, name: str, x):
+    """sum_j |W[i, j] x[j]|: the size of the terms each output sums."""
+    ax = np.abs(np.asarray(x, np.float64))
+    if kind == "bf16":
+        return ax @ np.abs(bf16_to_f32(m[name]).astype(np.float64)).T
+    dots = ax @ np.abs(np.asarray(m[name], np.int8).astype(np.float64)).T
+    return dots * np.abs(np.asarray(m[name + "_scales"], np.float32).astype(np.float64))[None, :]
+
+
+def moe_block_f64(kind: str, m: dict, expert_span, hidden, inter: int, k: int,
+                  with_mag: bool = False):
     """The K3 block for hidden [P, H]; m holds the spine as numpy arrays
     (router, router_bias, routed_down, routed_norm, routed_up, shared_gate,
     shared_up, shared_down, and *_scales for kind "int8"); expert_span(id)
     returns that expert's raw-v1 bytes.  Returns (out [P, H], ids [P, k],
-    weights [P, k], routed [P, R]) in float64."""
+    weights [P, k], routed [P, R]) in float64; with_mag also the size of the
+    terms each output sums, [P, H]: sum_j |routed_up[i, j] norm_j| +
+    sum_j |shared_down[i, j] h_j| (the scale of a condition-aware bar,
+    oracle.cond_rel_err with n = R + shared)."""
     import oracle
     x = np.atleast_2d(np.asarray(hidden, np.float64))
     R = m["routed_down"].shape[0]
-    outs, all_ids, all_w, routed_all = [], [], [], []
+    outs, all_ids, all_w, routed_all, mags = [], [], [], [], []
     for p in range(x.shape[0]):
         xp = x[p:p + 1]
         logits = _linear(kind, m, "router", xp)[0]
@@ -162,7 +175,11 @@ def moe_block_f64(kind: str, m: dict, expert_span, hidden, inter: int, k: int):
         all_ids.append(ids)
         all_w.append(w)
         routed_all.append(routed)
-    return np.array(outs), np.array(all_ids), np.array(all_w), np.array(routed_all)
+        if with_mag:
+            mags.append(_linear_abs(kind, m, "routed_up", norm)[0] +
+                        _linear_abs(kind, m, "shared_down", h)[0])
+    res = (np.array(outs), np.array(all_ids), np.array(all_w), np.array(routed_all))
+    return res + (np.array(mags),) if with_mag else res
 
 
 # The reference's tiny MoE geometry (kTestGeometry, provider_moe_test.cpp:50):

@@ -252,3 +252,197 @@ def test_cache_poison_fails_closed(gpu):
         assert lib.k3_hip_cache_read_back(cache, 0, 5, back.ctypes.data, span) != 0
     finally:
         lib.k3_hip_cache_destroy(cache)
+
+
+# ------------------------------------------------------------ budget and recovery
+def _geo_small():
+    from deltafin_amd import moe
+    return moe.geometry(512, 256, moe.K3_ACT_SILU)
+
+
+def _host_experts(g, n, seed):
+    """Pinned host spans of n synthetic experts (oracle generator) + numpy views."""
+    spans = [oracle.synth_expert(seed, e, g.hidden, g.intermediate) for e in range(n)]
+    hosts = []
+    for s in spans:
+        h = _pinned(g.expert_span)
+        h.numpy()[:] = s
+        hosts.append(h)
+    return spans, hosts
+
+
+def test_cache_budget_policy(gpu):
+    """CudaMoeCachePolicy (provider_cuda_moe.h:16-28): bounds checked as
+    validate_cache_policy (:60-74); the budget is free memory at the first
+    plan minus the reserve (:668-705); the policy is frozen from then on."""
+    from deltafin_amd import _lib, moe
+    g = _geo_small()
+    say("cache budget and policy")
+    cache = moe.ExpertCache(g.expert_span, 0, 1, staging_slots=0)
+    try:
+        with pytest.raises(_lib.K3HipError):
+            cache.configure(True, capacity=5)        # automatic with a count
+        with pytest.raises(_lib.K3HipError):
+            cache.configure(False, capacity=_lib.K3_HIP_CACHE_MAX_EXPERTS + 1)
+        with pytest.raises(_lib.K3HipError):
+            cache.configure(True, reserve_kind=_lib.K3_CACHE_RESERVE_RATIO_PPM,
+                            reserve_value=1_000_001)
+        reserve = 1 << 30
+        cache.configure(True, reserve_kind=_lib.K3_CACHE_RESERVE_BYTES, reserve_value=reserve)
+        assert not cache.budget()["measured"]
+        _, hosts = _host_experts(g, 2, 3)
+        assert cache.plan(1, 0, [0, 1]) == [0, 1]
+        b = cache.budget()
+        slot = (g.expert_span + 4095) & ~4095
+        want = min(_lib.K3_HIP_CACHE_MAX_EXPERTS, (b["free_bytes"] - reserve) // slot)
+        assert b["reserve_bytes"] == reserve and b["capacity"] == want, b
+        assert b["allocated_slots"] == 0 and b["rebuilds_left"] == 2
+        cache.fetch(1, [h.data_ptr() for h in hosts])
+        assert cache.budget()["allocated_slots"] == 32  # one segment
+        cache.release(1)
+        with pytest.raises(_lib.K3HipError):
+            cache.configure(True)  # frozen after first use
+        assert "frozen" in _lib.last_error()
+    finally:
+        cache.close()
+
+
+def test_cache_recoverable_allocation_failure(gpu):
+    """A device allocation failure while admitting misses is recoverable
+    (provider_cuda_moe.cpp:545-567, :630-653): the fetch returns
+    K3_HIP_E_ALLOC, the plan's hits stay pinned and are materialized to the
+    host (materialize_plan_for_cpu, :1170-1196) for the caller's exact CPU
+    reconstruction of the tile (provider_moe.cpp:1117-1206) -- checked here
+    against the device layer on the same experts -- and the cache re-measures
+    its budget and carries on; after two rebuilds the next failure disables
+    it (its callers take their CPU path)."""
+    import torch
+    from deltafin_amd import _lib, moe
+    g = _geo_small()
+    say("cache recoverable allocation failure")
+    n = 36
+    spans, hosts = _host_experts(g, n, 11)
+    cache = moe.ExpertCache(g.expert_span, 40, 1, staging_slots=0)  # segments of 32 + 8
+    try:
+        # Fill the first segment with experts 0..31.
+        for p in range(4):
+            ids = list(range(8 * p, 8 * p + 8))
+            miss = cache.plan(1 + p, 0, ids)
+            cache.fetch(1 + p, [hosts[e].data_ptr() for e in miss])
+            cache.release(1 + p)
+        torch.cuda.synchronize()
+        assert cache.budget()["allocated_slots"] == 32
+        # Plan 10: hits 3 and 7, misses 33 and 34, which need the second
+        # segment: its allocation is refused.
+        ids = [3, 7, 33, 34]
+        miss = cache.plan(10, 0, ids)
+        assert miss == [33, 34]
+        cache.fail_allocations(1)
+        rc = gpu.k3_hip_cache_fetch(cache.handle, 10,
+                                    (C.c_void_p * 2)(*[hosts[e].data_ptr() for e in miss]), 2)
+        assert rc == _lib.K3_HIP_E_ALLOC and "recoverable" in _lib.last_error()
+        st, why = cache.state()
+        assert st == 1, why
+        b = cache.budget()
+        assert b["rebuilds_left"] == 1 and not b["measured"]  # measured again at the next plan
+        # The CPU path: hits from the device, misses from the caller's bytes.
+        hits = cache.materialize_plan(10, 4)
+        assert sorted(hits) == [3, 7]
+        for e, b in hits.items():
+            assert np.array_equal(b, spans[e])
+        w = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+        x = np.random.default_rng(5).standard_normal(g.hidden).astype(np.float32)
+        cpu_spans = [hits[e] if e in hits else spans[e] for e in ids]
+        ref, mag = oracle.moe_layer_f64(cpu_spans, w.astype(np.float64), g.hidden,
+                                        g.intermediate, g.activation, x)
+        dev = [torch.from_numpy(spans[e]).cuda() for e in ids]
+        ws = moe.workspace(g, 4)
+        out = moe.moe_layer(g, dev, w.tolist(), torch.from_numpy(x).cuda(), ws)
+        torch.cuda.synchronize()
+        assert oracle.cond_rel_err(out.cpu().numpy(), ref, mag, g.intermediate) <= 1e-3
+        cache.release(10)
+        # Unpinned entries were dropped; the cache carries on after re-measuring.
+        assert cache.stats()["resident"] == 2
+        miss = cache.plan(11, 0, [3, 33, 35])
+        assert miss == [33, 35]
+        cache.fetch(11, [hosts[e].data_ptr() for e in miss])
+        got = cache.resolve(11, [3, 33, 35])
+        torch.cuda.synchronize()
+        cache.release(11)
+        assert cache.budget()["measured"] and cache.read_back(0, 35).tobytes() == spans[35].tobytes()
+        assert len(got) == 3
+        # Two more failures: the second rebuild, then the cache disables itself.
+        statuses = []
+        for k in range(2):
+            cache.fail_allocations(100)
+            for p in range(40):
+                pid = 100 + 50 * k + p
+                miss = cache.plan(pid, 0, [p])
+                srcs = (C.c_void_p * max(len(miss), 1))(*[hosts[e % n].data_ptr() for e in miss])
+                rc = gpu.k3_hip_cache_fetch(cache.handle, pid, srcs, len(miss))
+                cache.release(pid)
+                if rc != 0:
+                    statuses.append((rc, _lib.last_error()))
+                    break
+        assert [s[0] for s in statuses] == [_lib.K3_HIP_E_ALLOC] * 2
+        assert "disabled" in statuses[1][1], statuses
+        st, why = cache.state()
+        assert st == _lib.K3_HIP_E_CAPABILITY and "rebuilds" in why, why
+        missing = (C.c_uint16 * 1)()
+        nm = C.c_int()
+        assert gpu.k3_hip_cache_plan(cache.handle, 999, 0, _ids([1]), 1, missing,
+                                     C.byref(nm)) == _lib.K3_HIP_E_CAPABILITY
+    finally:
+        cache.close()
+
+
+def test_cache_release_orders_reuse_on_every_stream(gpu):
+    """Two live plans hold the same slot and read it on two different streams
+    (resolve on one, ready_subset on the other); after both are released a
+    fetch evicts it.  The copy into the slot must wait for both streams' work:
+    both layers' outputs equal the same layer on a private copy of the
+    expert."""
+    import torch
+    from deltafin_amd import _lib, moe
+    g = _geo_small()
+    say("cache slot reuse after two streams")
+    spans, hosts = _host_experts(g, 3, 21)
+    cache = moe.ExpertCache(g.expert_span, 1, 1, staging_slots=0)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    try:
+        x = torch.from_numpy(np.random.default_rng(6).standard_normal(g.hidden)
+                             .astype(np.float32)).cuda()
+        ws1, ws2 = moe.workspace(g, 1), moe.workspace(g, 1)
+        private = torch.from_numpy(spans[0]).cuda()
+        want = moe.moe_layer(g, [private], [1.0], x, moe.workspace(g, 1))
+        torch.cuda.synchronize()
+        miss = cache.plan(1, 0, [0])
+        cache.fetch(1, [hosts[e].data_ptr() for e in miss])
+        # Wait (on the host) for the upload, so ready_subset sees it below.
+        cache.resolve(1, [0])
+        torch.cuda.current_stream().synchronize()
+        outs = []
+        with torch.cuda.stream(s1):
+            sp = cache.resolve(1, [0], stream=moe.stream_handle(s1))
+            for _ in range(20):
+                outs.append(moe.moe_layer(g, sp, [1.0], x, ws1))
+        assert cache.plan(2, 0, [0]) == []
+        with torch.cuda.stream(s2):
+            sp2 = cache.ready_subset(2, [0], stream=moe.stream_handle(s2))
+            assert sp2 == sp
+            for _ in range(20):
+                outs.append(moe.moe_layer(g, sp2, [1.0], x, ws2))
+        # Both plans released with their kernels still queued on s1 and s2.
+        cache.release(1)
+        cache.release(2)
+        # Evict the slot: expert 1's bytes land where expert 0 was read.
+        miss = cache.plan(3, 0, [1])
+        assert miss == [1]
+        cache.fetch(3, [hosts[1].data_ptr()])
+        cache.release(3)
+        torch.cuda.synchronize()
+        ref = want.cpu().numpy().view(np.uint32)
+        for o in outs:
+            assert np.array_equal(o.cpu().numpy().view(np.uint32), ref)
+    finally:
+        cache.close()

@@ -242,3 +242,62 @@ def test_block_oracle_on_reference_tiny_fixture(positions):
     assert out.shape == (positions, 32) and ids.shape == (positions, 16)
     assert np.max(np.abs(out - want)) <= 1e-10 * max(1.0, np.max(np.abs(want)))
     assert sorted(ids[0].tolist()) == list(range(16))  # top 16 of 16: every expert
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_block_oracle_magnitude(kind):
+    """The per-element scale of the block bar: the magnitude of the terms the
+    last two projections sum equals the same projections over |W| and |input|
+    (pinned on the reference's tiny fixture with its own row-int8 spine, and a
+    random BF16 one), and bounds the output from above."""
+    if kind == "int8":
+        m = S.tiny_spine()
+    else:
+        rng = np.random.default_rng(3)
+        m = {}
+        for name, (rows, cols) in {"router": (16, 32), "routed_down": (32, 32),
+                                   "routed_up": (32, 32), "shared_gate": (64, 32),
+                                   "shared_up": (64, 32), "shared_down": (32, 64)}.items():
+            v = rng.standard_normal((rows, cols), dtype=np.float32)
+            m[name] = (v.view(np.uint32) >> 16).astype(np.uint16)
+        m["router_bias"] = np.zeros(16, np.float32)
+        m["routed_norm"] = np.ones(32, np.float32)
+    hidden = S.tiny_hidden(3)
+    out, ids, w, routed, mag = S.moe_block_f64(kind, m, S.tiny_expert_span, hidden, 32, 16,
+                                               with_mag=True)
+    assert mag.shape == out.shape and np.all(mag >= np.abs(out) - 1e-12 * np.abs(out).max())
+    for p in range(3):
+        norm = S.rms_norm_f64(routed[p][None, :], m["routed_norm"], S.RMS_EPS)
+        h = S.situ_f64(S._linear(kind, m, "shared_gate", hidden[p:p + 1]),
+                       S._linear(kind, m, "shared_up", hidden[p:p + 1]))
+        if kind == "bf16":
+            dense = {n: np.abs(S.bf16_to_f32(m[n]).astype(np.float64)) for n in ("routed_up", "shared_down")}
+        else:
+            dense = {n: np.abs(m[n].astype(np.float64)) * np.abs(m[n + "_scales"].astype(np.float64))[:, None]
+                     for n in ("routed_up", "shared_down")}
+        want = dense["routed_up"] @ np.abs(norm[0]) + dense["shared_down"] @ np.abs(h[0])
+        assert np.allclose(mag[p], want, rtol=1e-12, atol=0)
+
+
+def test_moe_spine_validation_on_host():
+    """MoeSpine checks every shape before any pointer reaches the library."""
+    import torch
+    from deltafin_amd import spine
+    H, R, Sh, E = 64, 32, 48, 8
+
+    def bf(r, c):
+        return torch.zeros((r, c), dtype=torch.int16)
+    args = dict(router=bf(E, H), router_bias=torch.zeros(E), routed_down=bf(R, H),
+                routed_norm=torch.ones(R), routed_up=bf(H, R), shared_gate=bf(Sh, H),
+                shared_up=bf(Sh, H), shared_down=bf(H, Sh))
+    bad = dict(args, routed_up=bf(H, R + 1))
+    with pytest.raises(ValueError, match="routed_up must be"):
+        spine.MoeSpine("bf16", **bad)
+    bad = dict(args, router_bias=torch.zeros(E + 1))
+    with pytest.raises(ValueError, match="router_bias"):
+        spine.MoeSpine("bf16", **bad)
+    with pytest.raises(ValueError, match="device tensor"):
+        spine.MoeSpine("bf16", **args)  # host tensors: refused, not passed on
+    bad = dict(args, router=torch.zeros((E, H), dtype=torch.int8))
+    with pytest.raises(ValueError):
+        spine.MoeSpine("bf16", **bad)
