@@ -148,51 +148,6 @@ __device__ __forceinline__ float weight_of(const RouteRegs& rr, int e) {
 }
 
 // ======================================================================
-// single-activation GEMV: one wave per kRows rows, x slice in registers
-// ======================================================================
-template <typename XT, typename OT, int CPL, int kRows>
-__global__ __launch_bounds__(256) void k_gemv1(const uint8_t* __restrict__ packed,
-                                               const uint8_t* __restrict__ scales,
-                                               const XT* __restrict__ x,
-                                               OT* __restrict__ out, int rows, int cols) {
-  const int lane = threadIdx.x & 63;
-  const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kRows;
-  if (r0 >= rows) return;
-  const int G = cols >> 5;
-  const size_t cp = (size_t)cols >> 1;
-
-  XChunk<XT> xs[CPL];
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const int chunk = lane + 64 * c;
-    if (chunk < G) xs[c].load(x, chunk);
-  }
-  float acc[kRows];
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    float a = 0.0f;
-    if (r0 + r < rows) {
-      const uint8_t* pr = packed + (size_t)(r0 + r) * cp;
-      const uint8_t* sr = scales + (size_t)(r0 + r) * G;
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        const int chunk = lane + 64 * c;
-        if (chunk < G) {
-          const u32x4 w = load_chunk(pr + (size_t)chunk * 16);
-          a = fmaf(xs[c].dot(w), e8m0_scale(sr[chunk]), a);
-        }
-      }
-    }
-    acc[r] = a;
-  }
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const float v = wave_sum(acc[r]);
-    if (lane == 0 && r0 + r < rows) store_out(out + r0 + r, v);
-  }
-}
-
-// ======================================================================
 // multi-activation GEMV: x rows staged in LDS, each weight chunk decoded once
 // and applied to every staged activation
 // ======================================================================
@@ -289,6 +244,62 @@ __device__ __forceinline__ void load_x_chunk<float>(XChunk<float>& xc, const flo
   xc.load(x, cs.cc);
 #pragma unroll
   for (int i = 0; i < 32; ++i) xc.v[i] = cs.valid ? xc.v[i] : 0.0f;
+}
+
+// ======================================================================
+// single-activation GEMV (k3_hip_mxfp4_gemv at one batch): the column split
+// above over units of kR rows.  A workgroup holds 4 / S row groups of S waves;
+// each lane keeps its one activation chunk in registers, loads the chunk and
+// scale byte of all kR rows of its unit at once, and a butterfly reduces the
+// kR partials across the wave; the S wave partials meet in LDS.  Every unit
+// is one round of loads, so a 2048 x 7168 matrix (256 units of 8 rows) is one
+// wave of loads over the whole chip.
+// ======================================================================
+template <typename XT, typename OT, int kR>
+__global__ __launch_bounds__(256) void k_gemv_cs(const uint8_t* __restrict__ packed,
+                                                 const uint8_t* __restrict__ scales,
+                                                 const XT* __restrict__ x, OT* __restrict__ out,
+                                                 int rows, int cols, int S) {
+  constexpr int L = log2c<kR>();
+  __shared__ float red[4][kR];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int G = cols >> 5;
+  const int groups = 4 / S;
+  const int grp = wave / S;
+  const int gw = wave - grp * S;
+  const bool active = grp < groups;  // S = 3 leaves one wave idle
+  const ColSplit cs = col_split(G, S, active ? gw : 0, lane);
+  XChunk<XT> xc;
+  load_x_chunk<XT>(xc, x, cs);
+  const size_t cp = (size_t)cols >> 1;
+  const int n_units = (rows + kR - 1) / kR;
+  const int per_round = (int)gridDim.x * groups;
+  const int iters = (n_units + per_round - 1) / per_round;  // the same in every workgroup
+  for (int it = 0; it < iters; ++it) {
+    const int u = (it * (int)gridDim.x + (int)blockIdx.x) * groups + grp;
+    const int r0 = min(u, n_units - 1) * kR;  // a unit past the end repeats the last one's loads
+    u32x4 w[kR];
+    uint32_t sc[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      const int row = min(r0 + r, rows - 1);
+      w[r] = load_chunk(packed + (size_t)row * cp + (size_t)cs.cc * 16);
+      sc[r] = load_scale(scales + (size_t)row * G + cs.cc);
+    }
+    float v[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) v[r] = xc.dot(w[r]) * e8m0_scale(sc[r]);
+    wave_reduce_multi<kR>(v, lane);
+    if ((lane & ((1 << (6 - L)) - 1)) == 0) red[wave][lane >> (6 - L)] = v[0];
+    __syncthreads();
+    if (active && gw == 0 && lane < kR && u < n_units && r0 + lane < rows) {
+      float t = red[grp * S][lane];
+      for (int w2 = 1; w2 < S; ++w2) t += red[grp * S + w2][lane];
+      store_out(out + r0 + lane, t);
+    }
+    __syncthreads();
+  }
 }
 
 
@@ -423,7 +434,8 @@ __device__ __forceinline__ uint32_t route_bases(const RouteRegs& rr, int n, int 
 }
 
 __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
-                           uint64_t* keys, int* sel, float* wsel);
+                           uint64_t* keys, int* sel, float* wsel, float pre = 0.0f,
+                           bool have_pre = false);
 
 // The route as every wave of the workgroup holds it (lane e: expert e's span
 // and weight).  Router mode: the workgroup ranks the logits itself (no
@@ -562,13 +574,18 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
                             : GluGather{0, 0};
   // cw (scale4-v2: cw / 2): bpermute bytes per row
   const int row_step = (((g.hidden >> 5) + S - 1) / S) >> (kS4 ? 1 : 0);
+  // Router mode: the logits are requested before the activation chunk, so
+  // the ranking below waits for them alone.
+  const bool pre = route.logits && route.n_bank <= (int)blockDim.x;
+  float logit = 0.0f;
+  if (pre && (int)threadIdx.x < route.n_bank) logit = route.logits[threadIdx.x];
   XChunk<XT> xc;
   load_x_chunk<XT>(xc, x, cs);
   RouteRegs rr;
   if (route.logits) {
     // Router mode: every workgroup ranks the logits itself (no separate
     // launch); workgroup 0 publishes the route for the down kernel.
-    block_topk(route.logits, route.n_bank, route.n, route_scratch, sel, wsel);
+    block_topk(route.logits, route.n_bank, route.n, route_scratch, sel, wsel, logit, pre);
     if (blockIdx.x == 0) {
       for (int j = threadIdx.x; j < route.n; j += blockDim.x) {
         route.ids_pub[j] = sel[j];
@@ -1239,15 +1256,25 @@ __device__ __forceinline__ uint64_t route_key(float v, int i) {
 // Block-level top-k + softmax.  keys: nseg*64 + round_up(nseg*top_k, 2) uint64
 // of LDS scratch (16-byte aligned); sel/wsel receive the selected ids (rank
 // order) and weights.  All threads of the workgroup call it; it ends with a
-// barrier.  Comparisons read two keys per 128-bit LDS load.
+// barrier.  Comparisons read two keys per 128-bit LDS load.  have_pre: the
+// caller already loaded logit threadIdx.x into pre (issued ahead of its other
+// loads, so ranking starts as soon as the logits arrive).
 __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
-                           uint64_t* keys, int* sel, float* wsel) {
+                           uint64_t* keys, int* sel, float* wsel, float pre, bool have_pre) {
   const int nseg = (n_bank + 63) >> 6;
   const int ncand = nseg * top_k;
   const int ncand2 = (ncand + 1) & ~1;
   uint64_t* cand = keys + (size_t)nseg * 64;
   const int T = blockDim.x;
-  for (int i = threadIdx.x; i < nseg * 64; i += T)
+  int i0 = threadIdx.x;
+  if (have_pre) {
+    // The preloaded key is stored on its own, so this store waits for that
+    // load only (a store shared with the loop below would wait for every
+    // load in flight, the caller's later ones included).
+    if (i0 < nseg * 64) keys[i0] = i0 < n_bank ? route_key(pre, i0) : 0ull;
+    i0 += T;
+  }
+  for (int i = i0; i < nseg * 64; i += T)
     keys[i] = i < n_bank ? route_key(src[i], i) : 0ull;  // 0 ranks below every real key
   for (int i = threadIdx.x; i < ncand2; i += T) cand[i] = 0ull;
   __syncthreads();
@@ -1682,18 +1709,15 @@ template <typename XT, typename OT>
 int gemv1_dispatch(const uint8_t* p, const uint8_t* s, const XT* x, OT* y, int rows, int cols,
                    hipStream_t st) {
   const int G = cols / 32;
-  const int cpl = (G + 63) / 64;
-  const int waves = (rows + kRowsGemv - 1) / kRowsGemv;
-  const dim3 grid((waves + 3) / 4), block(256);
-  if (cpl > 4) return -1;  // caller falls back to the LDS kernel
+  const int S = (G + 63) / 64;
+  if (S > 4) return -1;  // caller falls back to the LDS kernel
+  const int groups = 4 / S;
+  const int n_units = (rows + kRowsGemv - 1) / kRowsGemv;
+  const int cus = std::max(1, device_cu_count());
+  const int grid = std::max(1, std::min((n_units + groups - 1) / groups, 8 * cus));
   TimedLaunch tl(KC_GEMV, st);
-  switch (cpl) {
-    case 1: launch_timed(tl, (k_gemv1<XT, OT, 1, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
-    case 2: launch_timed(tl, (k_gemv1<XT, OT, 2, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
-    case 3: launch_timed(tl, (k_gemv1<XT, OT, 3, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
-    case 4: launch_timed(tl, (k_gemv1<XT, OT, 4, kRowsGemv>), grid, block, 0, st, p, s, x, y, rows, cols); break;
-    default: return -1;  // caller falls back to the LDS kernel
-  }
+  launch_timed(tl, (k_gemv_cs<XT, OT, kRowsGemv>), dim3(grid), dim3(256), 0, st, p, s, x, y,
+               rows, cols, S);
   return launched(tl, "mxfp4 GEMV launch");
 }
 
@@ -1871,7 +1895,13 @@ int down_g64_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT*
                       hipStream_t st) {
   const int nbt = (g.hidden + 3) / 4;
   const int cus = std::max(1, device_cu_count());
-  const int blocks = std::min(nbt, std::max(cus, (nbt + kDownG64MaxNB - 1) / kDownG64MaxNB));
+  // A workgroup holds one wave per routed expert: with fewer than 16 experts
+  // the grid grows (16 / n workgroups per CU) so the chip keeps ~16 waves of
+  // row batches per CU in flight (one expert: 1,792 one-batch workgroups at
+  // hidden 7168 instead of 256 that walk 7 batches each).
+  const int per_cu = std::max(1, 16 / std::max(1, route.n));
+  const int blocks =
+      std::min(nbt, std::max(cus * per_cu, (nbt + kDownG64MaxNB - 1) / kDownG64MaxNB));
   const int nb = (nbt + blocks - 1) / blocks;
   switch (nb) {
     case 1: return down_g64_launch<OT, 1>(g, route, h, out, blocks, st);
