@@ -252,8 +252,10 @@ __device__ __forceinline__ void load_x_chunk<float>(XChunk<float>& xc, const flo
 // each lane keeps its one activation chunk in registers, loads the chunk and
 // scale byte of all kR rows of its unit at once, and a butterfly reduces the
 // kR partials across the wave; the S wave partials meet in LDS.  Every unit
-// is one round of loads, so a 2048 x 7168 matrix (256 units of 8 rows) is one
-// wave of loads over the whole chip.
+// is one round of loads, so a 2048 x 7168 matrix (512 units of 4 rows, two
+// 256-thread workgroups per CU) is one wave of loads over the whole chip.
+// Units of 4 rows measured 4.9 us per call at that shape on MI355X, against
+// 7.5 us for 8 rows, 7.8 us for 16, 6.7 us for 2 and 9.6 us for 1.
 // ======================================================================
 template <typename XT, typename OT, int kR>
 __global__ __launch_bounds__(256) void k_gemv_cs(const uint8_t* __restrict__ packed,
@@ -960,6 +962,138 @@ __global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route, const
     if (row >= g.hidden) continue;
     float acc = 0.0f;
     for (int e = 0; e < route.n; ++e) acc += weight_of(rreg, e) * ybuf[e][t];
+    store_out(out + row, acc);
+  }
+}
+
+// k_down_g96: the same split for intermediate 3072 (96 scale groups per row:
+// the K3 geometry).  The batch is a pair of output rows (2 p, 2 p + 1): its
+// weights are 3,072 contiguous bytes of the matrix and its scales 192
+// contiguous bytes.  Lane l takes group l of both rows (the "head" chunks: two
+// coalesced 1 KB loads) and group 64 + l % 32 of row 2 p + l / 32 (the "tail"
+// chunk: two 512 B runs), so every lane has three chunks of every pair and
+// holds two chunks of h_e (l and 64 + l % 32: 64 floats) instead of three.
+// Lane m (< 48) loads dword m of the pair's scales and ds_bpermute hands each
+// lane its three bytes: head of row 2 p is byte l, head of row 2 p + 1 byte
+// 96 + l, the tail byte 64 + l (l < 32) or 128 + l (l >= 32).  kS4
+// (scale4-v2): the pair's 192 index nibbles are 96 bytes (lane m < 24 loads
+// dword m) and nibble q sits in dword q / 8 at bit 4 (q % 8), added to the
+// expert's base.  One wave per routed expert, NB pair slots unrolled with two
+// in flight, h_e's chunks transposed through LDS and the route-ordered
+// combine out of LDS, as in k_down_g64.
+constexpr int kG96RowBytes = 1536;  // 3072 nibbles
+constexpr int kG96ScaleBytes = 96;  // per row (raw-v1)
+
+struct PairBatch {
+  u32x4 a, b, c;  // head of row 2 p, head of row 2 p + 1, tail
+  uint32_t s;     // the scale dword this lane loaded for the pair
+};
+
+template <bool kS4>
+__device__ __forceinline__ void pair_load(PairBatch& bt, const uint8_t* span, const Geo& g,
+                                          int p, int lane) {
+  const uint8_t* dp = span + g.w2p + (size_t)p * (2 * kG96RowBytes);
+  const uint8_t* ds = span + g.w2s + (size_t)p * (kS4 ? kG96ScaleBytes : 2 * kG96ScaleBytes);
+  bt.s = load_u32(ds + 4 * min(lane, kS4 ? 23 : 47));
+  const uint32_t lo = (uint32_t)lane << 4;
+  bt.a = load_chunk(dp + lo);
+  bt.b = load_chunk(dp + kG96RowBytes + lo);
+  bt.c = load_chunk(dp + 1024 + (lane >> 5) * kG96RowBytes + ((uint32_t)(lane & 31) << 4));
+}
+
+// E8M0 scale of byte / nibble index q of the pair (see k_down_g96).
+template <bool kS4>
+__device__ __forceinline__ float pair_scale(uint32_t s, int q, uint32_t base) {
+  if constexpr (kS4) {
+    const uint32_t word = (uint32_t)__builtin_amdgcn_ds_bpermute((q >> 3) << 2, (int)s);
+    return e8m0_scale(base + ((word >> (4 * (q & 7))) & 0xfu));
+  } else {
+    const uint32_t word = (uint32_t)__builtin_amdgcn_ds_bpermute((q >> 2) << 2, (int)s);
+    return e8m0_scale((word >> (8 * (q & 3))) & 0xffu);
+  }
+}
+
+// Partial sums of rows 2 p and 2 p + 1 over the wave: v[0] in lanes 0-31 holds
+// row 2 p, in lanes 32-63 row 2 p + 1.
+template <bool kS4>
+__device__ __forceinline__ float pair_dots(const PairBatch& bt, const XChunk<float>& hh,
+                                           const XChunk<float>& ht, int lane, uint32_t base) {
+  const float va = hh.dot(bt.a) * pair_scale<kS4>(bt.s, lane, base);
+  const float vb = hh.dot(bt.b) * pair_scale<kS4>(bt.s, 96 + lane, base);
+  const float vc = ht.dot(bt.c) * pair_scale<kS4>(bt.s, 64 + lane + ((lane >> 5) << 6), base);
+  float v[2] = {va + (lane < 32 ? vc : 0.0f), vb + (lane < 32 ? 0.0f : vc)};
+  wave_reduce_multi<2>(v, lane);
+  return v[0];
+}
+
+template <typename OT, int NB, bool kS4>
+__global__ __launch_bounds__(1024) void k_down_g96(const TokenRoute route, const Geo g,
+                                                   const float* __restrict__ h,
+                                                   OT* __restrict__ out) {
+  __shared__ float ybuf[K3_HIP_MAX_TOKEN_EXPERTS][NB * 2];
+  extern __shared__ float4 hbuf[];  // kHSliceF4 float4 per wave
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: SGPR
+  const int G = gridDim.x;
+  const int npt = g.hidden >> 1;                       // pairs in the output (hidden even)
+  const int nb = (npt - (int)blockIdx.x + G - 1) / G;  // 1 <= nb <= NB (host)
+  auto pair_of = [&](int i) { return min(i, nb - 1) * G + (int)blockIdx.x; };
+  const int e = wave;  // one routed expert per wave (route.n <= 16 waves)
+  const float* he = h + (size_t)e * g.inter;
+  // h_e's head (floats 0-2047: float4 64 q + lane) and tail (floats
+  // 2048-3071: float4 512 + 64 q + lane) go out first: they are indexed by
+  // route slot, not by the expert's span.
+  float4 th[8], tt[4];
+  h_slice_issue(th, he, lane);
+  {
+    const float4* src = reinterpret_cast<const float4*>(he) + 512 + lane;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) tt[q] = src[64 * q];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const RouteRegs rreg = route_regs(route, lane);
+  const uint32_t base = kS4 ? (__builtin_amdgcn_readlane(route_bases(rreg, route.n, lane), e) >> 8) & 0xffu
+                            : 0u;
+  {
+    const uint8_t* span = span_of(rreg, e);
+    PairBatch bt[2];
+    pair_load<kS4>(bt[0], span, g, pair_of(0), lane);
+    if constexpr (NB > 1) pair_load<kS4>(bt[1], span, g, pair_of(1), lane);
+    __builtin_amdgcn_sched_barrier(0);
+    float4* hw = hbuf + wave * kHSliceF4;
+    XChunk<float> hh, ht;
+    h_slice_transpose(hh, th, hw, lane);
+    // The tail reuses the wave's LDS region: a wave's LDS operations run in
+    // issue order, so the head's reads above are served before these writes;
+    // the empty asm (a compiler memory barrier) keeps the compiler from moving
+    // the writes above the reads.
+    asm volatile("" ::: "memory");
+    {
+      float4* dst = hw + 9 * (lane >> 3) + (lane & 7);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dst[72 * q] = tt[q];
+      const float4* mine = hw + 9 * (lane & 31);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float4 v = mine[q];
+        ht.v[4 * q + 0] = v.x;
+        ht.v[4 * q + 1] = v.y;
+        ht.v[4 * q + 2] = v.z;
+        ht.v[4 * q + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float v = pair_dots<kS4>(bt[b & 1], hh, ht, lane, base);
+      if (b + 2 < NB) pair_load<kS4>(bt[b & 1], span, g, pair_of(b + 2), lane);
+      if ((lane & 31) == 0 && b < nb) ybuf[e][2 * b + (lane >> 5)] = v;
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < nb * 2; t += blockDim.x) {
+    const int row = 2 * pair_of(t >> 1) + (t & 1);
+    float acc = 0.0f;
+    for (int e2 = 0; e2 < route.n; ++e2) acc += weight_of(rreg, e2) * ybuf[e2][t];
     store_out(out + row, acc);
   }
 }
@@ -1692,6 +1826,11 @@ __global__ void k_synth_normal(void* out, int dtype, uint64_t n, uint64_t seed, 
 namespace {
 
 constexpr int kRowsGemv = 8;
+// Rows per unit of the single-activation GEMV (k_gemv_cs).
+#ifndef K3_GEMV_CS_ROWS
+#define K3_GEMV_CS_ROWS 4
+#endif
+constexpr int kRowsGemvCs = K3_GEMV_CS_ROWS;
 // Rows per unit of the decode gate/up kernel (gate and up each).
 constexpr int kRowsGlu = K3_GLU_ROWS;
 // Rows per load batch of the decode down kernel.
@@ -1712,11 +1851,11 @@ int gemv1_dispatch(const uint8_t* p, const uint8_t* s, const XT* x, OT* y, int r
   const int S = (G + 63) / 64;
   if (S > 4) return -1;  // caller falls back to the LDS kernel
   const int groups = 4 / S;
-  const int n_units = (rows + kRowsGemv - 1) / kRowsGemv;
+  const int n_units = (rows + kRowsGemvCs - 1) / kRowsGemvCs;
   const int cus = std::max(1, device_cu_count());
   const int grid = std::max(1, std::min((n_units + groups - 1) / groups, 8 * cus));
   TimedLaunch tl(KC_GEMV, st);
-  launch_timed(tl, (k_gemv_cs<XT, OT, kRowsGemv>), dim3(grid), dim3(256), 0, st, p, s, x, y,
+  launch_timed(tl, (k_gemv_cs<XT, OT, kRowsGemvCs>), dim3(grid), dim3(256), 0, st, p, s, x, y,
                rows, cols, S);
   return launched(tl, "mxfp4 GEMV launch");
 }
@@ -1916,6 +2055,52 @@ int down_g64_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT*
   }
 }
 
+template <typename OT, int NB, bool kS4>
+int down_g96_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out, int blocks,
+                    hipStream_t st) {
+  const int nw = route.n;  // one wave per routed expert (route.n <= 16)
+  const unsigned lds = (unsigned)(nw * kHSliceF4 * sizeof(float4));
+  if (!lds_fits((const void*)k_down_g96<OT, NB, kS4>, 64 * nw, lds))
+    return fail(K3_HIP_E_EXEC, "decode layer: %u B of LDS per workgroup not available", lds);
+  TimedLaunch tl(KC_DOWN_DECODE, st);
+  launch_timed(tl, (k_down_g96<OT, NB, kS4>), dim3(blocks), dim3(64 * nw), lds, st, route, g, h,
+               out);
+  return launched(tl, "decode down/combine launch");
+}
+
+// Workgroups for k_down_g96, sized as for k_down_g64 over row pairs.
+template <typename OT, bool kS4>
+int down_g96_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
+                      hipStream_t st) {
+  const int npt = g.hidden / 2;
+  const int cus = std::max(1, device_cu_count());
+  const int per_cu = std::max(1, 16 / std::max(1, route.n));
+  const int blocks =
+      std::min(npt, std::max(cus * per_cu, (npt + kDownG64MaxNB - 1) / kDownG64MaxNB));
+  const int nb = (npt + blocks - 1) / blocks;
+  switch (nb) {
+    case 1: return down_g96_launch<OT, 1, kS4>(g, route, h, out, blocks, st);
+    case 2: return down_g96_launch<OT, 2, kS4>(g, route, h, out, blocks, st);
+    case 3: return down_g96_launch<OT, 3, kS4>(g, route, h, out, blocks, st);
+    case 4: return down_g96_launch<OT, 4, kS4>(g, route, h, out, blocks, st);
+    case 5: return down_g96_launch<OT, 5, kS4>(g, route, h, out, blocks, st);
+    case 6: return down_g96_launch<OT, 6, kS4>(g, route, h, out, blocks, st);
+    case 7: return down_g96_launch<OT, 7, kS4>(g, route, h, out, blocks, st);
+    case 8: return down_g96_launch<OT, 8, kS4>(g, route, h, out, blocks, st);
+    default: return fail(K3_HIP_E_INVALID, "decode layer: %d down pairs per workgroup", nb);
+  }
+}
+
+// k_down_g96 serves intermediate 3072 with at most 16 routed experts and an
+// even hidden width (a build knob keeps k_down_blocks for comparison).
+#ifndef K3_DOWN_G96
+#define K3_DOWN_G96 1
+#endif
+bool down_g96_fits(const Geo& g, const TokenRoute& route) {
+  return K3_DOWN_G96 && g.inter == 3072 && route.n <= 16 && g.hidden % 2 == 0 && g.w2p % 16 == 0 &&
+         g.w2s % 4 == 0;
+}
+
 template <typename OT>
 int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace& ws, OT* out,
                          hipStream_t st) {
@@ -1923,9 +2108,11 @@ int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace&
   if (g.layout == K3_LAYOUT_SCALE4_V2) {
     // The format is defined for K3 only (96 groups per down row).
     if (GB != 96) return fail(K3_HIP_E_CAPABILITY, "scale4-v2: intermediate %d is not supported", g.inter);
+    if (down_g96_fits(g, route)) return down_g96_dispatch<OT, true>(g, route, ws.h, out, st);
     return down_blocks_launch<OT, 2, 2, true>(g, route, ws.h, out, st);
   }
   if (GB == 64 && route.n <= 16) return down_g64_dispatch<OT>(g, route, ws.h, out, st);
+  if (down_g96_fits(g, route)) return down_g96_dispatch<OT, false>(g, route, ws.h, out, st);
   switch ((GB + 63) / 64) {
     case 1: return down_blocks_launch<OT, 1, kDownBlocksBatch>(g, route, ws.h, out, st);
     case 2: return down_blocks_launch<OT, 2, K3_DOWN_BATCH_CPL2>(g, route, ws.h, out, st);

@@ -424,3 +424,35 @@ def test_k3_layer_vs_reference_expert_set(gpu):
     for name, got in outs.items():
         err = oracle.cond_rel_err(got, want, mag, g.intermediate)
         assert err <= 2e-4, f"{name}: {err:.3e}"
+
+
+@pytest.mark.parametrize("n", [1, 3, 8, 13])
+def test_k3_layer_route_counts(gpu, n):
+    """The K3 down kernel at every workgroup shape it takes (1, 2, 4 and 7 row
+    pairs per workgroup for 1, 3, 8 and 13 routed experts), raw-v1 against the
+    oracle, and scale4-v2 spans bit-equal to raw-v1 (same arithmetic)."""
+    import torch
+    from deltafin_amd import _lib, moe
+    g = moe.preset(1)
+    assert gpu.k3_hip_configure_v1(C.byref(g)) == 0
+    say(f"K3 layer, {n} experts")
+    spans = _experts(n, g.hidden, g.intermediate, 515 + n)
+    rng = np.random.default_rng(n)
+    w = rng.random(n).astype(np.float32) + 0.05
+    w /= w.sum()
+    x = rng.standard_normal(g.hidden).astype(np.float32)
+    dspans = [_t(sp) for sp in spans]
+    ws = moe.workspace(g, n)
+    out = moe.moe_layer(g, dspans, w, _t(x), ws)
+    out_bf = moe.moe_layer(g, dspans, w, _t(x), ws, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    ref, mag = oracle.moe_layer_f64(spans, w.astype(np.float64), g.hidden, g.intermediate,
+                                    g.activation, x)
+    err = oracle.cond_rel_err(o, ref, mag, g.intermediate)
+    assert err <= TOL, f"cond rel err {err:.3e}"
+    bits = out_bf.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(bits, synth.to_bf16_bits(o))
+    s4 = [oracle.scale4_span(sp) for sp in spans]
+    got = moe.moe_layer_desc(s4, w, x, layout=_lib.K3_LAYOUT_SCALE4_V2)
+    assert np.array_equal(got.view(np.uint32), moe.moe_layer_desc(spans, w, x).view(np.uint32))
