@@ -933,9 +933,10 @@ __global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route, const
   const int idx = lane >> 4;
   const bool writer = (lane & 15) == 0;
   // One routed expert per wave (the host launches route.n <= 16 waves).
-  // h_e is indexed by route slot, so its loads go out before the route ids
-  // (and with them the expert's span) come back; then batches 0 and 1, then
-  // the LDS transpose waits for h_e (scheduling barriers keep the order).
+  // h_e is indexed by route slot, not by the expert's span, so its loads are
+  // written ahead of the route; the compiler still issues them after the
+  // route's wait, behind the loads of batches 0 and 1 (hipcc 7.2 ISA), and the
+  // LDS transpose then waits for them.
   const int e = wave;
   float4 ht[8];
   h_slice_issue(ht, h + (size_t)e * g.inter, lane);
@@ -1041,8 +1042,8 @@ __global__ __launch_bounds__(1024) void k_down_g96(const TokenRoute route, const
   const int e = wave;  // one routed expert per wave (route.n <= 16 waves)
   const float* he = h + (size_t)e * g.inter;
   // h_e's head (floats 0-2047: float4 64 q + lane) and tail (floats
-  // 2048-3071: float4 512 + 64 q + lane) go out first: they are indexed by
-  // route slot, not by the expert's span.
+  // 2048-3071: float4 512 + 64 q + lane), written ahead of the route as in
+  // k_down_g64 (and issued, as there, behind the first pairs' loads).
   float4 th[8], tt[4];
   h_slice_issue(th, he, lane);
   {
@@ -1425,18 +1426,34 @@ __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
     if (rank < top_k) cand[(i >> 6) * top_k + rank] = k;
   }
   __syncthreads();
-  // stage 2: rank among the candidates is the global rank
-  for (int t = threadIdx.x; t < ncand; t += T) {
-    const uint64_t k = cand[t];
-    if (k == 0ull) continue;
+  // stage 2: rank among the candidates is the global rank.  P adjacent
+  // threads share a candidate (P = the largest power of two <= 8 with P
+  // threads per candidate available), each counting over its 1/P of the
+  // candidate list; the partial counts meet by lane exchange inside the group.
+  {
+    int P = 1;
+    while (P < 8 && 2 * P * ncand <= T) P *= 2;
+    const int span2 = (ncand2 / 2 + P - 1) / P;  // ulonglong2 per part
     const ulonglong2* c2 = reinterpret_cast<const ulonglong2*>(cand);
-    int rank = 0;
-#pragma unroll 8
-    for (int j = 0; j < ncand2 / 2; ++j) {
-      const ulonglong2 q = c2[j];
-      rank += (q.x > k) + (q.y > k);
+    for (int t0 = 0; t0 < ncand * P; t0 += T) {
+      const int t = t0 + (int)threadIdx.x;
+      const int c = t / P, part = t - c * P;
+      const bool live = c < ncand;
+      const uint64_t k = live ? cand[c] : 0ull;
+      const int j0 = part * span2, j1 = min(ncand2 / 2, j0 + span2);
+      int rank = 0;
+      if (live) {
+#pragma unroll 4
+        for (int j = j0; j < j1; ++j) {
+          const ulonglong2 q = c2[j];
+          rank += (q.x > k) + (q.y > k);
+        }
+      }
+      // Every lane of the wave takes part in the exchanges (groups of P
+      // lanes are aligned, so a group is wholly live or wholly not).
+      for (int m = 1; m < P; m *= 2) rank += __shfl_xor(rank, m);
+      if (live && part == 0 && k != 0ull && rank < top_k) sel[rank] = (int)(~(uint32_t)k);
     }
-    if (rank < top_k) sel[rank] = (int)(~(uint32_t)k);
   }
   __syncthreads();
   // softmax over the selected logits: one wave, fixed summation order.  The
@@ -1961,6 +1978,19 @@ int launch_route_sigmoid_bias(const float* logits, const float* bias, int n_bank
 
 namespace {
 
+// Workgroups of k_down_g64 for n routed experts: one per CU, more when a
+// workgroup would own more than kDownG64MaxNB batches, and with fewer than 16
+// experts 16 / n per CU (a workgroup holds one wave per routed expert, so the
+// chip keeps ~16 waves of row batches per CU in flight: one expert at hidden
+// 7168 gives 1,792 one-batch workgroups instead of 256 that walk 7 batches
+// each); every workgroup owns at least one batch.
+int down_g64_blocks(const Geo& g, int n) {
+  const int nbt = (g.hidden + 3) / 4;
+  const int cus = std::max(1, device_cu_count());
+  const int per_cu = std::max(1, 16 / std::max(1, n));
+  return std::min(nbt, std::max(cus * per_cu, (nbt + kDownG64MaxNB - 1) / kDownG64MaxNB));
+}
+
 template <typename XT>
 int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, float* h,
                         hipStream_t st) {
@@ -2027,20 +2057,11 @@ int down_g64_launch(const Geo& g, const TokenRoute& route, const float* h, OT* o
   return launched(tl, "decode down/combine launch");
 }
 
-// Workgroups for k_down_g64: one per CU, more when a workgroup would own more
-// than kDownG64MaxNB batches; every workgroup owns at least one batch.
 template <typename OT>
 int down_g64_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
                       hipStream_t st) {
   const int nbt = (g.hidden + 3) / 4;
-  const int cus = std::max(1, device_cu_count());
-  // A workgroup holds one wave per routed expert: with fewer than 16 experts
-  // the grid grows (16 / n workgroups per CU) so the chip keeps ~16 waves of
-  // row batches per CU in flight (one expert: 1,792 one-batch workgroups at
-  // hidden 7168 instead of 256 that walk 7 batches each).
-  const int per_cu = std::max(1, 16 / std::max(1, route.n));
-  const int blocks =
-      std::min(nbt, std::max(cus * per_cu, (nbt + kDownG64MaxNB - 1) / kDownG64MaxNB));
+  const int blocks = down_g64_blocks(g, route.n);
   const int nb = (nbt + blocks - 1) / blocks;
   switch (nb) {
     case 1: return down_g64_launch<OT, 1>(g, route, h, out, blocks, st);
