@@ -2017,6 +2017,16 @@ int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, floa
     return launched(tl, "decode gate/up launch");
   }
   TimedLaunch tl(KC_GLU_DECODE, st);
+  // Few experts (every pipeline would hold one unit: config 1 is one expert):
+  // units of 2 rows, two per pipeline, measured 12.1 -> 10.9 us per expert at
+  // hidden 7168 / intermediate 2048 (the second unit's loads are in flight
+  // while the first is reduced).  Their scale bytes are loaded per row.
+  if (kRowsGlu == 4 && (n_units + groups - 1) / groups <= cus && g.inter % 2 == 0) {
+    const int n_units2 = route.n * (g.inter / 2);
+    launch_timed(tl, (k_glu_decode<XT, 2, false>), dim3(grid), dim3(64 * S * groups),
+                 (unsigned)lds, st, route, g, x, h, n_units2, S);
+    return launched(tl, "decode gate/up launch");
+  }
   if (gather)
     launch_timed(tl, (k_glu_decode<XT, kRowsGlu, true>), dim3(grid), dim3(64 * S * groups),
                  (unsigned)lds, st, route, g, x, h, n_units, S);

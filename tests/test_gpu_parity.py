@@ -456,3 +456,33 @@ def test_k3_layer_route_counts(gpu, n):
     s4 = [oracle.scale4_span(sp) for sp in spans]
     got = moe.moe_layer_desc(s4, w, x, layout=_lib.K3_LAYOUT_SCALE4_V2)
     assert np.array_equal(got.view(np.uint32), moe.moe_layer_desc(spans, w, x).view(np.uint32))
+
+
+@pytest.mark.parametrize("n,xdt", [(1, "bf16"), (1, "f32"), (2, "bf16"), (3, "f32")])
+def test_moe_layer_few_experts(gpu, n, xdt):
+    """Preset 2 with 1-3 routed experts: the gate/up kernel's 2-row units (a
+    pipeline would otherwise hold one unit) and the down kernel's 16 / n
+    workgroups per CU, against the oracle; two calls bit-equal."""
+    import torch
+    from deltafin_amd import moe
+    g = moe.preset(2)
+    say(f"layer preset 2, {n} experts, x={xdt}")
+    spans = _experts(n, g.hidden, g.intermediate, 700 + n)
+    rng = np.random.default_rng(70 + n)
+    w = rng.random(n).astype(np.float32) + 0.1
+    w /= w.sum()
+    x = rng.standard_normal(g.hidden).astype(np.float32)
+    if xdt == "bf16":
+        x = synth.bf16_bits_to_f32(synth.to_bf16_bits(x))
+        dx = _bf16(x)
+    else:
+        dx = _t(x)
+    dspans = [_t(sp) for sp in spans]
+    ws = moe.workspace(g, n)
+    out = moe.moe_layer(g, dspans, w, dx, ws).cpu().numpy()
+    out2 = moe.moe_layer(g, dspans, w, dx, ws).cpu().numpy()
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+    ref, mag = oracle.moe_layer_f64(spans, w.astype(np.float64), g.hidden, g.intermediate,
+                                    g.activation, x)
+    err = oracle.cond_rel_err(out, ref, mag, g.intermediate)
+    assert err <= TOL, f"cond rel err {err:.3e}"
