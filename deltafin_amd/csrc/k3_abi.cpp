@@ -20,6 +20,12 @@
 
 #include "k3_internal.h"
 
+// Per-position decode layers of one call as one position-batched launch pair
+// (launch_decode_positions) where supported; 0 keeps one layer per position.
+#ifndef K3_BATCH_POSITIONS
+#define K3_BATCH_POSITIONS 1
+#endif
+
 namespace k3 {
 
 // ---------------------------------------------------------------- errors
@@ -795,15 +801,20 @@ int experts_on_device_routes(const Geo& g, const uint8_t* bank, uint64_t stride,
     return mfma ? launch_verify_mfma(g, n_edges, P, x, K3_DTYPE_F32, out, K3_DTYPE_F32, ws, st)
                 : launch_verify_layer(g, n_edges, P, x, K3_DTYPE_F32, out, K3_DTYPE_F32, ws, st);
   }
+  TokenRoute route;
+  memset(&route, 0, sizeof(route));
+  route.bank = bank;
+  route.stride = stride;
+  route.ids = ws.ids;
+  route.wdev = ws.w;
+  route.n = top_k;
+  if (K3_BATCH_POSITIONS && P > 1 && decode_positions_supported(g, top_k))
+    return launch_decode_positions(g, route, P, x, K3_DTYPE_F32, out, K3_DTYPE_F32, ws, st);
   for (int p = 0; p < P; ++p) {
-    TokenRoute route;
-    memset(&route, 0, sizeof(route));
-    route.bank = bank;
-    route.stride = stride;
-    route.ids = ws.ids + (size_t)p * top_k;
-    route.wdev = ws.w + (size_t)p * top_k;
-    route.n = top_k;
-    const int rc = launch_decode_layer(g, route, x + (size_t)p * g.hidden, K3_DTYPE_F32,
+    TokenRoute rp = route;
+    rp.ids = ws.ids + (size_t)p * top_k;
+    rp.wdev = ws.w + (size_t)p * top_k;
+    const int rc = launch_decode_layer(g, rp, x + (size_t)p * g.hidden, K3_DTYPE_F32,
                                        out + (size_t)p * g.hidden, K3_DTYPE_F32, ws, st);
     if (rc != K3_HIP_OK) return rc;
   }
@@ -1341,24 +1352,33 @@ int k3_hip_moe_verify_route_device(const K3HipGeometryV1* gd, const uint8_t* ban
     return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
                 : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
   }
-  // One routed decode layer per position, in order on the stream: each
-  // position's gate/up kernel ranks its own logits, so the routes equal the
-  // per-position router's.  An expert picked by several positions is read once
-  // per position.
+  // One routed decode layer per position: each position's gate/up workgroups
+  // rank its own logits, so the routes equal the per-position router's.  An
+  // expert picked by several positions is read once per position.  Where the
+  // geometry allows, all positions run as one gate/up launch and one down
+  // launch (position on the grid's y axis: one position's workgroups start as
+  // the previous one's finish, with no launch boundary between positions);
+  // otherwise one layer after another on the stream.
   const size_t xb = x_dtype == K3_DTYPE_BF16 ? 2 : 4, ob = out_dtype == K3_DTYPE_BF16 ? 2 : 4;
+  TokenRoute route;
+  memset(&route, 0, sizeof(route));
+  route.bank = bank;
+  route.stride = expert_stride;
+  route.logits = logits;
+  route.n_bank = n_bank;
+  route.ids_pub = ws.ids;
+  route.w_pub = ws.w;
+  route.ids_user = route_ids;
+  route.w_user = route_weights;
+  route.n = top_k;
+  if (K3_BATCH_POSITIONS && n_positions > 1 && decode_positions_supported(g, top_k))
+    return launch_decode_positions(g, route, n_positions, x, x_dtype, out, out_dtype, ws, st);
   for (int p = 0; p < n_positions; ++p) {
-    TokenRoute route;
-    memset(&route, 0, sizeof(route));
-    route.bank = bank;
-    route.stride = expert_stride;
-    route.logits = logits + (size_t)p * n_bank;
-    route.n_bank = n_bank;
-    route.ids_pub = ws.ids;
-    route.w_pub = ws.w;
-    route.ids_user = route_ids ? route_ids + (size_t)p * top_k : nullptr;
-    route.w_user = route_weights ? route_weights + (size_t)p * top_k : nullptr;
-    route.n = top_k;
-    const int rc = launch_decode_layer(g, route, static_cast<const uint8_t*>(x) + p * g.hidden * xb,
+    TokenRoute rp = route;
+    rp.logits = logits + (size_t)p * n_bank;
+    rp.ids_user = route_ids ? route_ids + (size_t)p * top_k : nullptr;
+    rp.w_user = route_weights ? route_weights + (size_t)p * top_k : nullptr;
+    const int rc = launch_decode_layer(g, rp, static_cast<const uint8_t*>(x) + p * g.hidden * xb,
                                        x_dtype, static_cast<uint8_t*>(out) + p * g.hidden * ob,
                                        out_dtype, ws, st);
     if (rc != K3_HIP_OK) return rc;

@@ -122,6 +122,17 @@ int launch_route_sigmoid_bias(const float* logits, const float* bias, int n_bank
 int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x,
                         int x_dtype, void* out, int out_dtype,
                         const Workspace& ws, hipStream_t stream);
+// n_positions decode layers of one bank-mode route (router mode: logits
+// strided by n_bank; caller mode: ids / wdev strided by route.n) as one
+// gate/up launch and one down launch, position p on blockIdx.y: x and out rows
+// strided by hidden, h by route.n * intermediate (ws holds n_positions *
+// route.n edges).  Outputs equal n_positions launch_decode_layer calls bit for
+// bit.  Only where decode_positions_supported holds (k_down_g64 / k_down_g96
+// geometries, at most 16 experts, fused decode off).
+bool decode_positions_supported(const Geo& g, int n);
+int launch_decode_positions(const Geo& g, const TokenRoute& route, int n_positions,
+                            const void* x, int x_dtype, void* out, int out_dtype,
+                            const Workspace& ws, hipStream_t stream);
 // Process-wide decode path switch (k3_hip_set_fused_decode); returns the
 // previous setting.
 int set_fused_decode(int enabled);

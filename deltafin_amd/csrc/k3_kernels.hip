@@ -108,11 +108,13 @@ __device__ __forceinline__ void store_out<uint16_t>(uint16_t* p, float v) {
   *p = f32_to_bf16_bits(v);
 }
 
-__device__ __forceinline__ const uint8_t* route_span(const TokenRoute& r, int e) {
-  return r.bank ? r.bank + (uint64_t)r.ids[e] * r.stride : r.ptr[e];
+// off: first entry of this route in the device ids / weights (bank mode;
+// position-batched kernels route position p at p * n).
+__device__ __forceinline__ const uint8_t* route_span(const TokenRoute& r, int e, size_t off = 0) {
+  return r.bank ? r.bank + (uint64_t)r.ids[off + e] * r.stride : r.ptr[e];
 }
-__device__ __forceinline__ float route_weight(const TokenRoute& r, int e) {
-  return r.bank ? r.wdev[e] : r.w[e];
+__device__ __forceinline__ float route_weight(const TokenRoute& r, int e, size_t off = 0) {
+  return r.bank ? r.wdev[off + e] : r.w[e];
 }
 
 // A wave's copy of the route: lane e (< n) holds expert e's span address and
@@ -123,15 +125,15 @@ struct RouteRegs {
   float w;
 };
 
-__device__ __forceinline__ RouteRegs route_regs(const TokenRoute& r, int lane) {
+__device__ __forceinline__ RouteRegs route_regs(const TokenRoute& r, int lane, size_t off = 0) {
   RouteRegs o;
   o.lo = o.hi = 0u;
   o.w = 0.0f;
   if (lane < r.n) {
-    const uint64_t p = reinterpret_cast<uint64_t>(route_span(r, lane));
+    const uint64_t p = reinterpret_cast<uint64_t>(route_span(r, lane, off));
     o.lo = (uint32_t)p;
     o.hi = (uint32_t)(p >> 32);
-    o.w = route_weight(r, lane);
+    o.w = route_weight(r, lane, off);
   }
   return o;
 }
@@ -540,6 +542,13 @@ __device__ __forceinline__ void glu_sweep(const RouteRegs& rr, const Geo& g, con
   }
 }
 
+// Positions along blockIdx.y (kPos kernels, router mode): position p reads
+// logits + p n_bank and x + p x, writes h + p h and out + p out, and
+// publishes its route at ids/w + p n.  Element strides.
+struct PosStride {
+  int64_t x, h, out;
+};
+
 // Unit pipelines per gate/up workgroup (each S column-split waves) and rows
 // per unit; the launch bound follows so the register budget matches the
 // resident waves (16 waves/CU -> 128 VGPRs, 8 -> 256).
@@ -551,11 +560,21 @@ __device__ __forceinline__ void glu_sweep(const RouteRegs& rr, const Geo& g, con
 #endif
 constexpr int kGluMaxThreads = 256 * K3_GLU_GROUPS;
 
-template <typename XT, int kR, bool kG, bool kS4 = false>
-__global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute route, const Geo g,
-                                                     const XT* __restrict__ x,
-                                                     float* __restrict__ h, int n_units,
-                                                     int S) {
+template <typename XT, int kR, bool kG, bool kS4 = false, bool kPos = false>
+__global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute route_arg,
+                                                     const Geo g,
+                                                     const XT* __restrict__ x_arg,
+                                                     float* __restrict__ h_arg, int n_units,
+                                                     int S, const PosStride pos) {
+  // The route is read from the kernel argument itself (a modified copy would
+  // live in scratch: its span table is indexed per lane); position pidx's
+  // pointers are offsets from it.
+  const TokenRoute& route = route_arg;
+  const int pidx = kPos ? (int)blockIdx.y : 0;
+  const size_t proute = (size_t)pidx * route.n;
+  const float* logits = route.logits ? route.logits + (size_t)pidx * route.n_bank : nullptr;
+  const XT* __restrict__ x = x_arg + pidx * pos.x;
+  float* __restrict__ h = h_arg + pidx * pos.h;
   constexpr int N = 2 * kR;
   constexpr int L = log2c<N>();
   extern __shared__ __attribute__((aligned(16))) uint64_t route_scratch[];
@@ -578,22 +597,22 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
   const int row_step = (((g.hidden >> 5) + S - 1) / S) >> (kS4 ? 1 : 0);
   // Router mode: the logits are requested before the activation chunk, so
   // the ranking below waits for them alone.
-  const bool pre = route.logits && route.n_bank <= (int)blockDim.x;
+  const bool pre = logits && route.n_bank <= (int)blockDim.x;
   float logit = 0.0f;
-  if (pre && (int)threadIdx.x < route.n_bank) logit = route.logits[threadIdx.x];
+  if (pre && (int)threadIdx.x < route.n_bank) logit = logits[threadIdx.x];
   XChunk<XT> xc;
   load_x_chunk<XT>(xc, x, cs);
   RouteRegs rr;
-  if (route.logits) {
+  if (logits) {
     // Router mode: every workgroup ranks the logits itself (no separate
     // launch); workgroup 0 publishes the route for the down kernel.
-    block_topk(route.logits, route.n_bank, route.n, route_scratch, sel, wsel, logit, pre);
+    block_topk(logits, route.n_bank, route.n, route_scratch, sel, wsel, logit, pre);
     if (blockIdx.x == 0) {
       for (int j = threadIdx.x; j < route.n; j += blockDim.x) {
-        route.ids_pub[j] = sel[j];
-        route.w_pub[j] = wsel[j];
-        if (route.ids_user) route.ids_user[j] = sel[j];
-        if (route.w_user) route.w_user[j] = wsel[j];
+        route.ids_pub[proute + j] = sel[j];
+        route.w_pub[proute + j] = wsel[j];
+        if (route.ids_user) route.ids_user[proute + j] = sel[j];
+        if (route.w_user) route.w_user[proute + j] = wsel[j];
       }
     }
     rr.lo = rr.hi = 0u;
@@ -605,7 +624,7 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
       rr.w = wsel[lane];
     }
   } else {
-    rr = route_regs(route, lane);
+    rr = route_regs(route, lane, proute);
   }
   const uint32_t rb4 = kS4 ? route_bases(rr, route.n, lane) : 0u;
   // Unit pipelines: global pipeline index q = blockIdx.x * groups + grp takes
@@ -915,10 +934,15 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
 // after b's registers are free.
 constexpr int kDownG64MaxNB = 8;
 
-template <typename OT, int NB>
-__global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route, const Geo g,
-                                                   const float* __restrict__ h,
-                                                   OT* __restrict__ out) {
+template <typename OT, int NB, bool kPos = false>
+__global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route_arg, const Geo g,
+                                                   const float* __restrict__ h_arg,
+                                                   OT* __restrict__ out_arg, const PosStride pos) {
+  const TokenRoute& route = route_arg;  // read in place (see k_glu_decode)
+  const int pidx = kPos ? (int)blockIdx.y : 0;
+  const size_t proute = (size_t)pidx * route.n;
+  const float* __restrict__ h = h_arg + pidx * pos.h;
+  OT* __restrict__ out = out_arg + pidx * pos.out;
   constexpr int kB = 4;
   __shared__ float ybuf[K3_HIP_MAX_TOKEN_EXPERTS][NB * kB];
   extern __shared__ float4 hbuf[];  // kHSliceF4 float4 per wave
@@ -941,7 +965,7 @@ __global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route, const
   float4 ht[8];
   h_slice_issue(ht, h + (size_t)e * g.inter, lane);
   __builtin_amdgcn_sched_barrier(0);
-  const RouteRegs rreg = route_regs(route, lane);
+  const RouteRegs rreg = route_regs(route, lane, proute);
   {
     const uint8_t* span = span_of(rreg, e);
     DownBatch<1, kB, true> bt[2];
@@ -1027,10 +1051,15 @@ __device__ __forceinline__ float pair_dots(const PairBatch& bt, const XChunk<flo
   return v[0];
 }
 
-template <typename OT, int NB, bool kS4>
-__global__ __launch_bounds__(1024) void k_down_g96(const TokenRoute route, const Geo g,
-                                                   const float* __restrict__ h,
-                                                   OT* __restrict__ out) {
+template <typename OT, int NB, bool kS4, bool kPos = false>
+__global__ __launch_bounds__(1024) void k_down_g96(const TokenRoute route_arg, const Geo g,
+                                                   const float* __restrict__ h_arg,
+                                                   OT* __restrict__ out_arg, const PosStride pos) {
+  const TokenRoute& route = route_arg;  // read in place (see k_glu_decode)
+  const int pidx = kPos ? (int)blockIdx.y : 0;
+  const size_t proute = (size_t)pidx * route.n;
+  const float* __restrict__ h = h_arg + pidx * pos.h;
+  OT* __restrict__ out = out_arg + pidx * pos.out;
   __shared__ float ybuf[K3_HIP_MAX_TOKEN_EXPERTS][NB * 2];
   extern __shared__ float4 hbuf[];  // kHSliceF4 float4 per wave
   const int lane = threadIdx.x & 63;
@@ -1052,7 +1081,7 @@ __global__ __launch_bounds__(1024) void k_down_g96(const TokenRoute route, const
     for (int q = 0; q < 4; ++q) tt[q] = src[64 * q];
   }
   __builtin_amdgcn_sched_barrier(0);
-  const RouteRegs rreg = route_regs(route, lane);
+  const RouteRegs rreg = route_regs(route, lane, proute);
   const uint32_t base = kS4 ? (__builtin_amdgcn_readlane(route_bases(rreg, route.n, lane), e) >> 8) & 0xffu
                             : 0u;
   {
@@ -1991,9 +2020,28 @@ int down_g64_blocks(const Geo& g, int n) {
   return std::min(nbt, std::max(cus * per_cu, (nbt + kDownG64MaxNB - 1) / kDownG64MaxNB));
 }
 
+// Positions of one launch (kPos kernels along blockIdx.y); n = 1 launches
+// the single-position kernels.
+struct PosLaunch {
+  int n = 1;
+  PosStride s{0, 0, 0};
+};
+
+template <typename XT, int kR, bool kG, bool kS4 = false>
+void glu_go(TimedLaunch& tl, int grid, int threads, size_t lds, hipStream_t st,
+            const TokenRoute& route, const Geo& g, const XT* x, float* h, int n_units, int S,
+            const PosLaunch& pl) {
+  if (pl.n > 1)
+    launch_timed(tl, (k_glu_decode<XT, kR, kG, kS4, true>), dim3(grid, pl.n), dim3(threads),
+                 (unsigned)lds, st, route, g, x, h, n_units, S, pl.s);
+  else
+    launch_timed(tl, (k_glu_decode<XT, kR, kG, kS4>), dim3(grid), dim3(threads), (unsigned)lds,
+                 st, route, g, x, h, n_units, S, pl.s);
+}
+
 template <typename XT>
 int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, float* h,
-                        hipStream_t st) {
+                        hipStream_t st, const PosLaunch& pl = PosLaunch{}) {
   const int G = g.hidden / 32;
   const int S = (G + 63) / 64;
   if (S > 4) return fail(K3_HIP_E_INVALID, "decode layer: hidden %d exceeds 8192", g.hidden);
@@ -2004,35 +2052,31 @@ int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, floa
   const int groups = std::max(1, std::min(kGluMaxThreads / (64 * S), 16 / S));
   const int cus = std::max(1, device_cu_count());
   const int grid = std::max(1, std::min(cus, (n_units + groups - 1) / groups));
+  const int threads = 64 * S * groups;
   const int cw = (G + S - 1) / S;
   const bool gather = kRowsGlu == 4 && G % 4 == 0 && cw % 4 == 0 && kRowsGlu * cw <= 256;
+  TimedLaunch tl(KC_GLU_DECODE, st);
   if (g.layout == K3_LAYOUT_SCALE4_V2) {
     // Index dwords gathered per unit: whole bytes per wave and row, dword
     // aligned, at most one dword per lane.
     if (!(kRowsGlu == 4 && G % 8 == 0 && cw % 8 == 0 && kRowsGlu * (cw / 8) <= 64))
       return fail(K3_HIP_E_CAPABILITY, "scale4-v2: hidden %d is not supported", g.hidden);
-    TimedLaunch tl(KC_GLU_DECODE, st);
-    launch_timed(tl, (k_glu_decode<XT, kRowsGlu, true, true>), dim3(grid), dim3(64 * S * groups),
-                 (unsigned)lds, st, route, g, x, h, n_units, S);
+    glu_go<XT, kRowsGlu, true, true>(tl, grid, threads, lds, st, route, g, x, h, n_units, S, pl);
     return launched(tl, "decode gate/up launch");
   }
-  TimedLaunch tl(KC_GLU_DECODE, st);
   // Few experts (every pipeline would hold one unit: config 1 is one expert):
   // units of 2 rows, two per pipeline, measured 12.1 -> 10.9 us per expert at
   // hidden 7168 / intermediate 2048 (the second unit's loads are in flight
   // while the first is reduced).  Their scale bytes are loaded per row.
   if (kRowsGlu == 4 && (n_units + groups - 1) / groups <= cus && g.inter % 2 == 0) {
     const int n_units2 = route.n * (g.inter / 2);
-    launch_timed(tl, (k_glu_decode<XT, 2, false>), dim3(grid), dim3(64 * S * groups),
-                 (unsigned)lds, st, route, g, x, h, n_units2, S);
+    glu_go<XT, 2, false>(tl, grid, threads, lds, st, route, g, x, h, n_units2, S, pl);
     return launched(tl, "decode gate/up launch");
   }
   if (gather)
-    launch_timed(tl, (k_glu_decode<XT, kRowsGlu, true>), dim3(grid), dim3(64 * S * groups),
-                 (unsigned)lds, st, route, g, x, h, n_units, S);
+    glu_go<XT, kRowsGlu, true>(tl, grid, threads, lds, st, route, g, x, h, n_units, S, pl);
   else
-    launch_timed(tl, (k_glu_decode<XT, kRowsGlu, false>), dim3(grid), dim3(64 * S * groups),
-                 (unsigned)lds, st, route, g, x, h, n_units, S);
+    glu_go<XT, kRowsGlu, false>(tl, grid, threads, lds, st, route, g, x, h, n_units, S, pl);
   return launched(tl, "decode gate/up launch");
 }
 
@@ -2057,52 +2101,64 @@ int down_blocks_launch(const Geo& g, const TokenRoute& route, const float* h, OT
 
 template <typename OT, int NB>
 int down_g64_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out, int blocks,
-                    hipStream_t st) {
+                    hipStream_t st, const PosLaunch& pl) {
   const int nw = route.n;  // one wave per routed expert (route.n <= 16)
   const unsigned lds = (unsigned)(nw * kHSliceF4 * sizeof(float4));
-  if (!lds_fits((const void*)k_down_g64<OT, NB>, 64 * nw, lds))
+  const void* fn = pl.n > 1 ? (const void*)k_down_g64<OT, NB, true> : (const void*)k_down_g64<OT, NB>;
+  if (!lds_fits(fn, 64 * nw, lds))
     return fail(K3_HIP_E_EXEC, "decode layer: %u B of LDS per workgroup not available", lds);
   TimedLaunch tl(KC_DOWN_DECODE, st);
-  launch_timed(tl, (k_down_g64<OT, NB>), dim3(blocks), dim3(64 * nw), lds, st, route, g, h, out);
+  if (pl.n > 1)
+    launch_timed(tl, (k_down_g64<OT, NB, true>), dim3(blocks, pl.n), dim3(64 * nw), lds, st,
+                 route, g, h, out, pl.s);
+  else
+    launch_timed(tl, (k_down_g64<OT, NB>), dim3(blocks), dim3(64 * nw), lds, st, route, g, h, out,
+                 pl.s);
   return launched(tl, "decode down/combine launch");
 }
 
 template <typename OT>
 int down_g64_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
-                      hipStream_t st) {
+                      hipStream_t st, const PosLaunch& pl) {
   const int nbt = (g.hidden + 3) / 4;
   const int blocks = down_g64_blocks(g, route.n);
   const int nb = (nbt + blocks - 1) / blocks;
   switch (nb) {
-    case 1: return down_g64_launch<OT, 1>(g, route, h, out, blocks, st);
-    case 2: return down_g64_launch<OT, 2>(g, route, h, out, blocks, st);
-    case 3: return down_g64_launch<OT, 3>(g, route, h, out, blocks, st);
-    case 4: return down_g64_launch<OT, 4>(g, route, h, out, blocks, st);
-    case 5: return down_g64_launch<OT, 5>(g, route, h, out, blocks, st);
-    case 6: return down_g64_launch<OT, 6>(g, route, h, out, blocks, st);
-    case 7: return down_g64_launch<OT, 7>(g, route, h, out, blocks, st);
-    case 8: return down_g64_launch<OT, 8>(g, route, h, out, blocks, st);
+    case 1: return down_g64_launch<OT, 1>(g, route, h, out, blocks, st, pl);
+    case 2: return down_g64_launch<OT, 2>(g, route, h, out, blocks, st, pl);
+    case 3: return down_g64_launch<OT, 3>(g, route, h, out, blocks, st, pl);
+    case 4: return down_g64_launch<OT, 4>(g, route, h, out, blocks, st, pl);
+    case 5: return down_g64_launch<OT, 5>(g, route, h, out, blocks, st, pl);
+    case 6: return down_g64_launch<OT, 6>(g, route, h, out, blocks, st, pl);
+    case 7: return down_g64_launch<OT, 7>(g, route, h, out, blocks, st, pl);
+    case 8: return down_g64_launch<OT, 8>(g, route, h, out, blocks, st, pl);
     default: return fail(K3_HIP_E_INVALID, "decode layer: %d down batches per workgroup", nb);
   }
 }
 
 template <typename OT, int NB, bool kS4>
 int down_g96_launch(const Geo& g, const TokenRoute& route, const float* h, OT* out, int blocks,
-                    hipStream_t st) {
+                    hipStream_t st, const PosLaunch& pl) {
   const int nw = route.n;  // one wave per routed expert (route.n <= 16)
   const unsigned lds = (unsigned)(nw * kHSliceF4 * sizeof(float4));
-  if (!lds_fits((const void*)k_down_g96<OT, NB, kS4>, 64 * nw, lds))
+  const void* fn = pl.n > 1 ? (const void*)k_down_g96<OT, NB, kS4, true>
+                            : (const void*)k_down_g96<OT, NB, kS4>;
+  if (!lds_fits(fn, 64 * nw, lds))
     return fail(K3_HIP_E_EXEC, "decode layer: %u B of LDS per workgroup not available", lds);
   TimedLaunch tl(KC_DOWN_DECODE, st);
-  launch_timed(tl, (k_down_g96<OT, NB, kS4>), dim3(blocks), dim3(64 * nw), lds, st, route, g, h,
-               out);
+  if (pl.n > 1)
+    launch_timed(tl, (k_down_g96<OT, NB, kS4, true>), dim3(blocks, pl.n), dim3(64 * nw), lds, st,
+                 route, g, h, out, pl.s);
+  else
+    launch_timed(tl, (k_down_g96<OT, NB, kS4>), dim3(blocks), dim3(64 * nw), lds, st, route, g, h,
+                 out, pl.s);
   return launched(tl, "decode down/combine launch");
 }
 
 // Workgroups for k_down_g96, sized as for k_down_g64 over row pairs.
 template <typename OT, bool kS4>
 int down_g96_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
-                      hipStream_t st) {
+                      hipStream_t st, const PosLaunch& pl) {
   const int npt = g.hidden / 2;
   const int cus = std::max(1, device_cu_count());
   const int per_cu = std::max(1, 16 / std::max(1, route.n));
@@ -2110,14 +2166,14 @@ int down_g96_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT*
       std::min(npt, std::max(cus * per_cu, (npt + kDownG64MaxNB - 1) / kDownG64MaxNB));
   const int nb = (npt + blocks - 1) / blocks;
   switch (nb) {
-    case 1: return down_g96_launch<OT, 1, kS4>(g, route, h, out, blocks, st);
-    case 2: return down_g96_launch<OT, 2, kS4>(g, route, h, out, blocks, st);
-    case 3: return down_g96_launch<OT, 3, kS4>(g, route, h, out, blocks, st);
-    case 4: return down_g96_launch<OT, 4, kS4>(g, route, h, out, blocks, st);
-    case 5: return down_g96_launch<OT, 5, kS4>(g, route, h, out, blocks, st);
-    case 6: return down_g96_launch<OT, 6, kS4>(g, route, h, out, blocks, st);
-    case 7: return down_g96_launch<OT, 7, kS4>(g, route, h, out, blocks, st);
-    case 8: return down_g96_launch<OT, 8, kS4>(g, route, h, out, blocks, st);
+    case 1: return down_g96_launch<OT, 1, kS4>(g, route, h, out, blocks, st, pl);
+    case 2: return down_g96_launch<OT, 2, kS4>(g, route, h, out, blocks, st, pl);
+    case 3: return down_g96_launch<OT, 3, kS4>(g, route, h, out, blocks, st, pl);
+    case 4: return down_g96_launch<OT, 4, kS4>(g, route, h, out, blocks, st, pl);
+    case 5: return down_g96_launch<OT, 5, kS4>(g, route, h, out, blocks, st, pl);
+    case 6: return down_g96_launch<OT, 6, kS4>(g, route, h, out, blocks, st, pl);
+    case 7: return down_g96_launch<OT, 7, kS4>(g, route, h, out, blocks, st, pl);
+    case 8: return down_g96_launch<OT, 8, kS4>(g, route, h, out, blocks, st, pl);
     default: return fail(K3_HIP_E_INVALID, "decode layer: %d down pairs per workgroup", nb);
   }
 }
@@ -2132,18 +2188,27 @@ bool down_g96_fits(const Geo& g, const TokenRoute& route) {
          g.w2s % 4 == 0;
 }
 
+// The down kernels with a position-batched form (k_down_g64, k_down_g96).
+bool down_positions_fit(const Geo& g, int n) {
+  TokenRoute r{};
+  r.n = n;
+  return n <= 16 && ((g.inter == 2048 && g.layout != K3_LAYOUT_SCALE4_V2) || down_g96_fits(g, r));
+}
+
 template <typename OT>
 int down_decode_dispatch(const Geo& g, const TokenRoute& route, const Workspace& ws, OT* out,
-                         hipStream_t st) {
+                         hipStream_t st, const PosLaunch& pl = PosLaunch{}) {
   const int GB = g.inter / 32;
+  if (pl.n > 1 && !down_positions_fit(g, route.n))
+    return fail(K3_HIP_E_CAPABILITY, "decode layer: no batched down kernel for this geometry");
   if (g.layout == K3_LAYOUT_SCALE4_V2) {
     // The format is defined for K3 only (96 groups per down row).
     if (GB != 96) return fail(K3_HIP_E_CAPABILITY, "scale4-v2: intermediate %d is not supported", g.inter);
-    if (down_g96_fits(g, route)) return down_g96_dispatch<OT, true>(g, route, ws.h, out, st);
+    if (down_g96_fits(g, route)) return down_g96_dispatch<OT, true>(g, route, ws.h, out, st, pl);
     return down_blocks_launch<OT, 2, 2, true>(g, route, ws.h, out, st);
   }
-  if (GB == 64 && route.n <= 16) return down_g64_dispatch<OT>(g, route, ws.h, out, st);
-  if (down_g96_fits(g, route)) return down_g96_dispatch<OT, false>(g, route, ws.h, out, st);
+  if (GB == 64 && route.n <= 16) return down_g64_dispatch<OT>(g, route, ws.h, out, st, pl);
+  if (down_g96_fits(g, route)) return down_g96_dispatch<OT, false>(g, route, ws.h, out, st, pl);
   switch ((GB + 63) / 64) {
     case 1: return down_blocks_launch<OT, 1, kDownBlocksBatch>(g, route, ws.h, out, st);
     case 2: return down_blocks_launch<OT, 2, K3_DOWN_BATCH_CPL2>(g, route, ws.h, out, st);
@@ -2288,6 +2353,35 @@ int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x, in
   return out_dtype == K3_DTYPE_BF16
              ? down_decode_dispatch<uint16_t>(g, down_route, ws, static_cast<uint16_t*>(out), st)
              : down_decode_dispatch<float>(g, down_route, ws, static_cast<float*>(out), st);
+}
+
+bool decode_positions_supported(const Geo& g, int n) {
+  return n >= 1 && n <= 16 && down_positions_fit(g, n) && g_fused_enabled.load() == 0;
+}
+
+int launch_decode_positions(const Geo& g, const TokenRoute& route, int n_positions,
+                            const void* x, int x_dtype, void* out, int out_dtype,
+                            const Workspace& ws, hipStream_t st) {
+  if (!route.bank || n_positions < 1 || !decode_positions_supported(g, route.n))
+    return fail(K3_HIP_E_CAPABILITY, "decode positions: no batched form for this call");
+  PosLaunch pl;
+  pl.n = n_positions;
+  pl.s.x = g.hidden;
+  pl.s.h = (int64_t)route.n * g.inter;
+  pl.s.out = g.hidden;
+  int rc = x_dtype == K3_DTYPE_BF16
+               ? glu_decode_dispatch<uint16_t>(g, route, static_cast<const uint16_t*>(x), ws.h, st, pl)
+               : glu_decode_dispatch<float>(g, route, static_cast<const float*>(x), ws.h, st, pl);
+  if (rc != K3_HIP_OK) return rc;
+  TokenRoute down_route = route;
+  if (route.logits) {
+    down_route.logits = nullptr;
+    down_route.ids = ws.ids;
+    down_route.wdev = ws.w;
+  }
+  return out_dtype == K3_DTYPE_BF16
+             ? down_decode_dispatch<uint16_t>(g, down_route, ws, static_cast<uint16_t*>(out), st, pl)
+             : down_decode_dispatch<float>(g, down_route, ws, static_cast<float*>(out), st, pl);
 }
 
 int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride, int n_positions,
