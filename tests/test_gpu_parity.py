@@ -486,3 +486,52 @@ def test_moe_layer_few_experts(gpu, n, xdt):
                                     g.activation, x)
     err = oracle.cond_rel_err(out, ref, mag, g.intermediate)
     assert err <= TOL, f"cond rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("preset_id,n", [(2, 20), (2, 32), (1, 24)])
+def test_moe_layer_many_experts(gpu, preset_id, n):
+    """More than 16 routed experts (up to K3_HIP_MAX_TOKEN_EXPERTS = 32): the
+    down kernel for more experts than a workgroup has waves (k_down_blocks,
+    waves walking several experts), against the oracle."""
+    import torch
+    from deltafin_amd import moe
+    g = moe.preset(preset_id)
+    say(f"layer preset {preset_id}, {n} experts")
+    spans = _experts(n, g.hidden, g.intermediate, 900 + n)
+    rng = np.random.default_rng(90 + n)
+    w = rng.random(n).astype(np.float32) + 0.05
+    w /= w.sum()
+    x = rng.standard_normal(g.hidden).astype(np.float32)
+    dspans = [_t(sp) for sp in spans]
+    ws = moe.workspace(g, n)
+    out = moe.moe_layer(g, dspans, w, _t(x), ws).cpu().numpy()
+    ref, mag = oracle.moe_layer_f64(spans, w.astype(np.float64), g.hidden, g.intermediate,
+                                    g.activation, x)
+    err = oracle.cond_rel_err(out, ref, mag, g.intermediate)
+    assert err <= TOL, f"cond rel err {err:.3e}"
+
+
+def test_route_layer_top24(gpu):
+    """Device router with top_k 24 over a 40-expert bank: ids identical to the
+    oracle's top-k, output within the bar."""
+    import torch
+    from deltafin_amd import moe
+    g = moe.preset(2)
+    n_bank, k = 40, 24
+    say(f"route layer bank={n_bank} top_k={k}")
+    stride = g.expert_span
+    bank = torch.empty(n_bank * stride, dtype=torch.uint8, device="cuda")
+    moe.synth_bank(g, bank, stride, n_bank, 0, 4321)
+    ws = moe.workspace(g, k)
+    rng = np.random.default_rng(24)
+    logits = rng.standard_normal(n_bank).astype(np.float32)
+    x = synth.bf16_bits_to_f32(synth.to_bf16_bits(rng.standard_normal(g.hidden).astype(np.float32)))
+    out, ids, wts = moe.moe_route_layer(g, bank, stride, n_bank, _t(logits), k, _bf16(x), ws)
+    torch.cuda.synchronize()
+    rid, rw = oracle.topk_softmax(logits, k)
+    assert ids.cpu().numpy().tolist() == rid.tolist()
+    assert np.max(np.abs(wts.cpu().numpy() - rw)) <= 1e-6
+    spans = [oracle.synth_expert(4321, int(e), g.hidden, g.intermediate) for e in rid]
+    ref, mag = oracle.moe_layer_f64(spans, rw, g.hidden, g.intermediate, g.activation, x)
+    err = oracle.cond_rel_err(out.cpu().numpy(), ref, mag, g.intermediate)
+    assert err <= TOL, f"cond rel err {err:.3e}"
