@@ -461,7 +461,8 @@ __device__ __forceinline__ RouteRegs workgroup_route(const TokenRoute& route, ui
   rr.lo = rr.hi = 0u;
   rr.w = 0.0f;
   if (lane < route.n) {
-    const uint64_t p = reinterpret_cast<uint64_t>(route.bank) + (uint64_t)sel[lane] * route.stride;
+    const int id = min(max(sel[lane], 0), route.n_bank - 1);  // bank address in range
+    const uint64_t p = reinterpret_cast<uint64_t>(route.bank) + (uint64_t)id * route.stride;
     rr.lo = (uint32_t)p;
     rr.hi = (uint32_t)(p >> 32);
     rr.w = wsel[lane];
@@ -618,7 +619,10 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
     rr.lo = rr.hi = 0u;
     rr.w = 0.0f;
     if (lane < route.n) {
-      const uint64_t p = reinterpret_cast<uint64_t>(route.bank) + (uint64_t)sel[lane] * route.stride;
+      // The ranking writes every sel[j < n]; the clamp keeps a bank address
+      // in range whatever LDS holds.
+      const int id = min(max(sel[lane], 0), route.n_bank - 1);
+      const uint64_t p = reinterpret_cast<uint64_t>(route.bank) + (uint64_t)id * route.stride;
       rr.lo = (uint32_t)p;
       rr.hi = (uint32_t)(p >> 32);
       rr.w = wsel[lane];
@@ -1460,13 +1464,14 @@ __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
   // threads per candidate available), each counting over its 1/P of the
   // candidate list; the partial counts meet by lane exchange inside the group.
   {
-    int P = 1;
-    while (P < 8 && 2 * P * ncand <= T) P *= 2;
-    const int span2 = (ncand2 / 2 + P - 1) / P;  // ulonglong2 per part
+    int lgP = 0;
+    while (lgP < 3 && (2 << lgP) * ncand <= T) ++lgP;
+    const int P = 1 << lgP;
+    const int span2 = ((ncand2 >> 1) + P - 1) >> lgP;  // ulonglong2 per part
     const ulonglong2* c2 = reinterpret_cast<const ulonglong2*>(cand);
     for (int t0 = 0; t0 < ncand * P; t0 += T) {
       const int t = t0 + (int)threadIdx.x;
-      const int c = t / P, part = t - c * P;
+      const int c = t >> lgP, part = t & (P - 1);
       const bool live = c < ncand;
       const uint64_t k = live ? cand[c] : 0ull;
       const int j0 = part * span2, j1 = min(ncand2 / 2, j0 + span2);
