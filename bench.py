@@ -1089,8 +1089,12 @@ def _mfma_issued_per_expert() -> int:
     return PARITY_SPLIT * (glu + down)
 
 
+VERIFY_SETTLE_S = 0.05
+
+
 def _verify_batches(moe, _lib, g, bank, stride, logits, x, batches: int) -> dict:
-    """Time `batches` verify calls (after 3 warm-up calls) on each path:
+    """Time `batches` verify calls (after a 50 ms settle phase and 3 warm-up
+    calls) on each path:
     AUTO (the library's choice), the matrix-core union path and one decode
     layer per position; per-kernel stamps for the union path."""
     import torch
@@ -1112,6 +1116,16 @@ def _verify_batches(moe, _lib, g, bank, stride, logits, x, batches: int) -> dict
             raise _lib.K3HipError(rc, "k3_hip_moe_verify_route_device")
 
     def timed(stamps: bool):
+        # Settle: the batches back to back for VERIFY_SETTLE_S of host time
+        # (past the load-onset transient a cold GPU shows), then 3 warm-up
+        # calls, then the timed window.
+        t_end = time.perf_counter() + VERIFY_SETTLE_S
+        i = 0
+        while time.perf_counter() < t_end:
+            call(i % n)
+            i += 1
+            if i % n == 0:
+                torch.cuda.synchronize()
         for i in range(3):
             call(i)
         torch.cuda.synchronize()
