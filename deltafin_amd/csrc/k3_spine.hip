@@ -91,9 +91,37 @@ __device__ __forceinline__ int lds_slot(int c) {
 // provider_moe.cpp:535-542): norm_w[c] * (x[c] * r), r = 1 / sqrt(mean(x^2) +
 // eps), the sum of squares taken in a fixed order (thread-strided partials,
 // wave sums, the waves in order).  x rows and norm_w are 16-byte aligned.
+//
+// Rows with no padding (cols == kPad) and no norm go straight from memory to
+// LDS (global_load_lds_dwordx4): for each (position, piece, quarter) one
+// instruction of one wave brings 64 lanes' 16 bytes into the 1 KB that
+// ds_read_b128 reads back (lane l's 16 bytes: columns kPer l + 4 q .. + 3 of
+// the piece), every one in flight at once and no VGPR held.  The loop below
+// takes one memory round trip per float4 per thread (each ~1 µs when x comes
+// from L2 or the Infinity Cache: a 16-position router projection spent most
+// of its time there).
 template <int kKind, int kPad>
 __device__ __forceinline__ void stage_x(float* xs, const float* x, int cols, int p0, int pg,
                                         const float* norm_w, float eps, float* red) {
+  if (!norm_w && cols == kPad) {
+    constexpr int kPer = SpineElem<kKind>::kPerChunk;
+    constexpr int kQ = kPer / 4;
+    constexpr int kPieces = kPad / (64 * kPer);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n = pg * kPieces * kQ;  // one wave instruction each
+    for (int idx = (int)(threadIdx.x / kWave); idx < n; idx += kSpineWaves) {
+      const int p = idx / (kPieces * kQ);
+      const int jq = idx - p * (kPieces * kQ);  // piece j * kQ + quarter q
+      const int j = jq / kQ, q = jq - j * kQ;
+      const float* src = x + (uint64_t)(p0 + p) * cols + j * 64 * kPer + lane * kPer + 4 * q;
+      float* dst = xs + p * kPad + jq * 64 * 4;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0,
+                                       0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS writes have landed
+    __syncthreads();
+    return;
+  }
   for (int p = 0; p < pg; ++p) {
     const float* xp = x + (uint64_t)(p0 + p) * cols;
     float r = 1.f;
