@@ -172,7 +172,15 @@ __global__ __launch_bounds__(256) void k_gemv_multi(const uint8_t* __restrict__ 
     __syncthreads();
     const int n16 = (int)((size_t)nb * cols * sizeof(XT) / 16);
     const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)b0 * cols);
-    for (int i = threadIdx.x; i < n16; i += blockDim.x) smem_multi[i] = src[i];
+    // Straight to LDS (global_load_lds_dwordx4: a wave's 64 lanes fill 1 KB),
+    // every copy in flight at once; vmcnt(0) before the barrier.
+    for (int i0 = (int)threadIdx.x & ~63; i0 < n16; i0 += blockDim.x) {
+      const int i = i0 + lane;
+      if (i < n16)
+        __builtin_amdgcn_global_load_lds(src + i, (__attribute__((address_space(3))) void*)(smem_multi + i0),
+                                         16, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     for (int r = 0; r < kRows; ++r) {
       const int row = r0 + r;
