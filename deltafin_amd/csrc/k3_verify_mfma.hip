@@ -476,13 +476,19 @@ __global__ __launch_bounds__(256, 2) void k_verify_mfma(const Geo g, const Works
 // ======================================================================
 namespace {
 
-// 8-row tiles per unit: of gate and of up (4: 32 rows each with bf16 x, 2
-// with fp32 x's three terms), and of down (7: 56 rows, where the hidden size
-// allows, else 4).  Each keeps two items of weights and one of activation
-// terms within the 256 VGPRs of two waves per SIMD without spilling.
+// 8-row tiles per unit: of gate and of up (4: 32 rows each, with bf16 x's
+// two terms and with fp32 x's three), and of down (7: 56 rows, where the
+// hidden size allows, else 4).  Each keeps two items of weights and one of
+// activation terms within the 256 VGPRs of two waves per SIMD without
+// spilling (fp32 x at 4 tiles: 253).  Fp32 x at 2 tiles (16 rows each, half
+// the weights in flight per wave) ran the K3 block's 16-position gate/up at
+// 607-634 µs against 465 µs at 4.
+#ifndef K3_MFMA_GLU3_TILES
+#define K3_MFMA_GLU3_TILES 4
+#endif
 template <bool kGlu, int T>
 constexpr int glu_tiles() {
-  return T == 2 ? 4 : 2;
+  return T == 2 ? 4 : K3_MFMA_GLU3_TILES;
 }
 int down_tiles(const Geo& g) { return g.hidden % 56 == 0 ? 7 : 4; }
 
