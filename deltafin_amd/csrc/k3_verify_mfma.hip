@@ -477,12 +477,13 @@ __global__ __launch_bounds__(256, 2) void k_verify_mfma(const Geo g, const Works
 namespace {
 
 // 8-row tiles per unit: of gate and of up (4: 32 rows each, with bf16 x's
-// two terms and with fp32 x's three), and of down (7: 56 rows, where the
+// two terms and with fp32 x's three), and of down (8: 64 rows, where the
 // hidden size allows, else 4).  Each keeps two items of weights and one of
 // activation terms within the 256 VGPRs of two waves per SIMD without
-// spilling (fp32 x at 4 tiles: 253).  Fp32 x at 2 tiles (16 rows each, half
-// the weights in flight per wave) ran the K3 block's 16-position gate/up at
-// 607-634 µs against 465 µs at 4.
+// spilling (fp32 x at 4 tiles: 253, down at 8: 246).  More weight bytes per
+// item measured faster: fp32 x at 2 tiles (16 rows each) ran the K3 block's
+// 16-position gate/up at 607-634 µs against 465 µs at 4, and down at 7 tiles
+// the preset-2 16-position verify's down at 288-289 µs against 266 at 8.
 #ifndef K3_MFMA_GLU3_TILES
 #define K3_MFMA_GLU3_TILES 4
 #endif
@@ -490,7 +491,12 @@ template <bool kGlu, int T>
 constexpr int glu_tiles() {
   return T == 2 ? 4 : K3_MFMA_GLU3_TILES;
 }
-int down_tiles(const Geo& g) { return g.hidden % 56 == 0 ? 7 : 4; }
+#ifndef K3_MFMA_DOWN_TILES
+#define K3_MFMA_DOWN_TILES 8
+#endif
+int down_tiles(const Geo& g) {
+  return g.hidden % (8 * K3_MFMA_DOWN_TILES) == 0 ? K3_MFMA_DOWN_TILES : 4;
+}
 
 #ifndef K3_MFMA_GLU_WAVES
 #define K3_MFMA_GLU_WAVES 4
@@ -581,8 +587,9 @@ int launch_verify_mfma(const Geo& g, int n_edges, int n_positions, const void* x
   if (rc != K3_HIP_OK) return rc;
   rc = split_launch<3>(static_cast<const float*>(ws.h), n_edges, g.inter, ws.hq, ws.hqs, st);
   if (rc != K3_HIP_OK) return rc;
-  rc = down_tiles(g) == 7
-           ? mfma_launch<false, 7, 3>(g, n_edges, ws, ws.hq, ws.hqs, n_edges, ws.y, st)
+  rc = down_tiles(g) == K3_MFMA_DOWN_TILES
+           ? mfma_launch<false, K3_MFMA_DOWN_TILES, 3>(g, n_edges, ws, ws.hq, ws.hqs, n_edges,
+                                                       ws.y, st)
            : mfma_launch<false, 4, 3>(g, n_edges, ws, ws.hq, ws.hqs, n_edges, ws.y, st);
   if (rc != K3_HIP_OK) return rc;
   return launch_verify_combine(g, n_positions, out, out_dtype, ws, st);
