@@ -477,8 +477,9 @@ __global__ __launch_bounds__(256, 2) void k_verify_mfma(const Geo g, const Works
 namespace {
 
 // 8-row tiles per unit: of gate and of up (4: 32 rows each, with bf16 x's
-// two terms and with fp32 x's three), and of down (8: 64 rows, where the
-// hidden size allows, else 4).  Each keeps two items of weights and one of
+// two terms and with fp32 x's three), and of down (8: 64 rows; the path
+// takes hidden sizes that are multiples of 128, so these units always fit).
+// Each keeps two items of weights and one of
 // activation terms within the 256 VGPRs of two waves per SIMD without
 // spilling (fp32 x at 4 tiles: 253, down at 8: 246).  More weight bytes per
 // item measured faster: fp32 x at 2 tiles (16 rows each) ran the K3 block's
@@ -494,9 +495,7 @@ constexpr int glu_tiles() {
 #ifndef K3_MFMA_DOWN_TILES
 #define K3_MFMA_DOWN_TILES 8
 #endif
-int down_tiles(const Geo& g) {
-  return g.hidden % (8 * K3_MFMA_DOWN_TILES) == 0 ? K3_MFMA_DOWN_TILES : 4;
-}
+constexpr int kDownTiles = K3_MFMA_DOWN_TILES;
 
 #ifndef K3_MFMA_GLU_WAVES
 #define K3_MFMA_GLU_WAVES 4
@@ -556,13 +555,12 @@ int mfma_launch(const Geo& g, int n_edges, const Workspace& ws, const uint8_t* b
 
 bool verify_mfma_supported(const Geo& g) {
   // Whole K-step pairs (256 elements) per column wave, whole units of rows.
-  const int dt = down_tiles(g);
   return g.layout == K3_LAYOUT_RAW_V1 && g.hidden % 128 == 0 && g.inter % 128 == 0 &&
          g.inter % (8 * glu_tiles<true, 2>()) == 0 && g.inter % (8 * glu_tiles<true, 3>()) == 0 &&
-         g.hidden % (8 * dt) == 0 &&
+         g.hidden % (8 * kDownTiles) == 0 &&
          mfma_waves(g.hidden, 2 * glu_tiles<true, 2>(), K3_MFMA_GLU_WAVES) > 0 &&
          mfma_waves(g.hidden, 2 * glu_tiles<true, 3>(), K3_MFMA_GLU_WAVES) > 0 &&
-         mfma_waves(g.inter, dt, K3_MFMA_DOWN_WAVES) > 0;
+         mfma_waves(g.inter, kDownTiles, K3_MFMA_DOWN_WAVES) > 0;
 }
 
 int launch_verify_mfma(const Geo& g, int n_edges, int n_positions, const void* x, int x_dtype,
@@ -587,10 +585,7 @@ int launch_verify_mfma(const Geo& g, int n_edges, int n_positions, const void* x
   if (rc != K3_HIP_OK) return rc;
   rc = split_launch<3>(static_cast<const float*>(ws.h), n_edges, g.inter, ws.hq, ws.hqs, st);
   if (rc != K3_HIP_OK) return rc;
-  rc = down_tiles(g) == K3_MFMA_DOWN_TILES
-           ? mfma_launch<false, K3_MFMA_DOWN_TILES, 3>(g, n_edges, ws, ws.hq, ws.hqs, n_edges,
-                                                       ws.y, st)
-           : mfma_launch<false, 4, 3>(g, n_edges, ws, ws.hq, ws.hqs, n_edges, ws.y, st);
+  rc = mfma_launch<false, kDownTiles, 3>(g, n_edges, ws, ws.hq, ws.hqs, n_edges, ws.y, st);
   if (rc != K3_HIP_OK) return rc;
   return launch_verify_combine(g, n_positions, out, out_dtype, ws, st);
 }
