@@ -447,7 +447,9 @@ __device__ __forceinline__ uint32_t route_bases(const RouteRegs& rr, int n, int 
 
 __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
                            uint64_t* keys, int* sel, float* wsel, float pre = 0.0f,
-                           bool have_pre = false);
+                           bool have_pre = false, bool weights = true);
+__device__ void block_softmax(const uint64_t* keys, const int* sel, int top_k, float* wsel);
+__device__ __forceinline__ float key_value(uint64_t key);
 
 // The route as every wave of the workgroup holds it (lane e: expert e's span
 // and weight).  Router mode: the workgroup ranks the logits itself (no
@@ -614,18 +616,11 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
   RouteRegs rr;
   if (logits) {
     // Router mode: every workgroup ranks the logits itself (no separate
-    // launch); workgroup 0 publishes the route for the down kernel.
-    block_topk(logits, route.n_bank, route.n, route_scratch, sel, wsel, logit, pre);
-    if (blockIdx.x == 0) {
-      for (int j = threadIdx.x; j < route.n; j += blockDim.x) {
-        route.ids_pub[proute + j] = sel[j];
-        route.w_pub[proute + j] = wsel[j];
-        if (route.ids_user) route.ids_user[proute + j] = sel[j];
-        if (route.w_user) route.w_user[proute + j] = wsel[j];
-      }
-    }
+    // launch) and needs only the experts' ids; workgroup 0 publishes the
+    // route for the down kernel.
+    block_topk(logits, route.n_bank, route.n, route_scratch, sel, wsel, logit, pre, false);
     rr.lo = rr.hi = 0u;
-    rr.w = 0.0f;
+    rr.w = 0.0f;  // the gate/up units do not weight
     if (lane < route.n) {
       // The ranking writes every sel[j < n]; the clamp keeps a bank address
       // in range whatever LDS holds.
@@ -633,7 +628,25 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
       const uint64_t p = reinterpret_cast<uint64_t>(route.bank) + (uint64_t)id * route.stride;
       rr.lo = (uint32_t)p;
       rr.hi = (uint32_t)(p >> 32);
-      rr.w = wsel[lane];
+    }
+    if (blockIdx.x == 0 && wave == 0) {
+      // The route's softmax weights (only the down kernel uses them) and the
+      // published route: one wave, the same arithmetic as block_softmax, no
+      // barrier; the other workgroups skip them.
+      const int j = lane;
+      float ex = 0.0f;
+      if (j < route.n) {
+        const float top = key_value(route_scratch[sel[0]]);
+        ex = expf(key_value(route_scratch[sel[j]]) - top);
+      }
+      const float sum = wave_sum(ex);
+      if (j < route.n) {
+        const float wj = ex / sum;
+        route.ids_pub[proute + j] = sel[j];
+        route.w_pub[proute + j] = wj;
+        if (route.ids_user) route.ids_user[proute + j] = sel[j];
+        if (route.w_user) route.w_user[proute + j] = wj;
+      }
     }
   } else {
     rr = route_regs(route, lane, proute);
@@ -1436,7 +1449,8 @@ __device__ __forceinline__ uint64_t route_key(float v, int i) {
 // caller already loaded logit threadIdx.x into pre (issued ahead of its other
 // loads, so ranking starts as soon as the logits arrive).
 __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
-                           uint64_t* keys, int* sel, float* wsel, float pre, bool have_pre) {
+                           uint64_t* keys, int* sel, float* wsel, float pre, bool have_pre,
+                           bool weights) {
   const int nseg = (n_bank + 63) >> 6;
   const int ncand = nseg * top_k;
   const int ncand2 = (ncand + 1) & ~1;
@@ -1498,8 +1512,13 @@ __device__ void block_topk(const float* __restrict__ src, int n_bank, int top_k,
     }
   }
   __syncthreads();
-  // softmax over the selected logits: one wave, fixed summation order.  The
-  // logit is recovered from its key (no second global load).
+  if (weights) block_softmax(keys, sel, top_k, wsel);
+}
+
+// Softmax weights of the selected experts (keys and sel as block_topk leaves
+// them): one wave, fixed summation order; the logit is recovered from its key
+// (no second global load).  All threads call it.
+__device__ void block_softmax(const uint64_t* keys, const int* sel, int top_k, float* wsel) {
   if (threadIdx.x < 64) {
     const int j = threadIdx.x;
     float ex = 0.0f;
