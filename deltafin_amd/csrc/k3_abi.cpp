@@ -781,6 +781,44 @@ int from_spine(int rc, const char* step) {
               step, k3_hip_spine_last_error());
 }
 
+#ifndef K3_BLOCK_SIDE_STREAM
+#define K3_BLOCK_SIDE_STREAM 1
+#endif
+
+// The MoE block's second stream on one device (default priority,
+// non-blocking) and the events that fork work onto it from the caller's
+// stream and join it back; created on first use, kept for the process.
+// Null where HIP refused one of them: the block then runs on one stream.
+struct BlockSide {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t join = nullptr;
+  std::mutex mu;  // one record / wait / launch sequence at a time
+};
+
+BlockSide* block_side() {
+  if (!K3_BLOCK_SIDE_STREAM) return nullptr;
+  static std::mutex mu;
+  static std::unordered_map<int, BlockSide*> by_device;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = by_device.find(dev);
+  if (it != by_device.end()) return it->second;
+  BlockSide* bs = new BlockSide;
+  if (hipStreamCreateWithFlags(&bs->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&bs->fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&bs->join, hipEventDisableTiming) != hipSuccess) {
+    if (bs->join) (void)hipEventDestroy(bs->join);
+    if (bs->fork) (void)hipEventDestroy(bs->fork);
+    if (bs->stream) (void)hipStreamDestroy(bs->stream);
+    delete bs;
+    bs = nullptr;
+  }
+  by_device[dev] = bs;
+  return bs;
+}
+
 // The routed experts of P positions whose routes are already in ws.ids /
 // ws.w ([P][top_k]): the union path (plan + matrix-core or VALU kernels) when
 // the verify mode asks for it or AUTO expects the union to pay, else one
@@ -915,6 +953,58 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
       return rc;
     return K3_HIP_OK;
   }
+  // the shared expert: h = situ(gate, up), one launch reading each gate row
+  // and its up row together (two launches and the activation where the shape
+  // has no fused form); h overwrites gate
+  auto shared_glu = [&](hipStream_t s) -> int {
+    SpineOp glu{};
+    glu.w = sp.shared_gate;
+    glu.scales = sp.shared_gate_scales;
+    glu.w2 = sp.shared_up;
+    glu.scales2 = sp.shared_up_scales;
+    glu.act = K3_ACT_SITU;
+    glu.x = hidden;
+    glu.y = b.gate;
+    glu.rows = S;
+    glu.cols = H;
+    glu.positions = P;
+    int r = spine_gemv_op(kind, glu, s);
+    if (r == K3_SPINE_E_UNSUPPORTED) {
+      if ((r = from_spine(spine_gemv(kind, sp.shared_gate, sp.shared_gate_scales, hidden, b.gate,
+                                     S, H, P, false, s), "shared_gate")))
+        return r;
+      if ((r = from_spine(spine_gemv(kind, sp.shared_up, sp.shared_up_scales, hidden, b.up, S,
+                                     H, P, false, s), "shared_up")))
+        return r;
+      return launch_activation(b.gate, b.up, b.gate, (int64_t)P * S, K3_ACT_SITU, s);
+    }
+    return from_spine(r, "shared gate/up");
+  };
+  // It needs only the hidden rows, so it runs on the side stream where there
+  // is one, beside the router, the routed experts and routed_up (the two
+  // streams' kernels share the CUs and fill each other's ramps), and the
+  // caller's stream waits for it only before shared_down.  The next call's
+  // fork is recorded after this call's shared_down, so the side stream never
+  // overwrites h that is still to be read.  Every return after the fork
+  // joins first, so the caller's stream is never ahead of the side work.
+  BlockSide* side = block_side();
+  struct Join {
+    hipStream_t st;
+    BlockSide* side = nullptr;
+    ~Join() {
+      if (side) (void)hipStreamWaitEvent(st, side->join, 0);
+    }
+  } join{st};
+  if (side) {
+    std::lock_guard<std::mutex> lock(side->mu);
+    hipError_t e = hipEventRecord(side->fork, st);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
+    if (e != hipSuccess) return hip_fail("MoE block fork", e);
+    if ((rc = shared_glu(side->stream))) return rc;
+    if ((e = hipEventRecord(side->join, side->stream)) != hipSuccess)
+      return hip_fail("MoE block join", e);
+    join.side = side;
+  }
   // prepare: router logits and routed_down (one launch over both matrices,
   // which read the same hidden rows, where the shape allows), then the route
   SpineOp pre{};
@@ -947,33 +1037,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   if ((rc = experts_on_device_routes(g, bank, expert_stride, E, P, top_k, b.routed_in,
                                      b.routed_out, ws, st)))
     return rc;
-  // the shared expert: h = situ(gate, up), one launch reading each gate row
-  // and its up row together (two launches and the activation where the shape
-  // has no fused form); h overwrites gate
-  SpineOp glu{};
-  glu.w = sp.shared_gate;
-  glu.scales = sp.shared_gate_scales;
-  glu.w2 = sp.shared_up;
-  glu.scales2 = sp.shared_up_scales;
-  glu.act = K3_ACT_SITU;
-  glu.x = hidden;
-  glu.y = b.gate;
-  glu.rows = S;
-  glu.cols = H;
-  glu.positions = P;
-  rc = spine_gemv_op(kind, glu, st);
-  if (rc == K3_SPINE_E_UNSUPPORTED) {
-    if ((rc = from_spine(spine_gemv(kind, sp.shared_gate, sp.shared_gate_scales, hidden, b.gate,
-                                    S, H, P, false, st), "shared_gate")))
-      return rc;
-    if ((rc = from_spine(spine_gemv(kind, sp.shared_up, sp.shared_up_scales, hidden, b.up, S, H,
-                                    P, false, st), "shared_up")))
-      return rc;
-    if ((rc = launch_activation(b.gate, b.up, b.gate, (int64_t)P * S, K3_ACT_SITU, st)))
-      return rc;
-  } else if ((rc = from_spine(rc, "shared gate/up"))) {
-    return rc;
-  }
+  if (!side && (rc = shared_glu(st))) return rc;
   // complete: routed_up over the routed RMS norm (staged normalised by the
   // projection itself where the shape allows), + shared_down h (one fp32 add)
   SpineOp up{};
@@ -996,6 +1060,11 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
       return rc;
   } else if ((rc = from_spine(rc, "routed_up"))) {
     return rc;
+  }
+  if (join.side) {  // h from the side stream
+    join.side = nullptr;
+    const hipError_t e = hipStreamWaitEvent(st, side->join, 0);
+    if (e != hipSuccess) return hip_fail("MoE block join", e);
   }
   return from_spine(spine_gemv(kind, sp.shared_down, sp.shared_down_scales, b.gate, out, H, S, P,
                                true, st), "shared_down");
