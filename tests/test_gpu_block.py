@@ -20,7 +20,11 @@ moe_block_f64):
 * the route of a hidden row does not depend on the batch: the same rows at
   1, 4 and 16 positions route to the same experts with bit-identical weights;
 * 16 positions, where AUTO takes the union path: outputs equal the
-  one-decode-layer-per-position path's within 1e-4 normwise, same routes.
+  one-decode-layer-per-position path's within 1e-4 normwise, same routes;
+* calls at 1 and 2 positions back to back on one workspace with no
+  synchronisation between them (the shared expert's gate/up runs on the
+  library's side stream and joins before shared_down): every call's output
+  against the oracle.
 """
 import zlib
 
@@ -298,3 +302,33 @@ def test_block_unaligned_spine_falls_back(gpu, k3_bank, positions):
     got = out.cpu().numpy().astype(np.float64)
     for p in range(positions):
         assert _normwise(got[p], want[p]) <= 1e-3, f"position {p}"
+
+
+def test_block_back_to_back_calls_share_a_workspace(gpu, k3_bank):
+    """Four block calls (1, 2, 1 and 1 positions) queued back to back on one
+    workspace without a synchronisation between them: each call's shared h
+    comes from the side stream and is read by its own shared_down before the
+    next call's side work may overwrite it, so every output matches the
+    oracle as a lone call's does."""
+    import torch
+    from deltafin_amd import spine
+    g, bank, stride, span = k3_bank
+    say("block: back-to-back calls on one workspace (1, 2, 1, 1 positions)")
+    m = _k3_spine("bf16", 6161)
+    sp = _spine_from("bf16", m)
+    ws = spine.moe_block_workspace(sp, g, 2)
+    rng = np.random.default_rng(6161)
+    sizes = [1, 2, 1, 1]
+    hiddens = [rng.standard_normal((p, K3["hidden"]), dtype=np.float32) for p in sizes]
+    dev_rows = [_dev(h) for h in hiddens]
+    outs = [spine.moe_block(sp, g, bank, stride, d, workspace=ws) for d in dev_rows]
+    torch.cuda.synchronize()
+    for c, (h, (out, ids, wts)) in enumerate(zip(hiddens, outs)):
+        want, want_ids, want_w, _, mag = S.moe_block_f64("bf16", m, span, h, K3["inter"], 16,
+                                                         with_mag=True)
+        assert ids.cpu().numpy().tolist() == want_ids.tolist(), f"call {c}: route ids differ"
+        assert np.max(np.abs(wts.cpu().numpy() - want_w)) <= 1e-6
+        got = out.cpu().numpy().astype(np.float64)
+        for p in range(h.shape[0]):
+            err = oracle.cond_rel_err(got[p], want[p], mag[p], K3["routed"] + K3["shared"])
+            assert err <= 1e-3, f"call {c}, position {p}: cond rel err {err:.3e}"
