@@ -721,7 +721,8 @@ struct BlockBufs {
   float* routed_out;
   float* gate;
   float* up;
-  uint8_t* terms;  // BF16 activation terms of the matrix-core spine (P >= 3)
+  uint8_t* terms;   // BF16 activation terms of the matrix-core spine (P >= 3)
+  uint8_t* terms2;  // the hidden rows' terms for the side stream's shared gate/up
 };
 
 uint64_t block_layout(const K3HipMoeSpineV1& sp, const Geo& g, int max_positions,
@@ -746,6 +747,8 @@ uint64_t block_layout(const K3HipMoeSpineV1& sp, const Geo& g, int max_positions
   const int wmax = (int)std::max(sp.hidden, std::max(sp.routed_hidden, sp.shared_intermediate));
   if (b) b->terms = base + off;
   off += align256(spine_mfma_terms_bytes(max_positions, wmax));
+  if (b) b->terms2 = base + off;
+  off += align256(spine_mfma_terms_bytes(max_positions, (int)sp.hidden));
   return off;
 }
 
@@ -909,6 +912,39 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   const int P = n_positions, H = (int)sp.hidden, R = (int)sp.routed_hidden;
   const int S = (int)sp.shared_intermediate, E = (int)sp.experts;
   int rc;
+  // The shared expert's gate/up needs only the hidden rows, so it runs on the
+  // side stream where there is one, beside the router, the routed experts and
+  // routed_up (the two streams' kernels share the CUs and fill each other's
+  // ramps), and the caller's stream waits for it only before shared_down.
+  // The next call's fork is recorded after this call's shared_down, so the
+  // side stream never overwrites h that is still to be read.  Every return
+  // after the fork joins first, so the caller's stream is never ahead of the
+  // side work.
+  BlockSide* side = block_side();
+  struct Join {
+    hipStream_t st;
+    BlockSide* side = nullptr;
+    ~Join() {
+      if (side) (void)hipStreamWaitEvent(st, side->join, 0);
+    }
+  } join{st};
+  auto fork = [&](auto&& work) -> int {
+    std::lock_guard<std::mutex> lock(side->mu);
+    hipError_t e = hipEventRecord(side->fork, st);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
+    if (e != hipSuccess) return hip_fail("MoE block fork", e);
+    if (const int r = work(side->stream)) return r;
+    if ((e = hipEventRecord(side->join, side->stream)) != hipSuccess)
+      return hip_fail("MoE block join", e);
+    join.side = side;
+    return K3_HIP_OK;
+  };
+  auto join_side = [&]() -> int {
+    if (!join.side) return K3_HIP_OK;
+    join.side = nullptr;
+    const hipError_t e = hipStreamWaitEvent(st, side->join, 0);
+    return e == hipSuccess ? K3_HIP_OK : hip_fail("MoE block join", e);
+  };
   // 3..16 positions of a BF16 spine: every projection on the matrix cores
   // from BF16 activation terms (the fp32 kernels are bound by LDS and FMAs
   // there); the steps and their order are the same.
@@ -920,22 +956,37 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   if (P >= K3_SPINE_MFMA_MIN_POSITIONS && kind == K3_SPINE_KIND_BF16 && matrices_aligned &&
       spine_mfma_supported(kind, P, R, H) && spine_mfma_supported(kind, P, S, H) &&
       spine_mfma_supported(kind, P, H, R) && spine_mfma_supported(kind, P, H, S)) {
-    auto mm = [&](const void* w, float* y, int rows, int cols, bool acc, const char* step) {
-      return from_spine(spine_mfma_gemv(w, b.terms, y, rows, cols, P, acc, st), step);
+    auto mm = [&](const void* w, const uint8_t* terms, float* y, int rows, int cols, bool acc,
+                  hipStream_t s, const char* step) {
+      return from_spine(spine_mfma_gemv(w, terms, y, rows, cols, P, acc, s), step);
     };
-    auto split = [&](const float* x, int cols) {
-      return from_spine(spine_mfma_split(x, P, cols, b.terms, st), "term split");
+    auto split = [&](const float* x, int cols, uint8_t* terms, hipStream_t s) {
+      return from_spine(spine_mfma_split(x, P, cols, terms, s), "term split");
     };
+    // shared gate and up from the hidden rows' terms (already split into
+    // `terms` when `split_first` is false), then h = situ(gate, up)
+    auto shared_glu = [&](uint8_t* terms, bool split_first, hipStream_t s) -> int {
+      int r;
+      if ((split_first && (r = split(hidden, H, terms, s))) ||
+          (r = mm(sp.shared_gate, terms, b.gate, S, H, false, s, "shared_gate")) ||
+          (r = mm(sp.shared_up, terms, b.up, S, H, false, s, "shared_up")))
+        return r;
+      return launch_activation(b.gate, b.up, b.gate, (int64_t)P * S, K3_ACT_SITU, s);
+    };
+    // With the side stream the shared expert reads its own copy of the hidden
+    // rows' terms (the main stream's buffer is reused for the routed output
+    // and h while the side work may still run).
+    if (side && (rc = fork([&](hipStream_t s) { return shared_glu(b.terms2, true, s); })))
+      return rc;
     // The router logits stay on the fp32 kernels at every P: each position's
     // logit is then summed in the same order whatever the batch (the fp32
     // spine kernels reduce every (row, position) identically), so a hidden row
     // routes to the same experts in a 1-token decode and in a verify batch.
     if ((rc = from_spine(spine_gemv(kind, sp.router, sp.router_scales, hidden, b.logits, E, H, P,
                                     false, st), "router")) ||
-        (rc = split(hidden, H)) ||
-        (rc = mm(sp.routed_down, b.routed_in, R, H, false, "routed_down")) ||
-        (rc = mm(sp.shared_gate, b.gate, S, H, false, "shared_gate")) ||
-        (rc = mm(sp.shared_up, b.up, S, H, false, "shared_up")))
+        (rc = split(hidden, H, b.terms, st)) ||
+        (rc = mm(sp.routed_down, b.terms, b.routed_in, R, H, false, st, "routed_down")) ||
+        (!side && (rc = shared_glu(b.terms, false, st))))
       return rc;
     if ((rc = launch_route_sigmoid_bias(b.logits, sp.router_bias, E, top_k, P, ws.ids, ws.w,
                                         route_ids, route_weights, st)))
@@ -943,13 +994,13 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
     if ((rc = experts_on_device_routes(g, bank, expert_stride, E, P, top_k, b.routed_in,
                                        b.routed_out, ws, st)))
       return rc;
-    if ((rc = launch_activation(b.gate, b.up, b.gate, (int64_t)P * S, K3_ACT_SITU, st)))
-      return rc;
     if ((rc = from_spine(spine_rms_norm(b.routed_out, sp.routed_norm, b.routed_out, P, R,
                                         K3_RMS_EPSILON, st), "routed RMS norm")))
       return rc;
-    if ((rc = split(b.routed_out, R)) || (rc = mm(sp.routed_up, out, H, R, false, "routed_up")) ||
-        (rc = split(b.gate, S)) || (rc = mm(sp.shared_down, out, H, S, true, "shared_down")))
+    if ((rc = split(b.routed_out, R, b.terms, st)) ||
+        (rc = mm(sp.routed_up, b.terms, out, H, R, false, st, "routed_up")) ||
+        (rc = join_side()) || (rc = split(b.gate, S, b.terms, st)) ||
+        (rc = mm(sp.shared_down, b.terms, out, H, S, true, st, "shared_down")))
       return rc;
     return K3_HIP_OK;
   }
@@ -980,31 +1031,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
     }
     return from_spine(r, "shared gate/up");
   };
-  // It needs only the hidden rows, so it runs on the side stream where there
-  // is one, beside the router, the routed experts and routed_up (the two
-  // streams' kernels share the CUs and fill each other's ramps), and the
-  // caller's stream waits for it only before shared_down.  The next call's
-  // fork is recorded after this call's shared_down, so the side stream never
-  // overwrites h that is still to be read.  Every return after the fork
-  // joins first, so the caller's stream is never ahead of the side work.
-  BlockSide* side = block_side();
-  struct Join {
-    hipStream_t st;
-    BlockSide* side = nullptr;
-    ~Join() {
-      if (side) (void)hipStreamWaitEvent(st, side->join, 0);
-    }
-  } join{st};
-  if (side) {
-    std::lock_guard<std::mutex> lock(side->mu);
-    hipError_t e = hipEventRecord(side->fork, st);
-    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
-    if (e != hipSuccess) return hip_fail("MoE block fork", e);
-    if ((rc = shared_glu(side->stream))) return rc;
-    if ((e = hipEventRecord(side->join, side->stream)) != hipSuccess)
-      return hip_fail("MoE block join", e);
-    join.side = side;
-  }
+  if (side && (rc = fork(shared_glu))) return rc;
   // prepare: router logits and routed_down (one launch over both matrices,
   // which read the same hidden rows, where the shape allows), then the route
   SpineOp pre{};
@@ -1061,11 +1088,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   } else if ((rc = from_spine(rc, "routed_up"))) {
     return rc;
   }
-  if (join.side) {  // h from the side stream
-    join.side = nullptr;
-    const hipError_t e = hipStreamWaitEvent(st, side->join, 0);
-    if (e != hipSuccess) return hip_fail("MoE block join", e);
-  }
+  if ((rc = join_side())) return rc;  // h from the side stream
   return from_spine(spine_gemv(kind, sp.shared_down, sp.shared_down_scales, b.gate, out, H, S, P,
                                true, st), "shared_down");
 }

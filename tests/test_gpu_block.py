@@ -24,7 +24,8 @@ moe_block_f64):
 * calls at 1 and 2 positions back to back on one workspace with no
   synchronisation between them (the shared expert's gate/up runs on the
   library's side stream and joins before shared_down): every call's output
-  against the oracle.
+  against the oracle (the other cases exercise the side stream at every
+  position count).
 """
 import zlib
 
