@@ -21,7 +21,7 @@ moe_block_f64):
   1, 4 and 16 positions route to the same experts with bit-identical weights;
 * 16 positions, where AUTO takes the union path: outputs equal the
   one-decode-layer-per-position path's within 1e-4 normwise, same routes;
-* calls at 1 and 2 positions back to back on one workspace with no
+* calls at 1, 2 and 4 positions back to back on one workspace with no
   synchronisation between them (the shared expert's gate/up runs on the
   library's side stream and joins before shared_down): every call's output
   against the oracle (the other cases exercise the side stream at every
@@ -306,7 +306,7 @@ def test_block_unaligned_spine_falls_back(gpu, k3_bank, positions):
 
 
 def test_block_back_to_back_calls_share_a_workspace(gpu, k3_bank):
-    """Four block calls (1, 2, 1 and 1 positions) queued back to back on one
+    """Four block calls (1, 2, 4 and 1 positions) queued back to back on one
     workspace without a synchronisation between them: each call's shared h
     comes from the side stream and is read by its own shared_down before the
     next call's side work may overwrite it, so every output matches the
@@ -314,12 +314,12 @@ def test_block_back_to_back_calls_share_a_workspace(gpu, k3_bank):
     import torch
     from deltafin_amd import spine
     g, bank, stride, span = k3_bank
-    say("block: back-to-back calls on one workspace (1, 2, 1, 1 positions)")
+    say("block: back-to-back calls on one workspace (1, 2, 4, 1 positions)")
     m = _k3_spine("bf16", 6161)
     sp = _spine_from("bf16", m)
-    ws = spine.moe_block_workspace(sp, g, 2)
+    ws = spine.moe_block_workspace(sp, g, 4)
     rng = np.random.default_rng(6161)
-    sizes = [1, 2, 1, 1]
+    sizes = [1, 2, 4, 1]
     hiddens = [rng.standard_normal((p, K3["hidden"]), dtype=np.float32) for p in sizes]
     dev_rows = [_dev(h) for h in hiddens]
     outs = [spine.moe_block(sp, g, bank, stride, d, workspace=ws) for d in dev_rows]
