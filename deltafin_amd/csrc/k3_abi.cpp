@@ -45,6 +45,89 @@ int hip_fail(const char* what, hipError_t e) {
   return fail(K3_HIP_E_EXEC, "%s: %s", what, hipGetErrorString(e));
 }
 
+#ifndef K3_SIDE_STREAM
+#define K3_SIDE_STREAM 1  // 0: everything on the caller's stream
+#endif
+
+// The library's second stream on one device (default priority,
+// non-blocking) and the events that fork work onto it from the caller's
+// stream and join it back; created on first use, kept for the process.
+// Null where HIP refused one of them: everything then runs on the caller's stream.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t join = nullptr;
+  std::mutex mu;  // one record / wait / launch sequence at a time
+};
+
+SideStream* side_stream() {
+  if (!K3_SIDE_STREAM) return nullptr;
+  static std::mutex mu;
+  static std::unordered_map<int, SideStream*> by_device;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = by_device.find(dev);
+  if (it != by_device.end()) return it->second;
+  SideStream* bs = new SideStream;
+  if (hipStreamCreateWithFlags(&bs->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&bs->fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&bs->join, hipEventDisableTiming) != hipSuccess) {
+    if (bs->join) (void)hipEventDestroy(bs->join);
+    if (bs->fork) (void)hipEventDestroy(bs->fork);
+    if (bs->stream) (void)hipStreamDestroy(bs->stream);
+    delete bs;
+    bs = nullptr;
+  }
+  by_device[dev] = bs;
+  return bs;
+}
+
+// Work forked from the caller's stream onto the side stream and joined back:
+// fork records an event on the caller's stream, the side stream waits on it
+// and runs `work`, and an event records its end; join makes the caller's
+// stream wait for that event.  A SideWork that forked and was not joined
+// joins when it goes out of scope, so no return leaves the caller's stream
+// ahead of the side work.  Without a side stream, fork runs `work` on the
+// caller's stream.
+class SideWork {
+ public:
+  explicit SideWork(hipStream_t st) : st_(st), side_(side_stream()) {}
+  ~SideWork() {
+    if (pending_) (void)hipStreamWaitEvent(st_, side_->join, 0);
+  }
+  SideWork(const SideWork&) = delete;
+  SideWork& operator=(const SideWork&) = delete;
+  bool parallel() const { return side_ != nullptr; }
+  template <typename F>
+  int fork(F&& work) {
+    if (!side_) return work(st_);
+    std::lock_guard<std::mutex> lock(side_->mu);
+    hipError_t e = hipEventRecord(side_->fork, st_);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side_->stream, side_->fork, 0);
+    if (e != hipSuccess) return hip_fail("side stream fork", e);
+    // The join event is recorded whether or not `work` launched everything,
+    // so an error return still joins what it did launch.
+    const int r = work(side_->stream);
+    if ((e = hipEventRecord(side_->join, side_->stream)) != hipSuccess)
+      return hip_fail("side stream join", e);
+    pending_ = true;
+    return r;
+  }
+  int join() {
+    if (!pending_) return K3_HIP_OK;
+    pending_ = false;
+    const hipError_t e = hipStreamWaitEvent(st_, side_->join, 0);
+    return e == hipSuccess ? K3_HIP_OK : hip_fail("side stream join", e);
+  }
+
+ private:
+  hipStream_t st_;
+  SideStream* side_;
+  bool pending_ = false;
+};
+
+
 // ---------------------------------------------------------------- geometry
 bool make_geo(const K3HipGeometryV1* d, Geo* out) {
   if (!d || d->abi_version != 1 || d->struct_bytes != sizeof(K3HipGeometryV1) ||
@@ -784,44 +867,6 @@ int from_spine(int rc, const char* step) {
               step, k3_hip_spine_last_error());
 }
 
-#ifndef K3_BLOCK_SIDE_STREAM
-#define K3_BLOCK_SIDE_STREAM 1
-#endif
-
-// The MoE block's second stream on one device (default priority,
-// non-blocking) and the events that fork work onto it from the caller's
-// stream and join it back; created on first use, kept for the process.
-// Null where HIP refused one of them: the block then runs on one stream.
-struct BlockSide {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr;
-  hipEvent_t join = nullptr;
-  std::mutex mu;  // one record / wait / launch sequence at a time
-};
-
-BlockSide* block_side() {
-  if (!K3_BLOCK_SIDE_STREAM) return nullptr;
-  static std::mutex mu;
-  static std::unordered_map<int, BlockSide*> by_device;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = by_device.find(dev);
-  if (it != by_device.end()) return it->second;
-  BlockSide* bs = new BlockSide;
-  if (hipStreamCreateWithFlags(&bs->stream, hipStreamNonBlocking) != hipSuccess ||
-      hipEventCreateWithFlags(&bs->fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&bs->join, hipEventDisableTiming) != hipSuccess) {
-    if (bs->join) (void)hipEventDestroy(bs->join);
-    if (bs->fork) (void)hipEventDestroy(bs->fork);
-    if (bs->stream) (void)hipStreamDestroy(bs->stream);
-    delete bs;
-    bs = nullptr;
-  }
-  by_device[dev] = bs;
-  return bs;
-}
-
 // The routed experts of P positions whose routes are already in ws.ids /
 // ws.w ([P][top_k]): the union path (plan + matrix-core or VALU kernels) when
 // the verify mode asks for it or AUTO expects the union to pay, else one
@@ -920,31 +965,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   // side stream never overwrites h that is still to be read.  Every return
   // after the fork joins first, so the caller's stream is never ahead of the
   // side work.
-  BlockSide* side = block_side();
-  struct Join {
-    hipStream_t st;
-    BlockSide* side = nullptr;
-    ~Join() {
-      if (side) (void)hipStreamWaitEvent(st, side->join, 0);
-    }
-  } join{st};
-  auto fork = [&](auto&& work) -> int {
-    std::lock_guard<std::mutex> lock(side->mu);
-    hipError_t e = hipEventRecord(side->fork, st);
-    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
-    if (e != hipSuccess) return hip_fail("MoE block fork", e);
-    if (const int r = work(side->stream)) return r;
-    if ((e = hipEventRecord(side->join, side->stream)) != hipSuccess)
-      return hip_fail("MoE block join", e);
-    join.side = side;
-    return K3_HIP_OK;
-  };
-  auto join_side = [&]() -> int {
-    if (!join.side) return K3_HIP_OK;
-    join.side = nullptr;
-    const hipError_t e = hipStreamWaitEvent(st, side->join, 0);
-    return e == hipSuccess ? K3_HIP_OK : hip_fail("MoE block join", e);
-  };
+  SideWork side(st);
   // 3..16 positions of a BF16 spine: every projection on the matrix cores
   // from BF16 activation terms (the fp32 kernels are bound by LDS and FMAs
   // there); the steps and their order are the same.
@@ -976,7 +997,8 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
     // With the side stream the shared expert reads its own copy of the hidden
     // rows' terms (the main stream's buffer is reused for the routed output
     // and h while the side work may still run).
-    if (side && (rc = fork([&](hipStream_t s) { return shared_glu(b.terms2, true, s); })))
+    if (side.parallel() &&
+        (rc = side.fork([&](hipStream_t s) { return shared_glu(b.terms2, true, s); })))
       return rc;
     // The router logits stay on the fp32 kernels at every P: each position's
     // logit is then summed in the same order whatever the batch (the fp32
@@ -986,7 +1008,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
                                     false, st), "router")) ||
         (rc = split(hidden, H, b.terms, st)) ||
         (rc = mm(sp.routed_down, b.terms, b.routed_in, R, H, false, st, "routed_down")) ||
-        (!side && (rc = shared_glu(b.terms, false, st))))
+        (!side.parallel() && (rc = shared_glu(b.terms, false, st))))
       return rc;
     if ((rc = launch_route_sigmoid_bias(b.logits, sp.router_bias, E, top_k, P, ws.ids, ws.w,
                                         route_ids, route_weights, st)))
@@ -999,7 +1021,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
       return rc;
     if ((rc = split(b.routed_out, R, b.terms, st)) ||
         (rc = mm(sp.routed_up, b.terms, out, H, R, false, st, "routed_up")) ||
-        (rc = join_side()) || (rc = split(b.gate, S, b.terms, st)) ||
+        (rc = side.join()) || (rc = split(b.gate, S, b.terms, st)) ||
         (rc = mm(sp.shared_down, b.terms, out, H, S, true, st, "shared_down")))
       return rc;
     return K3_HIP_OK;
@@ -1031,7 +1053,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
     }
     return from_spine(r, "shared gate/up");
   };
-  if (side && (rc = fork(shared_glu))) return rc;
+  if (side.parallel() && (rc = side.fork(shared_glu))) return rc;
   // prepare: router logits and routed_down (one launch over both matrices,
   // which read the same hidden rows, where the shape allows), then the route
   SpineOp pre{};
@@ -1064,7 +1086,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   if ((rc = experts_on_device_routes(g, bank, expert_stride, E, P, top_k, b.routed_in,
                                      b.routed_out, ws, st)))
     return rc;
-  if (!side && (rc = shared_glu(st))) return rc;
+  if (!side.parallel() && (rc = shared_glu(st))) return rc;
   // complete: routed_up over the routed RMS norm (staged normalised by the
   // projection itself where the shape allows), + shared_down h (one fp32 add)
   SpineOp up{};
@@ -1088,7 +1110,7 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
   } else if ((rc = from_spine(rc, "routed_up"))) {
     return rc;
   }
-  if ((rc = join_side())) return rc;  // h from the side stream
+  if ((rc = side.join())) return rc;  // h from the side stream
   return from_spine(spine_gemv(kind, sp.shared_down, sp.shared_down_scales, b.gate, out, H, S, P,
                                true, st), "shared_down");
 }
