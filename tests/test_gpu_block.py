@@ -25,7 +25,10 @@ moe_block_f64):
   synchronisation between them (the shared expert's gate/up runs on the
   library's side stream and joins before shared_down): every call's output
   against the oracle (the other cases exercise the side stream at every
-  position count).
+  position count);
+* two host threads, each on its own stream and workspace, issuing block calls
+  at the same time (their side work shares the library's side stream): every
+  output against the oracle.
 """
 import zlib
 
@@ -333,3 +336,55 @@ def test_block_back_to_back_calls_share_a_workspace(gpu, k3_bank):
         for p in range(h.shape[0]):
             err = oracle.cond_rel_err(got[p], want[p], mag[p], K3["routed"] + K3["shared"])
             assert err <= 1e-3, f"call {c}, position {p}: cond rel err {err:.3e}"
+
+
+def test_block_two_threads_two_streams(gpu, k3_bank):
+    """Two host threads, each with its own torch stream and workspace, queue
+    three 1-position block calls each at the same time; the library's side
+    stream (shared by both) runs their shared experts.  Every output matches
+    the oracle."""
+    import threading
+
+    import torch
+    from deltafin_amd import spine
+    g, bank, stride, span = k3_bank
+    say("block: two host threads on two streams, three calls each")
+    m = _k3_spine("bf16", 7272)
+    sp = _spine_from("bf16", m)
+    rng = np.random.default_rng(7272)
+    rows = [[rng.standard_normal((1, K3["hidden"]), dtype=np.float32) for _ in range(3)]
+            for _ in range(2)]
+    dev_rows = [[_dev(h) for h in per] for per in rows]
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    wss = [spine.moe_block_workspace(sp, g, 1) for _ in range(2)]
+    torch.cuda.synchronize()
+    results = [[None] * 3 for _ in range(2)]
+    errors = []
+
+    def worker(t):
+        try:
+            with torch.cuda.stream(streams[t]):
+                for c in range(3):
+                    results[t][c] = spine.moe_block(sp, g, bank, stride, dev_rows[t][c],
+                                                    workspace=wss[t])
+        except Exception as e:  # reported after the join
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not any(th.is_alive() for th in threads), "a host thread did not finish"
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for t in range(2):
+        for c in range(3):
+            out, ids, wts = results[t][c]
+            want, want_ids, want_w, _, mag = S.moe_block_f64("bf16", m, span, rows[t][c],
+                                                             K3["inter"], 16, with_mag=True)
+            assert ids.cpu().numpy().tolist() == want_ids.tolist(), f"thread {t} call {c}: ids"
+            assert np.max(np.abs(wts.cpu().numpy() - want_w)) <= 1e-6
+            err = oracle.cond_rel_err(out.cpu().numpy().astype(np.float64)[0], want[0], mag[0],
+                                      K3["routed"] + K3["shared"])
+            assert err <= 1e-3, f"thread {t} call {c}: cond rel err {err:.3e}"
