@@ -118,7 +118,7 @@ class K3HipCachePolicyV1(C.Structure):
 
 
 K3_CACHE_RESERVE_AUTO, K3_CACHE_RESERVE_BYTES, K3_CACHE_RESERVE_RATIO_PPM = 0, 1, 2
-K3_HIP_CACHE_MAX_EXPERTS = 65536
+K3_HIP_CACHE_MAX_EXPERTS = 1472  # 92 strata x 16 (provider_cuda_moe.cpp:55-57)
 assert C.sizeof(K3HipCachePolicyV1) == 32
 
 assert C.sizeof(K3HipMoeSpineV1) == 144

@@ -50,14 +50,15 @@ int hip_fail(const char* what, hipError_t e) {
 #endif
 
 // The library's second stream on one device (default priority,
-// non-blocking) and the events that fork work onto it from the caller's
-// stream and join it back; created on first use, kept for the process.
-// Null where HIP refused one of them: everything then runs on the caller's stream.
+// non-blocking), the event that forks work onto it from a caller's stream and
+// a pool of join events; created on first use, kept for the process.  Null
+// where HIP refused the stream or the fork event: everything then runs on the
+// caller's stream.
 struct SideStream {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr;
-  hipEvent_t join = nullptr;
-  std::mutex mu;  // one record / wait / launch sequence at a time
+  std::vector<hipEvent_t> free_joins;  // join events not held by a fork
+  std::mutex mu;  // one record / wait / launch sequence at a time; the pool
 };
 
 SideStream* side_stream() {
@@ -71,9 +72,7 @@ SideStream* side_stream() {
   if (it != by_device.end()) return it->second;
   SideStream* bs = new SideStream;
   if (hipStreamCreateWithFlags(&bs->stream, hipStreamNonBlocking) != hipSuccess ||
-      hipEventCreateWithFlags(&bs->fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&bs->join, hipEventDisableTiming) != hipSuccess) {
-    if (bs->join) (void)hipEventDestroy(bs->join);
+      hipEventCreateWithFlags(&bs->fork, hipEventDisableTiming) != hipSuccess) {
     if (bs->fork) (void)hipEventDestroy(bs->fork);
     if (bs->stream) (void)hipStreamDestroy(bs->stream);
     delete bs;
@@ -85,46 +84,73 @@ SideStream* side_stream() {
 
 // Work forked from the caller's stream onto the side stream and joined back:
 // fork records an event on the caller's stream, the side stream waits on it
-// and runs `work`, and an event records its end; join makes the caller's
-// stream wait for that event.  A SideWork that forked and was not joined
+// and runs `work`, and a join event of this fork's own (taken from the pool
+// while the side stream's mutex is held) records its end; join makes the
+// caller's stream wait for exactly that event and returns it to the pool (a
+// queued wait keeps the record it saw, so the event may be recorded again).
+// Another caller's fork therefore never joins this one, and a caller waits
+// only for its own side work.  A SideWork that forked and was not joined
 // joins when it goes out of scope, so no return leaves the caller's stream
-// ahead of the side work.  Without a side stream, fork runs `work` on the
-// caller's stream.
+// ahead of the side work.  The work runs on the caller's stream instead when
+// there is no side stream, when no join event could be had, or when the
+// caller's stream is being captured into a graph: the shared side stream
+// never joins a capture, so another thread's call cannot land in it.
 class SideWork {
  public:
   explicit SideWork(hipStream_t st) : st_(st), side_(side_stream()) {}
-  ~SideWork() {
-    if (pending_) (void)hipStreamWaitEvent(st_, side_->join, 0);
-  }
+  ~SideWork() { (void)join(); }
   SideWork(const SideWork&) = delete;
   SideWork& operator=(const SideWork&) = delete;
   bool parallel() const { return side_ != nullptr; }
   template <typename F>
   int fork(F&& work) {
     if (!side_) return work(st_);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st_, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+      return work(st_);
     std::lock_guard<std::mutex> lock(side_->mu);
+    hipEvent_t done = nullptr;
+    if (!side_->free_joins.empty()) {
+      done = side_->free_joins.back();
+      side_->free_joins.pop_back();
+    } else if (hipEventCreateWithFlags(&done, hipEventDisableTiming) != hipSuccess) {
+      return work(st_);
+    }
     hipError_t e = hipEventRecord(side_->fork, st_);
     if (e == hipSuccess) e = hipStreamWaitEvent(side_->stream, side_->fork, 0);
-    if (e != hipSuccess) return hip_fail("side stream fork", e);
+    if (e != hipSuccess) {
+      side_->free_joins.push_back(done);
+      return hip_fail("side stream fork", e);
+    }
     // The join event is recorded whether or not `work` launched everything,
     // so an error return still joins what it did launch.
     const int r = work(side_->stream);
-    if ((e = hipEventRecord(side_->join, side_->stream)) != hipSuccess)
+    if ((e = hipEventRecord(done, side_->stream)) != hipSuccess) {
+      // Nothing to wait on: drain the side stream so no side work outlives
+      // the call unjoined.
+      (void)hipStreamSynchronize(side_->stream);
+      side_->free_joins.push_back(done);
       return hip_fail("side stream join", e);
-    pending_ = true;
+    }
+    done_ = done;
     return r;
   }
   int join() {
-    if (!pending_) return K3_HIP_OK;
-    pending_ = false;
-    const hipError_t e = hipStreamWaitEvent(st_, side_->join, 0);
+    if (!done_) return K3_HIP_OK;
+    const hipError_t e = hipStreamWaitEvent(st_, done_, 0);
+    if (e != hipSuccess) (void)hipEventSynchronize(done_);  // the host waits instead
+    {
+      std::lock_guard<std::mutex> lock(side_->mu);
+      side_->free_joins.push_back(done_);
+    }
+    done_ = nullptr;
     return e == hipSuccess ? K3_HIP_OK : hip_fail("side stream join", e);
   }
 
  private:
   hipStream_t st_;
   SideStream* side_;
-  bool pending_ = false;
+  hipEvent_t done_ = nullptr;  // this fork's join event, until joined
 };
 
 

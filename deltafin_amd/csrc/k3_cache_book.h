@@ -32,8 +32,10 @@ struct CachePolicy {
   uint64_t reserve_value = 0;  // Auto: 0; Bytes: bytes; RatioPpm: parts per million of free
 };
 
-// Most slots a cache may hold (expert ids are 16-bit per layer).
-constexpr uint64_t kCacheMaxExperts = 65536;
+// Most slots a cache may hold: 92 layer strata x 16 routed experts, the
+// reference's kCudaMaximumExperts (provider_cuda_moe.cpp:55-57), enforced by
+// both the policy check and the budget clamp as there.
+constexpr uint64_t kCacheMaxExperts = 92 * 16;
 // Recoveries from allocation failure before the cache disables itself
 // (rebuilds_remaining, provider_cuda_moe.cpp:879).
 constexpr int kCacheRebuilds = 2;

@@ -571,6 +571,21 @@ struct PosStride {
 #endif
 constexpr int kGluMaxThreads = 256 * K3_GLU_GROUPS;
 
+// XCD-blocked workgroup order.  MI355X dispatches the workgroups of a launch
+// to its 8 XCDs round robin (workgroup k runs on XCD k % 8), and each XCD has
+// its own L2 and address-translation cache.  Relabelling workgroup k as
+// v = (k % 8) * (G / 8) + k / 8 gives every XCD one contiguous range of v, so
+// an XCD reads one contiguous stretch of each matrix instead of every eighth
+// slice of all of it.  Only which workgroup computes a row changes; every row
+// is computed the same way.  Grids that are not a multiple of 8 keep k.
+#ifndef K3_XCD_MAP
+#define K3_XCD_MAP 3  // bit 0: gate/up units, bit 1: down row batches
+#endif
+__device__ __forceinline__ int xcd_block_id(int k, int G) {
+  if (!(K3_XCD_MAP & 1) || (G & 7)) return k;
+  return (k & 7) * (G >> 3) + (k >> 3);
+}
+
 template <typename XT, int kR, bool kG, bool kS4 = false, bool kPos = false>
 __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute route_arg,
                                                      const Geo g,
@@ -658,7 +673,7 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
   // so), which keeps the workgroup-wide barrier below uniform.
   const int Q = gridDim.x * groups;
   const int iters = (n_units + Q - 1) / Q;
-  const int q0 = blockIdx.x * groups + grp;
+  const int q0 = xcd_block_id((int)blockIdx.x, (int)gridDim.x) * groups + grp;
   // Unit of iteration `it` (a unit past the end repeats unit 0's loads and
   // stores nothing, so every wave reaches every barrier).
   auto unit_pair0 = [&](int it) {
@@ -977,7 +992,15 @@ __global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route_arg, c
   const int nbt = (g.hidden + kB - 1) / kB;
   const int nb = (nbt - (int)blockIdx.x + G - 1) / G;  // 1 <= nb <= NB (host)
   const int cc[1] = {lane};
-  auto row_of = [&](int i) { return (min(i, nb - 1) * G + (int)blockIdx.x) * kB; };
+  // Batch i of workgroup k is i G + k; XCD-blocked (xcd_block_id) when the
+  // grid covers the batches exactly (nbt = G NB): XCD x = k % 8 owns batches
+  // x J NB .. (x + 1) J NB - 1 (J = G / 8) and its workgroup j = k / 8 takes
+  // x J NB + i J + j, so each XCD reads one contiguous stretch at a time.
+  const bool xmap = (K3_XCD_MAP & 2) && (G & 7) == 0 && nbt == G * NB;
+  const int xb = xmap ? ((int)blockIdx.x & 7) * (G >> 3) * NB + ((int)blockIdx.x >> 3)
+                      : (int)blockIdx.x;
+  const int xs = xmap ? (G >> 3) : G;
+  auto row_of = [&](int i) { return (min(i, nb - 1) * xs + xb) * kB; };
   auto rows_in = [&](int i) { return min(kB, g.hidden - row_of(i)); };
   const int idx = lane >> 4;
   const bool writer = (lane & 15) == 0;
@@ -1092,7 +1115,12 @@ __global__ __launch_bounds__(1024) void k_down_g96(const TokenRoute route_arg, c
   const int G = gridDim.x;
   const int npt = g.hidden >> 1;                       // pairs in the output (hidden even)
   const int nb = (npt - (int)blockIdx.x + G - 1) / G;  // 1 <= nb <= NB (host)
-  auto pair_of = [&](int i) { return min(i, nb - 1) * G + (int)blockIdx.x; };
+  // XCD-blocked pairs when the grid covers them exactly (as in k_down_g64).
+  const bool xmap = (K3_XCD_MAP & 2) && (G & 7) == 0 && npt == G * NB;
+  const int xb = xmap ? ((int)blockIdx.x & 7) * (G >> 3) * NB + ((int)blockIdx.x >> 3)
+                      : (int)blockIdx.x;
+  const int xs = xmap ? (G >> 3) : G;
+  auto pair_of = [&](int i) { return min(i, nb - 1) * xs + xb; };
   const int e = wave;  // one routed expert per wave (route.n <= 16 waves)
   const float* he = h + (size_t)e * g.inter;
   // h_e's head (floats 0-2047: float4 64 q + lane) and tail (floats

@@ -299,7 +299,7 @@ typedef struct K3HipCache K3HipCache;
  * the cache fills, after the budget is measured at the first plan.
  * staging_slots = pinned host staging buffers used for pageable sources.
  * Returns NULL on failure (see k3_hip_last_error). */
-#define K3_HIP_CACHE_MAX_EXPERTS 65536
+#define K3_HIP_CACHE_MAX_EXPERTS 1472 /* 92 strata x 16: kCudaMaximumExperts, provider_cuda_moe.cpp:55-57 */
 K3HipCache* k3_hip_cache_create(int device, uint64_t span_bytes,
                                 int capacity_experts, int n_layers,
                                 int staging_slots);

@@ -282,8 +282,11 @@ def test_cache_budget_policy(gpu):
     try:
         with pytest.raises(_lib.K3HipError):
             cache.configure(True, capacity=5)        # automatic with a count
+        # The reference's bound: 92 strata x 16 experts (kCudaMaximumExperts).
+        assert _lib.K3_HIP_CACHE_MAX_EXPERTS == 92 * 16
         with pytest.raises(_lib.K3HipError):
             cache.configure(False, capacity=_lib.K3_HIP_CACHE_MAX_EXPERTS + 1)
+        cache.configure(False, capacity=_lib.K3_HIP_CACHE_MAX_EXPERTS)
         with pytest.raises(_lib.K3HipError):
             cache.configure(True, reserve_kind=_lib.K3_CACHE_RESERVE_RATIO_PPM,
                             reserve_value=1_000_001)
