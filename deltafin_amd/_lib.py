@@ -154,6 +154,8 @@ SIGNATURES = {
     "k3_hip_moe_positions_desc_v1": (_i32, [_DP, _i32, _vp, _i32, _vp, _vp, _vp]),
     "k3_hip_moe_layer": (_i32, [_vp, _i32, _vp, _vp, _vp]),
     "k3_hip_moe_positions": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "k3_hip_moe_positions_flat": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "k3_hip_moe_positions_flat_desc_v1": (_i32, [_DP, _i32, _vp, _i32, _vp, _vp, _vp]),
     "k3_hip_moe_abi_version": (_u32, []),
     "k3_hip_moe_shapes": (None, [C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i64), C.POINTER(_u32)]),
     "k3_hip_moe_available": (_i32, [_i32]),

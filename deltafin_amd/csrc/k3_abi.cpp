@@ -353,7 +353,7 @@ namespace {
 
 bool geometry_from(const K3HipGeometryV1* g, Geo* out);
 int verify_table(const Geo& g, const EdgeTable& tbl, const void* x, int x_dtype, void* out,
-                 int out_dtype, const Workspace& ws, hipStream_t st);
+                 int out_dtype, const Workspace& ws, hipStream_t st, bool flat);
 
 // ---------------------------------------------------------------- presets
 void fill_geometry(uint32_t hidden, uint32_t inter, uint32_t act, K3HipGeometryV1* out) {
@@ -658,9 +658,13 @@ int layer_locked(Context& c, const Geo& lg, const uint8_t* const* blobs, int n,
 
 int positions_locked(Context& c, const Geo& lg, const uint8_t* const* blobs, int n_edges,
                      const int* offs, int n_pos, const float* weights, const float* x,
-                     float* out) {
+                     float* out, bool flat = false) {
   // Offset validation mirrors tools/metal_moe.mm:852-871.
   if (n_edges < 0 || n_pos < 0) return fail(K3_HIP_E_INVALID, "positions: negative counts");
+  // The flat form's bounds (tools/metal_moe.mm:1056-1059): at most 16
+  // positions and 16 edges per position on average, else invalid arguments.
+  if (flat && (n_pos > 16 || n_edges > n_pos * 16))
+    return fail(K3_HIP_E_INVALID, "flat positions: at most 16 positions and 16 x positions edges");
   if (n_pos == 0) return n_edges == 0 ? K3_HIP_OK : fail(K3_HIP_E_INVALID, "positions: edges without positions");
   if (!offs || !x || !out) return fail(K3_HIP_E_INVALID, "positions: null offsets/input/output");
   if (n_pos > K3_HIP_MAX_POSITIONS || n_edges > K3_HIP_MAX_EDGES)
@@ -701,7 +705,7 @@ int positions_locked(Context& c, const Geo& lg, const uint8_t* const* blobs, int
   // The same path selection as the device surface (k3_hip_set_verify_mode):
   // raw-v1 spans take the matrix-core union path where it applies and pays,
   // scale4-v2 spans run one decode layer per position.
-  int rc = verify_table(lg, tbl, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws, c.stream);
+  int rc = verify_table(lg, tbl, c.dx, K3_DTYPE_F32, c.dout, K3_DTYPE_F32, ws, c.stream, flat);
   if (rc == K3_HIP_OK &&
       (e = hipMemcpyAsync(c.hout, c.dout, bytes, hipMemcpyDeviceToHost, c.stream)) != hipSuccess)
     rc = fail(K3_HIP_E_COPY, "positions output copy: %s", hipGetErrorString(e));
@@ -749,7 +753,7 @@ double expected_union(int n_bank, int top_k, int n_positions) {
 // raw-v1 spans; other layouts run per position.  Positions without edges get
 // zero rows.
 int verify_table(const Geo& g, const EdgeTable& tbl, const void* x, int x_dtype, void* out,
-                 int out_dtype, const Workspace& ws, hipStream_t st) {
+                 int out_dtype, const Workspace& ws, hipStream_t st, bool flat) {
   const int n_edges = tbl.n_edges, n_positions = tbl.n_positions;
   const size_t xb = x_dtype == K3_DTYPE_BF16 ? 2 : 4, ob = out_dtype == K3_DTYPE_BF16 ? 2 : 4;
   if (n_edges == 0) return launch_zero(out, (uint64_t)n_positions * g.hidden * ob, st);
@@ -772,32 +776,82 @@ int verify_table(const Geo& g, const EdgeTable& tbl, const void* x, int x_dtype,
     return fail(K3_HIP_E_CAPABILITY,
                 "verify: no matrix-core path (geometry/layout, or an expert with %d > 16 edges)",
                 max_edges_per_expert);
-  const bool mfma = mode == K3_VERIFY_UNION_MFMA ||
-                    (mode == K3_VERIFY_AUTO && n_positions >= 2 && mfma_ok &&
-                     n_unique <= kUnionFraction * n_edges);
+  bool mfma = mode == K3_VERIFY_UNION_MFMA ||
+              (mode == K3_VERIFY_AUTO && n_positions >= 2 && mfma_ok &&
+               n_unique <= kUnionFraction * n_edges);
   // Without the matrix-core path, positions that share most of their experts
   // take the VALU union kernels (each shared expert read once); otherwise one
   // decode layer per position (about twice the streaming rate of the VALU
   // union kernels, so they win unless the union is under half the edges).
-  const bool valu = raw && (mode == K3_VERIFY_UNION_VALU ||
-                            (mode == K3_VERIFY_AUTO && !mfma && !mfma_ok && 2 * n_unique <= n_edges));
+  bool valu = raw && (mode == K3_VERIFY_UNION_VALU ||
+                      (mode == K3_VERIFY_AUTO && !mfma && !mfma_ok && 2 * n_unique <= n_edges));
+  if (flat && !mfma && !valu) {
+    // A flat batch runs as one dispatch sequence: per position only when the
+    // positions with edges form one run of equal edge counts that the
+    // position-batched decode takes (empty positions are zero rows), else
+    // the union kernels (raw-v1), else a capability miss.
+    int count = -1, runs = 0;
+    bool gap = false;
+    for (int p = 0; p < n_positions; ++p) {
+      const int n = tbl.pos_off[p + 1] - tbl.pos_off[p];
+      if (n == 0) {
+        gap = runs > 0;
+        continue;
+      }
+      if (n != count || gap) ++runs;
+      count = n;
+      gap = false;
+    }
+    const bool one_run = runs == 1 && (n_positions == 1 || (K3_BATCH_POSITIONS &&
+                                                            decode_positions_supported(g, count)));
+    if (!one_run) {
+      if (!raw)
+        return fail(K3_HIP_E_CAPABILITY,
+                    "flat positions: no single-dispatch form for these edge counts (layout %d)",
+                    g.layout);
+      mfma = mfma_ok;
+      valu = !mfma_ok;
+    }
+  }
   if (mfma || valu) {
     int rc = launch_verify_plan_table(tbl, ws, st);
     if (rc != K3_HIP_OK) return rc;
     return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
                 : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
   }
-  for (int p = 0; p < n_positions; ++p) {
+  // One decode layer per position: a run of two or more consecutive
+  // positions with the same edge count runs as one position-batched launch
+  // pair (launch_decode_positions over a table-mode route in the workspace);
+  // a lone position runs its own layer, and a position with no edges gets a
+  // zero row.
+  for (int p = 0; p < n_positions;) {
     const int e0 = tbl.pos_off[p], n = tbl.pos_off[p + 1] - e0;
     uint8_t* outp = static_cast<uint8_t*>(out) + (size_t)p * g.hidden * ob;
+    const uint8_t* xp = static_cast<const uint8_t*>(x) + (size_t)p * g.hidden * xb;
     if (n == 0) {  // no routed expert: a zero row
       const int rc = launch_zero(outp, (uint64_t)g.hidden * ob, st);
       if (rc != K3_HIP_OK) return rc;
+      ++p;
       continue;
     }
     if (n > K3_HIP_MAX_TOKEN_EXPERTS)
       return fail(K3_HIP_E_INVALID, "verify: position %d has %d edges (at most %d)", p, n,
                   K3_HIP_MAX_TOKEN_EXPERTS);
+    int run = 1;
+    while (p + run < n_positions && tbl.pos_off[p + run + 1] - tbl.pos_off[p + run] == n) ++run;
+    if (K3_BATCH_POSITIONS && run > 1 && decode_positions_supported(g, n)) {
+      int rc = launch_route_table(tbl, e0, run * n, ws, st);
+      if (rc != K3_HIP_OK) return rc;
+      TokenRoute route;
+      memset(&route, 0, sizeof(route));
+      route.pdev = ws.uptr;
+      route.wdev = ws.w;
+      route.n = n;
+      rc = launch_decode_positions(g, route, run, xp, x_dtype, outp, out_dtype, ws, st);
+      if (rc != K3_HIP_OK) return rc;
+      p += run;
+      continue;
+    }
     TokenRoute route;
     memset(&route, 0, sizeof(route));
     route.n = n;
@@ -805,9 +859,9 @@ int verify_table(const Geo& g, const EdgeTable& tbl, const void* x, int x_dtype,
       route.ptr[i] = tbl.ptr[e0 + i];
       route.w[i] = tbl.w[e0 + i];
     }
-    const int rc = launch_decode_layer(g, route, static_cast<const uint8_t*>(x) + (size_t)p * g.hidden * xb,
-                                       x_dtype, outp, out_dtype, ws, st);
+    const int rc = launch_decode_layer(g, route, xp, x_dtype, outp, out_dtype, ws, st);
     if (rc != K3_HIP_OK) return rc;
+    ++p;
   }
   return K3_HIP_OK;
 }
@@ -1287,6 +1341,20 @@ int k3_hip_moe_positions_desc_v1(const K3HipExpertDescriptorV1* experts, int edg
                           position_offsets, position_count, weights, input, output);
 }
 
+int k3_hip_moe_positions_flat_desc_v1(const K3HipExpertDescriptorV1* experts, int edge_count,
+                                      const int* position_offsets, int position_count,
+                                      const float* weights, const float* input, float* output) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
+  std::vector<const uint8_t*> blobs;
+  Geo lg;
+  const int rc = check_descriptors(c, experts, edge_count, &blobs, &lg);
+  if (rc != K3_HIP_OK) return rc;
+  return positions_locked(c, lg, blobs.empty() ? nullptr : blobs.data(), edge_count,
+                          position_offsets, position_count, weights, input, output, true);
+}
+
 int k3_hip_moe_layer(const uint8_t* const* expert_blobs, int n_experts, const float* weights,
                      const float* x, float* out) {
   Context& c = ctx();
@@ -1303,6 +1371,16 @@ int k3_hip_moe_positions(const uint8_t* const* expert_blobs, int n_edges,
   if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
   return positions_locked(c, c.geo, expert_blobs, n_edges, position_offsets, n_positions, weights,
                           x, out);
+}
+
+int k3_hip_moe_positions_flat(const uint8_t* const* expert_blobs, int n_edges,
+                              const int* position_offsets, int n_positions, const float* weights,
+                              const float* x, float* out) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (!init_locked(c, nullptr)) return K3_HIP_E_INIT;
+  return positions_locked(c, c.geo, expert_blobs, n_edges, position_offsets, n_positions, weights,
+                          x, out, true);
 }
 
 // ------------------------------------------------------------ surface 2
@@ -1564,7 +1642,7 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
     tbl.ptr[i] = edge_experts[i];
     tbl.w[i] = edge_weights[i];
   }
-  return verify_table(g, tbl, x, x_dtype, out, out_dtype, ws, st);
+  return verify_table(g, tbl, x, x_dtype, out, out_dtype, ws, st, false);
 }
 
 int k3_hip_set_fused_decode(int enabled) { return set_fused_decode(enabled); }

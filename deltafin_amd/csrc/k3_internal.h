@@ -46,6 +46,10 @@ struct TokenRoute {
   float* w_pub;
   int32_t* ids_user;
   float* w_user;
+  // Table mode (no bank, pdev non-null): a caller route already in device
+  // memory, span pointers pdev[p * n + e] and weights wdev[p * n + e] for
+  // position p (the position-batched decode of caller routes).
+  const uint8_t* const* pdev;
   const uint8_t* ptr[K3_HIP_MAX_TOKEN_EXPERTS];
   float w[K3_HIP_MAX_TOKEN_EXPERTS];
   int n;
@@ -122,8 +126,9 @@ int launch_route_sigmoid_bias(const float* logits, const float* bias, int n_bank
 int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x,
                         int x_dtype, void* out, int out_dtype,
                         const Workspace& ws, hipStream_t stream);
-// n_positions decode layers of one bank-mode route (router mode: logits
-// strided by n_bank; caller mode: ids / wdev strided by route.n) as one
+// n_positions decode layers of one bank-mode or table-mode route (router
+// mode: logits strided by n_bank; caller mode: ids or pdev, and wdev, strided
+// by route.n) as one
 // gate/up launch and one down launch, position p on blockIdx.y: x and out rows
 // strided by hidden, h by route.n * intermediate (ws holds n_positions *
 // route.n edges).  Outputs equal n_positions launch_decode_layer calls bit for
@@ -143,6 +148,10 @@ int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride,
                             hipStream_t stream);
 int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws,
                              hipStream_t stream);
+// Edges e0 .. e0 + n - 1 of a caller route table into the workspace as a
+// table-mode route (ws.uptr span pointers, ws.w weights).
+int launch_route_table(const EdgeTable& table, int e0, int n, const Workspace& ws,
+                       hipStream_t stream);
 // The VALU union verify kernels over the plan in ws, then the combine.
 int launch_verify_layer(const Geo& g, int n_edges, int n_positions,
                         const void* x, int x_dtype, void* out, int out_dtype,

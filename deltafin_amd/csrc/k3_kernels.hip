@@ -111,10 +111,10 @@ __device__ __forceinline__ void store_out<uint16_t>(uint16_t* p, float v) {
 // off: first entry of this route in the device ids / weights (bank mode;
 // position-batched kernels route position p at p * n).
 __device__ __forceinline__ const uint8_t* route_span(const TokenRoute& r, int e, size_t off = 0) {
-  return r.bank ? r.bank + (uint64_t)r.ids[off + e] * r.stride : r.ptr[e];
+  return r.bank ? r.bank + (uint64_t)r.ids[off + e] * r.stride : r.pdev ? r.pdev[off + e] : r.ptr[e];
 }
 __device__ __forceinline__ float route_weight(const TokenRoute& r, int e, size_t off = 0) {
-  return r.bank ? r.wdev[off + e] : r.w[e];
+  return r.bank || r.pdev ? r.wdev[off + e] : r.w[e];
 }
 
 // A wave's copy of the route: lane e (< n) holds expert e's span address and
@@ -973,6 +973,11 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
 // b is reduced batch b + 1 is in flight, and batch b + 2 is requested right
 // after b's registers are free.
 constexpr int kDownG64MaxNB = 8;
+// Row batches in flight per wave.  Three measured 22.6 -> 28.0 us for the
+// config-2 down kernel (more concurrent DRAM rows per CU), so two.
+#ifndef K3_DOWN_INFLIGHT
+#define K3_DOWN_INFLIGHT 2
+#endif
 
 template <typename OT, int NB, bool kPos = false>
 __global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route_arg, const Geo g,
@@ -1016,16 +1021,18 @@ __global__ __launch_bounds__(1024) void k_down_g64(const TokenRoute route_arg, c
   const RouteRegs rreg = route_regs(route, lane, proute);
   {
     const uint8_t* span = span_of(rreg, e);
-    DownBatch<1, kB, true> bt[2];
-    down_load(bt[0], span, g, cc, row_of(0), rows_in(0));
-    if constexpr (NB > 1) down_load(bt[1], span, g, cc, row_of(1), rows_in(1));
+    constexpr int kF = K3_DOWN_INFLIGHT;  // batches in flight per wave
+    DownBatch<1, kB, true> bt[kF];
+#pragma unroll
+    for (int f = 0; f < kF; ++f)
+      if (f < NB) down_load(bt[f], span, g, cc, row_of(f), rows_in(f));
     __builtin_amdgcn_sched_barrier(0);
     XChunk<float> hs;
     h_slice_transpose(hs, ht, hbuf + wave * kHSliceF4, lane);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const float v = down_dots(bt[b & 1], &hs, lane);
-      if (b + 2 < NB) down_load(bt[b & 1], span, g, cc, row_of(b + 2), rows_in(b + 2));
+      const float v = down_dots(bt[b % kF], &hs, lane);
+      if (b + kF < NB) down_load(bt[b % kF], span, g, cc, row_of(b + kF), rows_in(b + kF));
       if (writer && b < nb && idx < rows_in(b)) ybuf[e][b * kB + idx] = v;
     }
   }
@@ -1699,6 +1706,17 @@ __global__ __launch_bounds__(256) void k_verify_plan_table(const EdgeTable tbl,
   }
   if (e <= tbl.n_positions) ws.poff[e] = tbl.pos_off[e];
   plan_core(key, e, tbl.n_edges, tbl.n_positions, ws);
+}
+
+// A caller route table's edges e0 .. e0 + n - 1 as a table-mode route in
+// device memory (span pointers and weights, edge order).
+__global__ __launch_bounds__(256) void k_route_table(const EdgeTable tbl, int e0, int n,
+                                                      const uint8_t** __restrict__ ptr_out,
+                                                      float* __restrict__ w_out) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    ptr_out[i] = tbl.ptr[e0 + i];
+    w_out[i] = tbl.w[e0 + i];
+  }
 }
 
 // ======================================================================
@@ -2422,7 +2440,7 @@ bool decode_positions_supported(const Geo& g, int n) {
 int launch_decode_positions(const Geo& g, const TokenRoute& route, int n_positions,
                             const void* x, int x_dtype, void* out, int out_dtype,
                             const Workspace& ws, hipStream_t st) {
-  if (!route.bank || n_positions < 1 || !decode_positions_supported(g, route.n))
+  if (!(route.bank || route.pdev) || n_positions < 1 || !decode_positions_supported(g, route.n))
     return fail(K3_HIP_E_CAPABILITY, "decode positions: no batched form for this call");
   PosLaunch pl;
   pl.n = n_positions;
@@ -2459,6 +2477,14 @@ int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws, hipStr
   TimedLaunch tl(KC_VERIFY_PLAN, st);
   launch_timed(tl, k_verify_plan_table, dim3(1), dim3(256), 0, st, table, ws);
   return launched(tl, "verify plan launch");
+}
+
+int launch_route_table(const EdgeTable& table, int e0, int n, const Workspace& ws, hipStream_t st) {
+  if (e0 < 0 || n < 1 || e0 + n > table.n_edges)
+    return fail(K3_HIP_E_INVALID, "route table: edges %d .. %d outside the table", e0, e0 + n);
+  TimedLaunch tl(KC_VERIFY_PLAN, st);
+  launch_timed(tl, k_route_table, dim3(1), dim3(256), 0, st, table, e0, n, ws.uptr, ws.w);
+  return launched(tl, "route table launch");
 }
 
 namespace {

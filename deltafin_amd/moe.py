@@ -8,8 +8,10 @@ Reference counterparts:
   moe_layer           k3_metal_moe_layer (tools/metal_moe.mm:829-837) and the
                       per-expert loop + ordered_route_reduce of
                       provider_cuda_moe.cpp:1203-1258, :252-289
-  moe_positions       k3_metal_moe_positions (tools/metal_moe.mm:1023-1032)
   moe_layer_desc      k3_metal_moe_layer_desc_v1 (tools/metal_moe_abi.h:59-61)
+  moe_positions_desc  k3_metal_moe_positions_desc_v1 (tools/metal_moe_abi.h:63-66),
+                      flat=True: k3_metal_moe_positions_flat_desc_v1
+                      (tools/metal_moe.mm:1231-1243)
   ExpertCache         CudaMoeExpertCache (provider_cuda_moe.h:83-132)
 
 Device tensors are torch tensors on the current HIP device; the current torch
@@ -233,7 +235,10 @@ def moe_layer_desc(blobs: Sequence, weights: Sequence[float], x: np.ndarray,
 
 def moe_positions_desc(blobs: Sequence, position_offsets: Sequence[int],
                        weights: Sequence[float], x: np.ndarray,
-                       layout: int = _lib.K3_LAYOUT_RAW_V1) -> np.ndarray:
+                       layout: int = _lib.K3_LAYOUT_RAW_V1, flat: bool = False) -> np.ndarray:
+    """k3_hip_moe_positions_desc_v1, or with flat=True its flat form
+    k3_hip_moe_positions_flat_desc_v1 (one batched dispatch sequence; a
+    K3HipError with status K3_HIP_E_CAPABILITY where the batch has none)."""
     lib = load()
     h, i, span = C.c_int(), C.c_int(), C.c_longlong()
     lib.k3_hip_shapes(C.byref(h), C.byref(i), C.byref(span))
@@ -242,10 +247,10 @@ def moe_positions_desc(blobs: Sequence, position_offsets: Sequence[int],
     out = np.empty((m, h.value), dtype=np.float32)
     w = np.ascontiguousarray(weights, dtype=np.float32)
     offs = np.ascontiguousarray(position_offsets, dtype=np.int32)
-    rc = lib.k3_hip_moe_positions_desc_v1(_descs(blobs, _layout_span(layout, span.value), layout),
-                                          len(blobs), offs.ctypes.data, m, w.ctypes.data,
-                                          x.ctypes.data, out.ctypes.data)
-    check(rc, "k3_hip_moe_positions_desc_v1")
+    fn = lib.k3_hip_moe_positions_flat_desc_v1 if flat else lib.k3_hip_moe_positions_desc_v1
+    rc = fn(_descs(blobs, _layout_span(layout, span.value), layout), len(blobs),
+            offs.ctypes.data, m, w.ctypes.data, x.ctypes.data, out.ctypes.data)
+    check(rc, "k3_hip_moe_positions_flat_desc_v1" if flat else "k3_hip_moe_positions_desc_v1")
     return out
 
 

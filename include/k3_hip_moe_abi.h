@@ -173,6 +173,24 @@ int k3_hip_moe_layer(const uint8_t* const* expert_blobs, int n_experts,
 int k3_hip_moe_positions(const uint8_t* const* expert_blobs, int n_edges,
                          const int* position_offsets, int n_positions,
                          const float* weights, const float* x, float* out);
+/* Flat position batches: replace k3_metal_moe_positions_flat and
+ * k3_metal_moe_positions_flat_desc_v1 (tools/metal_moe.mm:1049-1070,
+ * :1194-1259), which the provider binds beside the plain positions calls and
+ * tries first (native/provider_gate/provider_moe.cpp:141-187, :1406-1478).
+ * Same arguments and outputs as the positions calls, run as one batched
+ * dispatch sequence over all edges.  Bounds as the Metal bridge's: at most 16
+ * positions and 16 x n_positions edges, else K3_HIP_E_INVALID.  Where the
+ * batch has no single-dispatch form here (positions with different edge
+ * counts over scale4-v2 spans, which have no union kernels) the call returns
+ * K3_HIP_E_CAPABILITY (-6) before touching its outputs, and the caller steps
+ * down to the positions call, as the provider does. */
+int k3_hip_moe_positions_flat(const uint8_t* const* expert_blobs, int n_edges,
+                              const int* position_offsets, int n_positions,
+                              const float* weights, const float* x, float* out);
+int k3_hip_moe_positions_flat_desc_v1(const K3HipExpertDescriptorV1* experts,
+                                      int edge_count, const int* position_offsets,
+                                      int position_count, const float* weights,
+                                      const float* input, float* output);
 
 /* ============================== surface 2: stream-explicit device API */
 

@@ -66,3 +66,65 @@ def test_batched_positions_equal_per_position_layers(gpu, positions_mode, preset
         ref, mag = oracle.moe_layer_f64(spans, rw, g.hidden, g.intermediate, g.activation, x[0])
         err = oracle.cond_rel_err(out[0].cpu().numpy(), ref, mag, g.intermediate)
         assert err <= TOL, f"position 0: {err:.3e}"
+
+
+@pytest.mark.parametrize("preset_id,counts,odt,xdt", [
+    (2, [16, 16, 16, 16], "f32", "bf16"),
+    (2, [16, 16, 0, 16, 16, 8, 8, 3], "bf16", "bf16"),
+    (1, [16, 16, 16], "f32", "f32"),
+    (1, [4, 0, 4, 4, 16], "bf16", "f32"),
+])
+def test_caller_route_batched_positions_equal_per_position_layers(gpu, positions_mode, preset_id,
+                                                                  counts, odt, xdt):
+    """k3_hip_moe_verify_device with a caller route on the per-position path:
+    each run of consecutive positions with the same edge count is one
+    position-batched launch pair over a table-mode route; every position must
+    equal its own single-position layer bit for bit (experts repeated across
+    positions, empty positions as zero rows, lone positions and runs of
+    different counts), and sampled positions match the oracle."""
+    import torch
+    from deltafin_amd import moe
+    g = moe.preset(preset_id)
+    n_bank = 40
+    say(f"caller-route batched positions preset {preset_id} counts {counts} out={odt} x={xdt}")
+    stride = g.expert_span
+    bank = torch.empty(n_bank * stride, dtype=torch.uint8, device="cuda")
+    moe.synth_bank(g, bank, stride, n_bank, 0, 616)
+    rng = np.random.default_rng(70 + preset_id + len(counts))
+    m = len(counts)
+    ids = [rng.choice(n_bank, size=c, replace=False) for c in counts]
+    wts = []
+    for c in counts:
+        w = rng.random(c).astype(np.float32) + 0.05
+        wts.append((w / w.sum()).astype(np.float32))
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(int).tolist()
+    x = rng.standard_normal((m, g.hidden)).astype(np.float32)
+    if xdt == "bf16":
+        x = synth.bf16_bits_to_f32(synth.to_bf16_bits(x))
+        xd = torch.from_numpy(synth.to_bf16_bits(x).view(np.int16)).view(torch.bfloat16).cuda()
+    else:
+        xd = _t(x)
+    out_dtype = torch.bfloat16 if odt == "bf16" else torch.float32
+    span = lambda e: bank[int(e) * stride:(int(e) + 1) * stride]
+    edges = [span(e) for p in range(m) for e in ids[p]]
+    ws = moe.workspace(g, sum(counts), m)
+    out = moe.moe_verify(g, edges, np.concatenate(wts), offs, xd, ws, out_dtype=out_dtype)
+    ws1 = moe.workspace(g, 16)
+    iv = torch.int16 if odt == "bf16" else torch.int32
+    for p in range(m):
+        if counts[p] == 0:
+            assert torch.count_nonzero(out[p].view(iv)) == 0, f"position {p} (no edges)"
+            continue
+        o1 = moe.moe_layer(g, [span(e) for e in ids[p]], wts[p], xd[p].contiguous(), ws1,
+                           out_dtype=out_dtype)
+        torch.cuda.synchronize()
+        assert torch.equal(out[p].view(iv), o1.view(iv)), f"position {p} differs from its layer"
+    if odt == "f32":
+        for p in (0, m - 1):
+            if counts[p] == 0:
+                continue
+            spans = [oracle.synth_expert(616, int(e), g.hidden, g.intermediate) for e in ids[p]]
+            ref, mag = oracle.moe_layer_f64(spans, wts[p].astype(np.float64), g.hidden,
+                                            g.intermediate, g.activation, x[p])
+            err = oracle.cond_rel_err(out[p].cpu().numpy(), ref, mag, g.intermediate)
+            assert err <= TOL, f"position {p}: {err:.3e}"
