@@ -94,6 +94,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--spine-only", action="store_true",
                     help="print only the spine-projection timings (K3 spine shapes)")
     ap.add_argument("--no-spine", action="store_true", help="skip the spine timings")
+    ap.add_argument("--no-k3", action="store_true", help="skip the K3 caller-route decode object")
+    ap.add_argument("--k3-only", action="store_true",
+                    help="print only the K3 caller-route decode object (k3_decode)")
     ap.add_argument("--block-only", action="store_true",
                     help="print only the whole-K3-MoE-block timings")
     ap.add_argument("--no-block", action="store_true", help="skip the K3 MoE block timings")
@@ -595,6 +598,11 @@ def main() -> int:
         print(json.dumps(_single_configs(moe, _lib, oracle, g, bank, stride, args.cpu_seconds,
                                          args.no_cpu)), flush=True)
         return 0
+    if args.k3_only:
+        print(json.dumps(_k3_decode_bench(moe, _lib, oracle, 300,
+                                          None if args.no_cpu else args.cpu_seconds / 2, bank)),
+              flush=True)
+        return 0
     if args.spine_only or args.block_only:
         del bank
         torch.cuda.empty_cache()
@@ -757,6 +765,9 @@ def main() -> int:
     if args.verify_batches > 0:
         res["verify"] = _verify_config3(moe, _lib, g, bank, stride, args.verify_batches,
                                         None if args.no_cpu else args.cpu_seconds)
+    if not args.no_k3:
+        res["k3_decode"] = _k3_decode_bench(moe, _lib, oracle, 300,
+                                            None if args.no_cpu else args.cpu_seconds / 2, bank)
     if not args.no_spine:
         res["spine"] = _spine_bench()
     if not args.no_block:
@@ -1106,14 +1117,17 @@ def _verify_batches(moe, _lib, g, bank, stride, logits, x, batches: int) -> dict
     st = moe.stream_handle()
     lib = _lib.load()
     ids = torch.empty((n, m, TOP_K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((n, m, TOP_K), dtype=torch.float32, device="cuda")
 
-    def call(i: int) -> None:
+    def routed(i: int) -> None:
         rc = lib.k3_hip_moe_verify_route_device(
             C.byref(g), bank.data_ptr(), stride, N_BANK, logits[i].data_ptr(), m, TOP_K,
             x[i].data_ptr(), _lib.K3_DTYPE_BF16, y[i].data_ptr(), _lib.K3_DTYPE_BF16,
-            ids[i].data_ptr(), None, base, nbytes, st)
+            ids[i].data_ptr(), wts[i].data_ptr(), base, nbytes, st)
         if rc != 0:
             raise _lib.K3HipError(rc, "k3_hip_moe_verify_route_device")
+
+    call = routed
 
     def timed(stamps: bool):
         # Settle: the batches back to back for VERIFY_SETTLE_S of host time
@@ -1149,6 +1163,32 @@ def _verify_batches(moe, _lib, g, bank, stride, logits, x, batches: int) -> dict
         prev = _lib.set_verify_mode(mode)
         try:
             res[path] = timed(path != "positions")
+        finally:
+            _lib.set_verify_mode(prev)
+    # The same routes handed over as caller routes (k3_hip_moe_verify_device:
+    # span tables and weights, the provider's execute_positions call), on
+    # AUTO and on the per-position path (runs of equal edge counts batched).
+    ids_h, w_h = ids.cpu().numpy(), wts.cpu().numpy()
+    tables = []
+    for i in range(n):
+        ptrs = (C.c_void_p * (m * TOP_K))(*[bank.data_ptr() + int(e) * stride
+                                             for e in ids_h[i].ravel()])
+        ww = (C.c_float * (m * TOP_K))(*[float(v) for v in w_h[i].ravel()])
+        tables.append((ptrs, ww))
+    offs = (C.c_int * (m + 1))(*[p * TOP_K for p in range(m + 1)])
+
+    def caller(i: int) -> None:
+        rc = lib.k3_hip_moe_verify_device(C.byref(g), tables[i][0], tables[i][1], offs, m,
+                                          x[i].data_ptr(), _lib.K3_DTYPE_BF16, y[i].data_ptr(),
+                                          _lib.K3_DTYPE_BF16, base, nbytes, st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_moe_verify_device")
+
+    call = caller
+    for path, mode in (("caller_auto", _lib.VERIFY_AUTO), ("caller_positions", _lib.VERIFY_POSITIONS)):
+        prev = _lib.set_verify_mode(mode)
+        try:
+            res[path] = timed(True)
         finally:
             _lib.set_verify_mode(prev)
     union = float(np.mean([len(set(ids[i].cpu().numpy().ravel().tolist())) for i in range(3, n)]))
@@ -1188,10 +1228,187 @@ def _verify_batches(moe, _lib, g, bank, stride, logits, x, batches: int) -> dict
         "mfma_issued_util": round(issued / mfma_s / (MFMA_PEAK_FP8_TFLOPS * 1e12), 4)
         if mfma_s else None,
         "useful_tflops_union_mfma": round(useful / usec / 1e12, 2),
+        "caller_route": _caller_summary(res, nbytes_alg, batches),
     }
     log(f"verify M={m}: auto -> {auto_path} {sec * 1e6:.1f} us/batch (union {union:.1f} of "
         f"{m * TOP_K} edges); union/mfma {usec * 1e6:.1f} us, per-position "
         f"{res['positions'][0] * 1e6:.1f} us; mfma kernels {kus}")
+    return out
+
+
+# The reference's own routed layer (provider_moe.h:40-42; K3 preset): 16 of
+# 896 experts, hidden 3584, intermediate 3072, SiTU, fp32 activations in and
+# out, caller routes.
+K3_BANK, K3_HIDDEN, K3_INTER = 896, 3584, 3072
+K3_MAT = K3_INTER * K3_HIDDEN // 2 + K3_INTER * (K3_HIDDEN // 32)  # 5,849,088 per matrix
+K3_SPAN = 3 * K3_MAT                                                 # 17,547,264
+K3_H_BYTES = TOP_K * K3_INTER * 4
+K3_KERNEL_BYTES = {
+    "glu_decode": 2 * TOP_K * K3_MAT + K3_HIDDEN * 4 + K3_H_BYTES,
+    "down_decode": TOP_K * K3_MAT + K3_H_BYTES + K3_HIDDEN * 4,
+}
+K3_LAYER_BYTES = TOP_K * K3_SPAN + 2 * K3_HIDDEN * 4                  # 280,784,896
+
+
+def _decode_caller(moe, _lib, g, bank, stride: int, n_bank: int, x_dtype, tokens: int,
+                   seed: int, settle_s: float = 0.05):
+    """Decode layers with caller routes through k3_hip_moe_layer_device (the
+    provider's per-token call): `tokens` tokens, each 16 distinct experts
+    drawn uniformly from the bank with positive weights summing to one, x
+    N(0,1) in x_dtype, fp32 out.  Returns (result, ids, weights, x, out) after
+    a settle phase, a timed pass and a kernel-stamp pass."""
+    import torch
+
+    lib = _lib.load()
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.choice(n_bank, TOP_K, replace=False) for _ in range(tokens)])
+    w = rng.random((tokens, TOP_K)).astype(np.float32) + 0.05
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    x = moe.synth_normal(tokens * g.hidden, x_dtype, seed, 2).view(tokens, g.hidden)
+    out = torch.empty((tokens, g.hidden), dtype=torch.float32, device="cuda")
+    ws = moe.workspace(g, TOP_K)
+    base, nbytes = moe._ws_args(ws)
+    st = moe.stream_handle()
+    xb = 2 if x_dtype == torch.bfloat16 else 4
+    xcode = _lib.K3_DTYPE_BF16 if x_dtype == torch.bfloat16 else _lib.K3_DTYPE_F32
+    tables = [((C.c_void_p * TOP_K)(*[bank.data_ptr() + int(e) * stride for e in ids[t]]),
+               (C.c_float * TOP_K)(*[float(v) for v in w[t]])) for t in range(tokens)]
+    gref = C.byref(g)
+    x_p, o_p = x.data_ptr(), out.data_ptr()
+
+    def step(t: int) -> None:
+        t %= tokens
+        rc = lib.k3_hip_moe_layer_device(gref, tables[t][0], tables[t][1], TOP_K,
+                                         x_p + t * g.hidden * xb, xcode, o_p + t * g.hidden * 4,
+                                         _lib.K3_DTYPE_F32, base, nbytes, st)
+        if rc != 0:
+            raise _lib.K3HipError(rc, "k3_hip_moe_layer_device")
+
+    t_end = time.perf_counter() + settle_s
+    i = 0
+    while time.perf_counter() < t_end:
+        step(i)
+        i += 1
+        if i % 100 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(tokens):
+        step(t)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / tokens
+    _lib.timing_begin(4 * tokens + 16)
+    for t in range(tokens):
+        step(t)
+    kern, _ = _lib.timing_end()
+    return sec, kern, ids, w, x, out
+
+
+def _k3_decode_bench(moe, _lib, oracle, tokens: int = 300, cpu_seconds: float | None = None,
+                     bank_cfg2=None) -> dict:
+    """The drop-in's own workload: the K3 routed decode layer (16 of 896
+    experts, 3584 / 3072, SiTU, fp32 x and out) with caller routes through
+    k3_hip_moe_layer_device, as the provider calls it
+    (provider_moe.cpp:1664-1669); roofline per decode kernel; the reference
+    CPU path beside it (the whole-set mxfp4_moe_expert_set,
+    tools/fused_gemv_batch.c:465-518, on host copies of the same experts).
+    With bank_cfg2, also the benchmark geometry (preset 2) with caller routes
+    and fp32 / bf16 x, against its router-mode kernels."""
+    import torch
+
+    g = moe.preset(1)
+    assert g.hidden == K3_HIDDEN and g.intermediate == K3_INTER and g.expert_span == K3_SPAN
+    bank = torch.empty(K3_BANK * K3_SPAN, dtype=torch.uint8, device="cuda")
+    moe.synth_bank(g, bank, K3_SPAN, K3_BANK, 0, SEED + 80)
+    torch.cuda.synchronize()
+    sec, kern, ids, w, x, out = _decode_caller(moe, _lib, g, bank, K3_SPAN, K3_BANK,
+                                               torch.float32, tokens, SEED + 81)
+    kus = {k: round(v["avg_ms"] * 1e3, 3) for k, v in kern.items()}
+    roof = {k: {"us": kus[k], "gbs": round(K3_KERNEL_BYTES[k] / (kus[k] * 1e-6) / 1e9, 1),
+                "frac": round(K3_KERNEL_BYTES[k] / (kus[k] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "algorithmic_bytes": K3_KERNEL_BYTES[k]}
+            for k in K3_KERNEL_BYTES if k in kus}
+    res = {
+        "workload": (f"K3 routed decode layer: {TOP_K} of {K3_BANK} experts ({K3_BANK * K3_SPAN / 1e9:.1f}"
+                     f" GB bank in HBM), hidden {K3_HIDDEN}, intermediate {K3_INTER}, SiTU, fp32 x "
+                     f"and out, caller routes (16 distinct uniform experts, positive weights) "
+                     f"through k3_hip_moe_layer_device, {tokens} seeded tokens"),
+        "us_per_token": round(sec * 1e6, 2),
+        "token_layers_per_s": round(1.0 / sec, 1),
+        "layer_bytes_per_token": K3_LAYER_BYTES,
+        "achieved_gbs": round(K3_LAYER_BYTES / sec / 1e9, 1),
+        "hbm_frac": round(K3_LAYER_BYTES / sec / 1e9 / HBM_PEAK_GBS, 4),
+        "kernels_us": kus,
+        "roofline": roof,
+    }
+    # Oracle check of two tokens (fp32 out against the fp64 oracle).
+    errs = []
+    for t in (0, tokens - 1):
+        spans = [oracle.synth_expert(SEED + 80, int(e), K3_HIDDEN, K3_INTER) for e in ids[t]]
+        ref, mag = oracle.moe_layer_f64(spans, w[t].astype(np.float64), K3_HIDDEN, K3_INTER,
+                                        g.activation, x[t].cpu().numpy())
+        errs.append(oracle.cond_rel_err(out[t].cpu().numpy(), ref, mag, K3_INTER))
+    res["oracle_max_cond_rel_err"] = float(max(errs))
+    if cpu_seconds:
+        threads = cpu_threads()
+        ref = oracle.ref()
+        ref.mxfp4_pool_init(threads)
+        host = {}
+        n, el, diffs = 0, 0.0, []
+        xh = x.cpu().numpy()
+        outh = out.cpu().numpy()
+        while n < tokens and el < cpu_seconds:
+            for e in ids[n]:
+                if int(e) not in host:
+                    host[int(e)] = bank[int(e) * K3_SPAN:(int(e) + 1) * K3_SPAN].cpu().numpy()
+            spans = [host[int(e)] for e in ids[n]]
+            if n == 0:
+                oracle.ref_expert_set(spans, w[n], xh[n], K3_HIDDEN, K3_INTER, threads)  # warm
+            t0 = time.perf_counter()
+            y = oracle.ref_expert_set(spans, w[n], xh[n], K3_HIDDEN, K3_INTER, threads)
+            el += time.perf_counter() - t0
+            diffs.append(float(np.max(np.abs(y - outh[n])) / np.max(np.abs(y))))
+            n += 1
+        rate = n / el
+        res["cpu_baseline"] = {
+            "value": round(rate, 2), "unit": "token-layers/s", **_cpu_env(threads),
+            "kind": "reference",
+            "sample": (f"first {n} tokens of the same workload: mxfp4_moe_expert_set (SiTU, "
+                       f"{threads} pool threads) on host copies of their experts ({el:.1f} s of "
+                       f"calls)"),
+            "achieved_gbs": round(rate * K3_LAYER_BYTES / 1e9, 1),
+            "gpu_vs_cpu_max_diff_over_max_abs": float(max(diffs)),
+        }
+    del bank
+    torch.cuda.empty_cache()
+    if bank_cfg2 is not None:
+        g2 = moe.preset(2)
+        cmp = {}
+        for name, dt in (("fp32_x", torch.float32), ("bf16_x", torch.bfloat16)):
+            s2, k2, *_ = _decode_caller(moe, _lib, g2, bank_cfg2, SPAN, N_BANK, dt, tokens,
+                                        SEED + 82)
+            cmp[name] = {"us_per_token": round(s2 * 1e6, 2),
+                         "kernels_us": {k: round(v["avg_ms"] * 1e3, 3) for k, v in k2.items()}}
+        res["preset2_caller_routes"] = cmp
+    return res
+
+
+def _caller_summary(res: dict, nbytes_alg: float, batches: int) -> dict:
+    """k3_hip_moe_verify_device over the routes the device router chose, as a
+    provider hands them over (span tables + weights): AUTO and the per-position
+    path, whose runs of equal edge counts are one position-batched launch
+    pair; the kernel split shows which path AUTO took."""
+    out = {}
+    for path in ("caller_auto", "caller_positions"):
+        sec, kern = res[path]
+        kus = {k: round(v["total_ms"] * 1e3 / batches, 2) for k, v in (kern or {}).items()}
+        out[path[len("caller_"):]] = {
+            "us_per_batch": round(sec * 1e6, 1),
+            "achieved_gbs": round(nbytes_alg / sec / 1e9, 1),
+            "hbm_frac": round(nbytes_alg / sec / 1e9 / HBM_PEAK_GBS, 4),
+            "kernels_us": kus,
+        }
+    out["auto_path"] = "union_mfma" if "glu_mfma" in out["auto"]["kernels_us"] else "positions"
     return out
 
 

@@ -177,7 +177,8 @@ SIGNATURES = {
     "k3_hip_cache_plan": (_i32, [_vp, _u64, _i32, _vp, _i32, _vp, C.POINTER(_i32)]),
     "k3_hip_cache_fetch": (_i32, [_vp, _u64, _vp, _i32]),
     "k3_hip_cache_resolve": (_i32, [_vp, _u64, _vp, _i32, _vp, _vp]),
-    "k3_hip_cache_ready_subset": (_i32, [_vp, _u64, _vp, _i32, _vp, _vp]),
+    "k3_hip_cache_ready_subset": (_i32, [_vp, _u64, _vp, _i32, _vp]),
+    "k3_hip_cache_ready_subset_v2": (_i32, [_vp, _u64, _vp, _i32, _vp, _vp]),
     "k3_hip_cache_release": (None, [_vp, _u64]),
     "k3_hip_cache_configure": (_i32, [_vp, C.POINTER(K3HipCachePolicyV1)]),
     "k3_hip_cache_budget": (_i32, [_vp, C.POINTER(C.c_longlong)]),

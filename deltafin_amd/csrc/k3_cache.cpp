@@ -566,7 +566,12 @@ int k3_hip_cache_resolve(K3HipCache* c, uint64_t plan_id, const uint16_t* ids, i
 }
 
 int k3_hip_cache_ready_subset(K3HipCache* c, uint64_t plan_id, const uint16_t* ids, int n,
-                              const uint8_t** device_spans, void* stream) {
+                              const uint8_t** device_spans) {
+  return k3_hip_cache_ready_subset_v2(c, plan_id, ids, n, device_spans, nullptr);
+}
+
+int k3_hip_cache_ready_subset_v2(K3HipCache* c, uint64_t plan_id, const uint16_t* ids, int n,
+                                 const uint8_t** device_spans, void* stream) {
   if (!c || !ids || n < 0 || (n > 0 && !device_spans))
     return fail(K3_HIP_E_INVALID, "cache ready: invalid arguments");
   std::lock_guard<std::mutex> lk(c->mu);
@@ -614,13 +619,20 @@ void k3_hip_cache_release(K3HipCache* c, uint64_t plan_id) {
         if (d.first == st) ev = d.second;
       const bool fresh = ev == nullptr;
       if (fresh) ev = c->take_event();
-      if (!ev) continue;
-      if (hipEventRecord(ev, st) != hipSuccess) {
-        (void)hipGetLastError();
-        if (fresh) c->event_pool.push_back(ev);
+      hipError_t e = ev ? hipEventRecord(ev, st) : hipErrorOutOfMemory;
+      if (e == hipSuccess) {
+        if (fresh) s.done.emplace_back(st, ev);
         continue;
       }
-      if (fresh) s.done.emplace_back(st, ev);
+      // No reuse point for this stream: the host waits for the stream
+      // instead, so nothing queued there can still read the slot when it is
+      // refilled; if that fails too, the cache fails closed.
+      (void)hipGetLastError();
+      if (ev && fresh) c->event_pool.push_back(ev);
+      if ((e = hipStreamSynchronize(st)) != hipSuccess) {
+        (void)runtime_fail_locked(c, "cache release: no reuse point for a stream", e);
+        return;
+      }
     }
   };
   for (int s : p->hit_slots) mark(s);

@@ -307,10 +307,10 @@ class ExpertCache:
         n = len(ids)
         a = (C.c_uint16 * n)(*ids)
         out = (C.c_void_p * n)()
-        rc = self._lib.k3_hip_cache_ready_subset(self.handle, plan_id, a, n, out,
+        rc = self._lib.k3_hip_cache_ready_subset_v2(self.handle, plan_id, a, n, out,
                                                  stream if stream is not None else stream_handle())
         if rc < 0:
-            raise K3HipError(rc, "k3_hip_cache_ready_subset")
+            raise K3HipError(rc, "k3_hip_cache_ready_subset_v2")
         return [int(out[i]) if out[i] else None for i in range(n)]
 
     def configure(self, automatic: bool, capacity: int = 0,

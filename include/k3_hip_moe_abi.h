@@ -378,12 +378,19 @@ int k3_hip_cache_resolve(K3HipCache* cache, uint64_t plan_id,
  * wait); others get NULL.  `stream` is where the caller will read them:
  * release orders the slots' reuse after the work queued there.  Returns the
  * number resident. */
+int k3_hip_cache_ready_subset_v2(K3HipCache* cache, uint64_t plan_id,
+                                 const uint16_t* ids, int n,
+                                 const uint8_t** device_spans, void* stream);
+/* The first form, without a stream: the caller reads the spans on the null
+ * stream (k3_hip_cache_ready_subset_v2 with stream NULL). */
 int k3_hip_cache_ready_subset(K3HipCache* cache, uint64_t plan_id,
                               const uint16_t* ids, int n,
-                              const uint8_t** device_spans, void* stream);
+                              const uint8_t** device_spans);
 /* Finish or cancel a plan (provider_cuda_moe.cpp:1166-1168).  Slots the plan
  * pinned are reused only after the work queued so far on every stream the
- * plan resolved on (resolve / ready_subset). */
+ * plan resolved on (resolve / ready_subset): release records a reuse event on
+ * each, and where it cannot, waits on the host for that stream (and fails the
+ * cache closed if even that fails). */
 void k3_hip_cache_release(K3HipCache* cache, uint64_t plan_id);
 /* Bounded device-to-host copy of the plan's pinned hits only, for the
  * caller's exact CPU reconstruction of the tile

@@ -14,6 +14,11 @@ of the routed experts, with the exact bf16 input the step consumed (max
 relative error <= 1e-3), and resident entries read back byte for byte.
 Follows the reference's plan/upload/execute sequence
 (provider_cuda_moe.cpp:757-805, :963-1164).
+
+A second case runs config 4 at its route width: top-16 Zipf routes over 40
+experts per layer (three layers, pinned / pageable / pinned), a 24-slot cache
+(the working set is 120 experts, so every layer's misses evict other layers'
+entries), with the same checks.
 """
 import ctypes as C
 
@@ -25,7 +30,6 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
-LAYERS, PER_LAYER, K, SLOTS, TOKENS = 3, 12, 4, 10, 12
 PINNED = (True, False, True)
 SEED = 4242
 
@@ -34,23 +38,26 @@ def say(msg):
     print(f"[gpu-case] {msg}", flush=True)
 
 
-def _routes(total):
+def _routes(total, layers, per_layer, k):
     rng = np.random.default_rng(SEED)
-    perms = [rng.permutation(PER_LAYER) for _ in range(LAYERS)]
-    pz = np.arange(1, PER_LAYER + 1, dtype=np.float64) ** -1.1
+    perms = [rng.permutation(per_layer) for _ in range(layers)]
+    pz = np.arange(1, per_layer + 1, dtype=np.float64) ** -1.1
     pz /= pz.sum()
-    r = np.empty((total, LAYERS, K), np.int64)
+    r = np.empty((total, layers, k), np.int64)
     for t in range(total):
-        for layer in range(LAYERS):
-            r[t, layer] = np.sort(perms[layer][rng.choice(PER_LAYER, K, replace=False, p=pz)])
-    w = rng.random((total, LAYERS, K)).astype(np.float32)
+        for layer in range(layers):
+            r[t, layer] = np.sort(perms[layer][rng.choice(per_layer, k, replace=False, p=pz)])
+    w = rng.random((total, layers, k)).astype(np.float32)
     w /= w.sum(axis=2, keepdims=True)
     return r, w
 
 
-def test_streamed_layers_pinned_and_pageable_vs_oracle(gpu):
+@pytest.mark.parametrize("PER_LAYER,K,SLOTS,TOKENS,every", [(12, 4, 10, 12, 3), (40, 16, 24, 6, 4)],
+                         ids=["top4_of_12", "top16_of_40"])
+def test_streamed_layers_pinned_and_pageable_vs_oracle(gpu, PER_LAYER, K, SLOTS, TOKENS, every):
     import torch
     from deltafin_amd import _lib, moe
+    LAYERS = len(PINNED)
     g = moe.preset(2)
     span = g.expert_span
     say(f"streamed: {LAYERS} layers x {PER_LAYER} experts, cache {SLOTS} slots, pinned {PINNED}")
@@ -64,7 +71,7 @@ def test_streamed_layers_pinned_and_pageable_vs_oracle(gpu):
         hosts.append(h)
     torch.cuda.synchronize()
     del dev
-    routes, weights = _routes(TOKENS)
+    routes, weights = _routes(TOKENS, LAYERS, PER_LAYER, K)
     cache = moe.ExpertCache(span, SLOTS, LAYERS, staging_slots=2)
     ws = moe.workspace(g, K)
     x = moe.synth_normal(g.hidden, torch.bfloat16, SEED, 9)
@@ -89,7 +96,7 @@ def test_streamed_layers_pinned_and_pageable_vs_oracle(gpu):
     assert st["evictions"] > 0 and st["misses"] > SLOTS
     worst = 0.0
     for i, (t, layer, xin, out) in enumerate(steps):
-        if i % 3 != 1 and i != len(steps) - 1:
+        if i % every != 1 and i != len(steps) - 1:
             continue
         hb = hosts[layer].numpy()
         sp = [hb[e * span:(e + 1) * span] for e in routes[t, layer]]
