@@ -3,10 +3,11 @@ k3_hip_moe_route_layer_device): top-k of the logits (descending, lower index
 on ties, NaN ranked as -inf, -0 equal to +0) and a softmax over the selected
 logits, the semantics of oracle.topk_softmax.
 
-Where a sweep iteration covers one expert (config-2 shape on a 256-CU device)
-and n_bank <= 512, the gate/up kernel requests its first two units from a
-register top-2 before the full ranking; larger banks take the ranking first.
-Both must select exactly the oracle's experts, and the layer output must be
+Every gate/up workgroup ranks the logits in LDS (block_topk: each key ranked
+within its 64-key segment, then the segment candidates ranked against each
+other); a bank of up to one key per thread has its logits preloaded ahead of
+the activation chunk, a larger bank is read in the ranking's fill loop.  Both
+must select exactly the oracle's experts, and the layer output must be
 bit-identical to a caller-routed call (explicit spans and the returned
 weights), which shares every kernel but the router.
 """
@@ -85,7 +86,8 @@ def test_router_edge_cases(gpu):
 
 @pytest.mark.parametrize("n_bank", [512, 513])
 def test_router_bank_size_boundary(gpu, n_bank):
-    """512 logits: the register top-2 path's limit; 513: the full ranking first."""
+    """512 logits: one preloaded key per thread of the 512-thread workgroup;
+    513: the key past the workgroup is read in the ranking's fill loop."""
     from deltafin_amd import moe
     g = moe.preset(2)
     say(f"router bank {n_bank}")
