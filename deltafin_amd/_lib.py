@@ -192,6 +192,7 @@ SIGNATURES = {
     "k3_hip_timing_end": (_i32, [C.POINTER(K3HipKernelTimingV1), _i32, C.POINTER(_i32),
                                  C.POINTER(C.c_longlong)]),
     "k3_hip_set_fused_decode": (_i32, [_i32]),
+    "k3_hip_set_decode_mfma": (_i32, [_i32]),
     "k3_hip_set_verify_mode": (_i32, [_i32]),
     "k3_hip_scale4_check_header": (_i32, [_vp, _u64]),
     "k3_hip_synth_bank": (_i32, [_GP, _vp, _u64, _i32, _u64, _u64, _i32, _i32, _vp]),
@@ -311,6 +312,18 @@ def set_fused_decode(enabled: bool) -> bool:
     """Select the fused single-launch decode path or the two-launch path (the
     default) for later layer calls; returns the previous setting."""
     return bool(load().k3_hip_set_fused_decode(1 if enabled else 0))
+
+
+DECODE_DOTS_VALU, DECODE_DOTS_MFMA_F32, DECODE_DOTS_MFMA_ALL = 0, 1, 2
+
+
+def set_decode_mfma(mode: int) -> int:
+    """Select where the single-token gate/up dots run (DECODE_DOTS_*) for
+    later layer calls; returns the previous setting."""
+    rc = load().k3_hip_set_decode_mfma(int(mode))
+    if rc < 0:
+        raise K3HipError(rc, "k3_hip_set_decode_mfma")
+    return rc
 
 
 VERIFY_AUTO, VERIFY_POSITIONS, VERIFY_UNION_MFMA, VERIFY_UNION_VALU = 0, 1, 2, 3

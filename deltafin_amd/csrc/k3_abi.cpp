@@ -1647,6 +1647,8 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
 
 int k3_hip_set_fused_decode(int enabled) { return set_fused_decode(enabled); }
 
+int k3_hip_set_decode_mfma(int mode) { return set_decode_mfma(mode); }
+
 int k3_hip_set_verify_mode(int mode) {
   if (mode < K3_VERIFY_AUTO || mode > K3_VERIFY_UNION_VALU)
     return fail(K3_HIP_E_INVALID, "verify mode %d unknown", mode);

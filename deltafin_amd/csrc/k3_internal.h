@@ -141,6 +141,10 @@ int launch_decode_positions(const Geo& g, const TokenRoute& route, int n_positio
 // Process-wide decode path switch (k3_hip_set_fused_decode); returns the
 // previous setting.
 int set_fused_decode(int enabled);
+// Process-wide choice of the single-token gate/up dots (k3_hip_set_decode_mfma:
+// 0 VALU, 1 matrix cores for fp32 activations, 2 also for bf16); returns the
+// previous setting, or K3_HIP_E_INVALID for another value.
+int set_decode_mfma(int mode);
 // LDS bytes the in-kernel router needs for a bank of n_bank logits and top_k.
 size_t route_scratch_bytes(int n_bank, int top_k);
 int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride,

@@ -563,6 +563,16 @@ struct PosStride {
 // Unit pipelines per gate/up workgroup (each S column-split waves) and rows
 // per unit; the launch bound follows so the register budget matches the
 // resident waves (16 waves/CU -> 128 VGPRs, 8 -> 256).
+// k_glu_decode refills a unit's registers with the next unit's loads row by
+// row (finish_refill) for fp32 activations: K3 gate/up 37.4 -> 34.9 us on
+// MI355X.  With bf16 activations the row-pinned schedule costs more than it
+// keeps in flight (the benchmark layer's gate/up 41.1 -> 43.0 us), so those
+// keep the unit-at-a-time loop.
+#ifndef K3_GLU_REFILL
+#define K3_GLU_REFILL 1
+#endif
+template <typename XT>
+constexpr bool kGluRefill = K3_GLU_REFILL && sizeof(XT) == 4;
 #ifndef K3_GLU_GROUPS
 #define K3_GLU_GROUPS 2
 #endif
@@ -587,7 +597,8 @@ __device__ __forceinline__ int xcd_block_id(int k, int G) {
 }
 
 template <typename XT, int kR, bool kG, bool kS4 = false, bool kPos = false>
-__global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute route_arg,
+__global__ __launch_bounds__(kGluMaxThreads) __attribute__((amdgpu_waves_per_eu(1, kGluMaxThreads / 256)))
+void k_glu_decode(const TokenRoute route_arg,
                                                      const Geo g,
                                                      const XT* __restrict__ x_arg,
                                                      float* __restrict__ h_arg, int n_units,
@@ -713,7 +724,126 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
       h[(size_t)u * kR + lane] = activate(g.act, gv, uv);
     }
   };
+  // Where unit it's loads go: its span and first row, or, past the end, every
+  // lane at unit 0's bases (row and lane offsets zero).
+  struct UnitAt {
+    const uint8_t* span;
+    size_t r0, rstep, loff, soff;
+    int e;
+    bool valid;
+  };
+  const int G = g.hidden >> 5;
+  const size_t cp = (size_t)g.hidden >> 1;
+  auto unit_at = [&](int it) {
+    UnitAt n;
+    const int un = q0 + it * Q;
+    n.valid = un < n_units;  // wave-uniform
+    const int pair0 = (n.valid ? un : 0) * kR;
+    n.e = pair0 / g.inter;
+    n.span = span_of(rr, n.e);
+    n.r0 = (size_t)(pair0 - n.e * g.inter);
+    n.rstep = n.valid ? cp : 0;
+    n.loff = n.valid ? (size_t)cs.cc * 16 : 0;
+    n.soff = n.valid ? (size_t)gg.off : 0;
+    return n;
+  };
+  // The loads of a unit in one fixed order (scale dwords, then row by row
+  // gate and up chunks with their scale bytes), pinned by scheduling barriers,
+  // so the wait counts in the loop see the same order from every path.
+  auto issue_scales = [&](GluBatch<XT, kR, kG, kS4>& bt, const UnitAt& n) {
+    if constexpr (kS4) {
+      const size_t so = n.r0 * (size_t)(G >> 1) + n.soff;
+      bt.sg[0] = load_u32(n.span + g.w1s + so);
+      bt.su[0] = load_u32(n.span + g.w3s + so);
+      bt.b4 = __builtin_amdgcn_readlane(rb4, n.e);
+    } else if constexpr (kG) {
+      const size_t so = n.r0 * (size_t)G + n.soff;
+      bt.sg[0] = load_u32(n.span + g.w1s + so);
+      bt.su[0] = load_u32(n.span + g.w3s + so);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto issue_row = [&](GluBatch<XT, kR, kG, kS4>& bt, const UnitAt& n, int r) {
+    const size_t wo = n.r0 * cp + r * n.rstep + n.loff;
+    bt.wg[r] = load_chunk(n.span + g.w1p + wo);
+    bt.wu[r] = load_chunk(n.span + g.w3p + wo);
+    if constexpr (!kG) {
+      const size_t so = n.r0 * (size_t)G + r * (n.valid ? (size_t)G : 0) + (n.valid ? cs.cc : 0);
+      bt.sg[r] = load_scale(n.span + g.w1s + so);
+      bt.su[r] = load_scale(n.span + g.w3s + so);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto issue_unit = [&](GluBatch<XT, kR, kG, kS4>& bt, int it) {
+    const UnitAt n = unit_at(it);
+    issue_scales(bt, n);
+#pragma unroll
+    for (int r = 0; r < kR; ++r) issue_row(bt, n, r);
+  };
+  if constexpr (kGluRefill<XT>) {
+  // Unit it's dots with bt refilled by unit it + 2 as its registers free up:
+  // every row's scale first (then the scale registers take the next unit's),
+  // then row r's products and right after them row r's next chunks.  The wave
+  // so keeps about two units' loads in flight through the products, instead
+  // of one between a unit's first product and its buffer's next request.  A
+  // unit past the end is requested as one 16-byte line and stores nothing, so
+  // every load is unconditional and the wait counts stay exact.  The
+  // arithmetic per row is that of finish above.
+  auto finish_refill = [&](GluBatch<XT, kR, kG, kS4>& bt, int it) {
+    const int u = q0 + it * Q;
+    const int parity = it & 1;
+    float sgv[kR], suv[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      if constexpr (kS4) {
+        sgv[r] = e8m0_scale(gathered_scale4(bt.sg[0], bt.b4 & 0xffu, gg.bp, row_step, r, lane));
+        suv[r] = e8m0_scale(
+            gathered_scale4(bt.su[0], (bt.b4 >> 16) & 0xffu, gg.bp, row_step, r, lane));
+      } else if constexpr (kG) {
+        sgv[r] = e8m0_scale(gathered_scale(bt.sg[0], gg.bp, row_step, r, lane));
+        suv[r] = e8m0_scale(gathered_scale(bt.su[0], gg.bp, row_step, r, lane));
+      } else {
+        sgv[r] = e8m0_scale(bt.sg[r]);
+        suv[r] = e8m0_scale(bt.su[r]);
+      }
+    }
+    const UnitAt n = unit_at(it + 2);
+    issue_scales(bt, n);
+    float v[N];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      v[r] = xc.dot(bt.wg[r]) * sgv[r];
+      v[kR + r] = xc.dot(bt.wu[r]) * suv[r];
+      issue_row(bt, n, r);
+    }
+    wave_reduce_multi<N>(v, lane);
+    if ((lane & ((1 << (6 - L)) - 1)) == 0) red[parity][wave][lane >> (6 - L)] = v[0];
+    lds_barrier();
+    if (u < n_units && gw == 0 && lane < kR) {
+      const int w0 = grp * S;
+      float gv = red[parity][w0][lane], uv = red[parity][w0][kR + lane];
+      for (int w = 1; w < S; ++w) {
+        gv += red[parity][w0 + w][lane];
+        uv += red[parity][w0 + w][kR + lane];
+      }
+      h[(size_t)u * kR + lane] = activate(g.act, gv, uv);
+    }
+  };
+  GluBatch<XT, kR, kG, kS4> A, B;
+  issue_unit(A, 0);
+  issue_unit(B, 1);
+  // iters is the same in every pipeline; with iters odd the last B unit is
+  // past the end (its loads are the one-line dummy, it stores nothing).
+  for (int it = 0; it < iters; it += 2) {
+    finish_refill(A, it);
+    finish_refill(B, it + 1);
+  }
+  } else {
   // Two units in flight: unit it + 1 is requested before unit it is reduced.
+  // (The compiler merges the loop head's wait counts over the entry and the
+  // back edge, so at the head the wave waits for both units; a loop that
+  // keeps exactly one unit in flight through every reduction measured slower
+  // with bf16 activations: 43.9 against 40.9 us on the benchmark layer.)
   GluBatch<XT, kR, kG, kS4> A, B;
   glu_load(A, rr, g, unit_pair0(0), cs, gg, rb4);
   glu_load(B, rr, g, unit_pair0(min(1, iters - 1)), cs, gg, rb4);
@@ -730,6 +860,405 @@ __global__ __launch_bounds__(kGluMaxThreads) void k_glu_decode(const TokenRoute 
       break;
     }
     glu_load(B, rr, g, unit_pair0(it + 3), cs, gg, rb4);
+  }
+  }
+}
+
+// ======================================================================
+// decode phase A on the matrix cores: k_glu_mfma
+// ======================================================================
+// The gate/up rows of k_glu_decode on v_mfma_f32_16x16x32_bf16, for raw-v1
+// spans and one token.  Operand layout of that MFMA on gfx950 (measured with a
+// one-hot probe): A lane l = row l % 16, K = 8 (l / 16) .. +7; B lane l =
+// column l % 16, the same K; D lane l = column l % 16, rows 4 (l / 16) .. +3.
+//
+// Tiles of 8 weight rows, parity split: lane l (r = l % 16, g = l / 16) loads
+// the 16-byte chunk of weight row r / 2 at byte 32 g + 16 (r % 2) of a
+// 128-byte line, so one dwordx4 load covers 8 rows x a whole line (256
+// columns: a K block) and MFMA row r is weight row r / 2 restricted to the
+// block's chunks of parity r % 2.  Dword m of the chunk (columns
+// 256 kb + 64 g + 32 (r % 2) + 8 m .. +7) becomes A's 8 bf16 through four
+// v_cvt_scalef32_pk_bf16_fp4 with the chunk's scale folded in.  The convert
+// applies the exponent field of its fp32 scale operand as an E8M0 scale, so
+// the operand is the E8M0 byte shifted into that field (2^(s-127) for s in
+// 1..254, NaN for 255, which poisons the row as the reference does); fp4
+// times a power of two is exact in bf16.  The reference reads scale byte 0 as
+// +0.0 where the convert would apply 2^-127, so a chunk with scale byte 0 has
+// its codes zeroed first.
+//
+// The activation enters as NT bf16 terms whose sum is x exactly (bf16 x: one
+// term; fp32 x: t0 = bf16(x), t1 = bf16(x - t0), t2 = bf16(x - t0 - t1), each
+// remainder exact in fp32), staged once per workgroup in LDS.  B column t
+// (t < NT) holds term t at the K block's even-parity columns and column 8 + t
+// the same term at the odd parity; the other columns read a row of zeros.
+// Products of a bf16 term with fp4 x 2^k are exact in fp32, so the dot
+// differs from the VALU kernel's fp32 chain only in summation order.  Row i's
+// dot is D[2 i][t] + D[2 i + 1][8 + t] summed over t: lane (n, g) holds
+// D[4 g + j][n] in acc[j], so rows 2 g and 2 g + 1 are the 16-lane sums of
+// (n < 8 ? acc[0] : acc[1]) and (n < 8 ? acc[2] : acc[3]); the columns
+// without a term are exact zeros.
+//
+// Work split as in k_glu_decode: a unit is one expert's gate and up tiles (8
+// rows each); a pipeline of S waves splits a row's KB K blocks (NB = KB / S
+// per wave); pipeline q takes units q, q + Q, ... with two units in flight,
+// the S partials meet in LDS and wave 0 of the pipeline applies the
+// activation.  A wave's unit is 2 NB dwordx4 weight loads plus NR =
+// ceil(NB / 4) scale dwords per tile: in register j, lane l holds dword l % 2
+// of the 8 scale bytes of row (l % 16) / 2 in K block 4 j + l / 16, and lane
+// (r, g) takes its byte of block b from lane 16 (b % 4) + 2 (r / 2) + g / 2
+// of register b / 4 by ds_bpermute.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// kS4 (scale4-v2): a row's 8 groups of a K block are 8 index nibbles, one
+// dword, so one register per matrix holds 8 blocks x 8 rows (lane l: block
+// l / 8, row l % 8) and b4 holds the span's scale bases (byte 0: w1, byte 2:
+// w3).
+template <int NB, bool kS4>
+struct GmUnit : std::conditional_t<kS4, SpanBases, NoBases> {
+  static constexpr int NR = kS4 ? (NB + 7) / 8 : (NB + 3) / 4;
+  u32x4 wg[NB], wu[NB];
+  uint32_t sg[NR], su[NR];
+};
+
+// Unit loads at rows r0 .. r0 + 7 of the gate and up matrices of `span`, K
+// blocks kb0 .. kb0 + NB - 1 (scale dwords first, so waiting for them never
+// waits for the weights).  rstep / loff: the byte step between a lane's rows
+// and its lane offset (0 and 0 turn every lane's loads into one line at the
+// unit's bases, for a unit past the end); b4: the span's scale bases.
+template <int NB, bool kS4>
+__device__ __forceinline__ void gm_issue_scales(GmUnit<NB, kS4>& u, const uint8_t* span,
+                                                const Geo& g, size_t r0, int kb0, int lane,
+                                                bool valid, uint32_t b4) {
+  const int G = g.hidden >> 5;
+#pragma unroll
+  for (int j = 0; j < GmUnit<NB, kS4>::NR; ++j) {
+    size_t so;
+    if constexpr (kS4) {
+      const int bb = min(8 * j + (lane >> 3), NB - 1);
+      so = (r0 + (valid ? (size_t)(lane & 7) : 0)) * (size_t)(G >> 1) + 4 * (size_t)(kb0 + bb);
+    } else {
+      const int bb = min(4 * j + (lane >> 4), NB - 1);
+      so = (r0 + (valid ? (size_t)((lane & 15) >> 1) : 0)) * (size_t)G +
+           8 * (size_t)(kb0 + bb) + (valid ? 4 * (size_t)(lane & 1) : 0);
+    }
+    u.sg[j] = load_u32(span + g.w1s + so);
+    u.su[j] = load_u32(span + g.w3s + so);
+  }
+  if constexpr (kS4) u.b4 = b4;
+}
+
+// Byte offset of this lane's chunk of K block 0 in the gate (or up) matrix.
+__device__ __forceinline__ size_t gm_chunk_off(const Geo& g, size_t r0, int kb0, int lane,
+                                               bool valid) {
+  return valid ? (r0 + ((lane & 15) >> 1)) * ((size_t)g.hidden >> 1) + 128 * (size_t)kb0 +
+                     32 * (lane >> 4) + 16 * (lane & 1)
+               : r0 * ((size_t)g.hidden >> 1);
+}
+
+template <int NB, bool kS4>
+__device__ __forceinline__ void gm_load(GmUnit<NB, kS4>& u, const uint8_t* span, const Geo& g,
+                                        size_t r0, int kb0, int lane, bool valid, uint32_t b4) {
+  gm_issue_scales<NB, kS4>(u, span, g, r0, kb0, lane, valid, b4);
+  const size_t wo = gm_chunk_off(g, r0, kb0, lane, valid);
+  const size_t bs = valid ? 128 : 0;
+  const uint8_t* gp = span + g.w1p + wo;
+  const uint8_t* up = span + g.w3p + wo;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    u.wg[b] = load_chunk(gp + bs * b);
+    u.wu[b] = load_chunk(up + bs * b);
+  }
+}
+
+// Dword d of a chunk (8 codes) as A's 8 bf16, times the scale whose E8M0 byte
+// is in the exponent field of sc.
+__device__ __forceinline__ bf16x8 gm_cvt(uint32_t d, float sc) {
+  const v2bf a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, sc, 0);
+  const v2bf b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, sc, 1);
+  const v2bf c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, sc, 2);
+  const v2bf e = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, sc, 3);
+  const u32x4 w = {__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                   __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, e)};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// A tile's chunk of K block b with its scale byte s (byte 0: all codes zero).
+__device__ __forceinline__ u32x4 gm_zero_if(u32x4 w, uint32_t s) {
+  const bool z = s == 0u;
+  w.x = z ? 0u : w.x;
+  w.y = z ? 0u : w.y;
+  w.z = z ? 0u : w.z;
+  w.w = z ? 0u : w.w;
+  return w;
+}
+
+// The 16-lane sums of the unit's four per-lane values: (gate row 2 g, gate
+// row 2 g + 1, up row 2 g, up row 2 g + 1) of lane group g.  kRefill: the
+// registers of u are refilled with the unit at (nspan, nr0) as they free up
+// (its scale dwords once every block's scale byte is extracted, block b's
+// chunks right after block b's products), so the wave keeps about two units'
+// loads in flight through the products instead of one.
+template <int NB, bool kS4, bool kRefill>
+__device__ __forceinline__ void gm_dots(GmUnit<NB, kS4>& u, const uint8_t* xb, int lane,
+                                        float (&v)[4], const uint8_t* nspan, const Geo& g,
+                                        size_t nr0, int kb0, bool nvalid, uint32_t nb4) {
+  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+  uint32_t sgb[NB], sub[NB];
+  if constexpr (kS4) {
+    // group 2 g + h of row (l % 16) / 2 in block b: nibble 2 g + h of lane
+    // 8 b + row's dword
+    const int sh = 4 * (2 * (lane >> 4) + (lane & 1));
+    const int src = 4 * ((lane & 15) >> 1);
+    const uint32_t bg = u.b4 & 0xffu, bu = (u.b4 >> 16) & 0xffu;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      sgb[b] = bg + (((uint32_t)__builtin_amdgcn_ds_bpermute(src + 32 * (b & 7),
+                                                             (int)u.sg[b >> 3]) >> sh) & 0xfu);
+      sub[b] = bu + (((uint32_t)__builtin_amdgcn_ds_bpermute(src + 32 * (b & 7),
+                                                             (int)u.su[b >> 3]) >> sh) & 0xfu);
+    }
+  } else {
+    const int sh = 8 * (2 * ((lane >> 4) & 1) + (lane & 1));
+    const int src = 4 * ((lane & 14) + (lane >> 5));
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      sgb[b] = ((uint32_t)__builtin_amdgcn_ds_bpermute(src + 64 * (b & 3), (int)u.sg[b >> 2]) >>
+                sh) & 0xffu;
+      sub[b] = ((uint32_t)__builtin_amdgcn_ds_bpermute(src + 64 * (b & 3), (int)u.su[b >> 2]) >>
+                sh) & 0xffu;
+    }
+  }
+  const uint8_t* ngp = nullptr;
+  const uint8_t* nup = nullptr;
+  const size_t bs = nvalid ? 128 : 0;
+  if constexpr (kRefill) {
+    gm_issue_scales<NB, kS4>(u, nspan, g, nr0, kb0, lane, nvalid, nb4);
+    const size_t wo = gm_chunk_off(g, nr0, kb0, lane, nvalid);
+    ngp = nspan + g.w1p + wo;
+    nup = nspan + g.w3p + wo;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float cg = e8m0_scale(sgb[b]), cu = e8m0_scale(sub[b]);
+    const u32x4 wg = gm_zero_if(u.wg[b], sgb[b]), wu = gm_zero_if(u.wu[b], sub[b]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const bf16x8 bx = *reinterpret_cast<const bf16x8*>(xb + 2 * (256 * b + 8 * m));
+      ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gm_cvt(wg[m], cg), bx, ag, 0, 0, 0);
+      au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gm_cvt(wu[m], cu), bx, au, 0, 0, 0);
+    }
+    if constexpr (kRefill) {
+      u.wg[b] = load_chunk(ngp + bs * b);
+      u.wu[b] = load_chunk(nup + bs * b);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  const bool lo = (lane & 8) == 0;
+  v[0] = lo ? ag[0] : ag[1];
+  v[1] = lo ? ag[2] : ag[3];
+  v[2] = lo ? au[0] : au[1];
+  v[3] = lo ? au[2] : au[3];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] += dpp_f32<0xB1>(v[k]);   // quad_perm [1,0,3,2]
+    v[k] += dpp_f32<0x4E>(v[k]);   // quad_perm [2,3,0,1]
+    v[k] += dpp_f32<0x141>(v[k]);  // row_half_mirror
+    v[k] += dpp_f32<0x140>(v[k]);  // row_mirror
+  }
+}
+
+// Bytes of one activation term row in LDS (16 bytes of padding shift the
+// terms' rows to distinct banks).
+__host__ __device__ constexpr size_t gm_term_bytes(int hidden) { return 2 * (size_t)hidden + 16; }
+
+constexpr int kGmThreads = 512;
+
+template <typename XT, int NT, int NB, int IT, bool kS4 = false, bool kPos = false>
+__global__ __launch_bounds__(kGmThreads) void k_glu_mfma(const TokenRoute route_arg, const Geo g,
+                                                         const XT* __restrict__ x_arg,
+                                                         float* __restrict__ h_arg, int n_units,
+                                                         int S, int xs_off, const PosStride pos) {
+  // Positions along blockIdx.y as in k_glu_decode (kPos).
+  const TokenRoute& route = route_arg;  // read in place (see k_glu_decode)
+  const int pidx = kPos ? (int)blockIdx.y : 0;
+  const size_t proute = (size_t)pidx * route.n;
+  const float* logits = route.logits ? route.logits + (size_t)pidx * route.n_bank : nullptr;
+  const XT* __restrict__ x = x_arg + pidx * pos.x;
+  float* __restrict__ h = h_arg + pidx * pos.h;
+  extern __shared__ __attribute__((aligned(16))) uint64_t route_scratch[];
+  __shared__ float red[2][8][16];
+  __shared__ int sel[K3_HIP_MAX_TOKEN_EXPERTS];
+  __shared__ float wsel[K3_HIP_MAX_TOKEN_EXPERTS];
+  uint8_t* xs = reinterpret_cast<uint8_t*>(route_scratch) + xs_off;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int groups = kGmThreads / (64 * S);
+  const int grp = wave / S;
+  const int gw = wave - grp * S;
+  const bool pre = logits && route.n_bank <= (int)blockDim.x;
+  float logit = 0.0f;
+  if (pre && (int)threadIdx.x < route.n_bank) logit = logits[threadIdx.x];
+  // The activation, 8 columns per thread and step, requested before the route.
+  const int n8 = g.hidden >> 3;
+  constexpr int kXSteps = 2;  // hidden <= 8192 (host)
+  typedef std::conditional_t<sizeof(XT) == 4, float4, uint4> XV;
+  XV xv[kXSteps][sizeof(XT) == 4 ? 2 : 1];
+#pragma unroll
+  for (int s = 0; s < kXSteps; ++s) {
+    const int k = min((int)threadIdx.x + s * kGmThreads, n8 - 1);
+    const XV* src = reinterpret_cast<const XV*>(x) + k * (sizeof(XT) == 4 ? 2 : 1);
+#pragma unroll
+    for (int q = 0; q < (sizeof(XT) == 4 ? 2 : 1); ++q) xv[s][q] = src[q];
+  }
+  RouteRegs rr;
+  if (logits) {
+    block_topk(logits, route.n_bank, route.n, route_scratch, sel, wsel, logit, pre, false);
+    rr.lo = rr.hi = 0u;
+    rr.w = 0.0f;
+    if (lane < route.n) {
+      const int id = min(max(sel[lane], 0), route.n_bank - 1);
+      const uint64_t p = reinterpret_cast<uint64_t>(route.bank) + (uint64_t)id * route.stride;
+      rr.lo = (uint32_t)p;
+      rr.hi = (uint32_t)(p >> 32);
+    }
+    if (blockIdx.x == 0 && wave == 0) {
+      const int j = lane;
+      float ex = 0.0f;
+      if (j < route.n) {
+        const float top = key_value(route_scratch[sel[0]]);
+        ex = expf(key_value(route_scratch[sel[j]]) - top);
+      }
+      const float sum = wave_sum(ex);
+      if (j < route.n) {
+        const float wj = ex / sum;
+        route.ids_pub[proute + j] = sel[j];
+        route.w_pub[proute + j] = wj;
+        if (route.ids_user) route.ids_user[proute + j] = sel[j];
+        if (route.w_user) route.w_user[proute + j] = wj;
+      }
+    }
+  } else {
+    rr = route_regs(route, lane, proute);
+  }
+  const uint32_t rb4 = kS4 ? route_bases(rr, route.n, lane) : 0u;
+  const int tpe = g.inter >> 3;      // tiles per expert
+  const int Q = gridDim.x * groups;  // IT = ceil(n_units / Q) (host)
+  const int q0 = xcd_block_id((int)blockIdx.x, (int)gridDim.x) * groups + grp;
+  const int kb0 = gw * NB;
+  // Where unit it's loads go: its span and first row; past the end every lane
+  // at unit 0's bases (one line, in bounds), so every load is unconditional.
+  struct UnitAt {
+    const uint8_t* span;
+    size_t r0;
+    uint32_t b4;
+    bool valid;
+  };
+  auto unit_at = [&](int it) {
+    UnitAt n;
+    const int un = q0 + it * Q;
+    n.valid = un < n_units;  // wave-uniform
+    const int u = n.valid ? un : 0;
+    const int e = u / tpe;
+    n.span = span_of(rr, e);
+    n.r0 = (size_t)(8 * (u - e * tpe));
+    n.b4 = kS4 ? (uint32_t)__builtin_amdgcn_readlane(rb4, e) : 0u;
+    return n;
+  };
+  // The scheduling barrier keeps a unit's loads where they are written: sunk
+  // into the next unit's dots, they would wait behind that unit's data.
+  auto load_unit = [&](GmUnit<NB, kS4>& dst, int it) {
+    const UnitAt n = unit_at(it);
+    gm_load<NB, kS4>(dst, n.span, g, n.r0, kb0, lane, n.valid, n.b4);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Two units in flight, in a fully unrolled loop of IT iterations with no
+  // branches around the loads: a loop-carried pair of buffers would become
+  // register copies at the loop head (copying an in-flight register waits for
+  // its load), and a load under a runtime condition makes the wait counts
+  // after it assume the branch that issued fewer loads.
+  GmUnit<NB, kS4> bt[2];
+  load_unit(bt[0], 0);
+  if constexpr (IT > 1) load_unit(bt[1], 1);
+  // Terms into LDS (waits for the activation loads only: they were issued
+  // first), then the zero row.
+  {
+    const size_t tb = gm_term_bytes(g.hidden);
+#pragma unroll
+    for (int s = 0; s < kXSteps; ++s) {
+      const int k = (int)threadIdx.x + s * kGmThreads;
+      if (k >= n8) continue;
+      uint32_t t[NT][4];
+      if constexpr (sizeof(XT) == 4) {
+        const float f[8] = {xv[s][0].x, xv[s][0].y, xv[s][0].z, xv[s][0].w,
+                            xv[s][1].x, xv[s][1].y, xv[s][1].z, xv[s][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          uint32_t b0[2], b1[2], b2[2];
+#pragma unroll
+          for (int o = 0; o < 2; ++o) {
+            const float v = f[e + o];
+            b0[o] = f32_to_bf16_bits(v);
+            const float r1 = v - __uint_as_float(b0[o] << 16);
+            b1[o] = f32_to_bf16_bits(r1);
+            b2[o] = f32_to_bf16_bits(r1 - __uint_as_float(b1[o] << 16));
+          }
+          t[0][e >> 1] = b0[0] | (b0[1] << 16);
+          if constexpr (NT > 1) t[1][e >> 1] = b1[0] | (b1[1] << 16);
+          if constexpr (NT > 2) t[2][e >> 1] = b2[0] | (b2[1] << 16);
+        }
+      } else {
+        t[0][0] = xv[s][0].x;
+        t[0][1] = xv[s][0].y;
+        t[0][2] = xv[s][0].z;
+        t[0][3] = xv[s][0].w;
+      }
+#pragma unroll
+      for (int q = 0; q < NT; ++q)
+        *reinterpret_cast<uint4*>(xs + q * tb + 16 * (size_t)k) =
+            make_uint4(t[q][0], t[q][1], t[q][2], t[q][3]);
+      *reinterpret_cast<uint4*>(xs + NT * tb + 16 * (size_t)k) = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  lds_barrier();
+  // This lane's B row: term n % 8 (the zero row past NT) at parity n / 8.
+  const int n = lane & 15;
+  const uint8_t* xb = xs + min(n & 7, NT) * gm_term_bytes(g.hidden) +
+                      2 * (256 * kb0 + 64 * (lane >> 4) + 32 * (n >> 3));
+  // Unit it's dots (refilling bt with unit it + 2 when kRefill), then its
+  // partials through LDS and the activation.
+  auto finish = [&](GmUnit<NB, kS4>& bt, int it, auto refill) {
+    constexpr bool kRefill = decltype(refill)::value;
+    const int u = q0 + it * Q;
+    const int parity = it & 1;
+    float v[4];
+    const UnitAt nx = unit_at(it + 2);
+    gm_dots<NB, kS4, kRefill>(bt, xb, lane, v, nx.span, g, nx.r0, kb0, nx.valid, nx.b4);
+    if ((lane & 15) == 0) {
+      const int gi = lane >> 4;
+      red[parity][wave][2 * gi] = v[0];
+      red[parity][wave][2 * gi + 1] = v[1];
+      red[parity][wave][8 + 2 * gi] = v[2];
+      red[parity][wave][8 + 2 * gi + 1] = v[3];
+    }
+    lds_barrier();
+    if (u < n_units && gw == 0 && lane < 8) {
+      const int w0 = grp * S;
+      float gv = red[parity][w0][lane], uv = red[parity][w0][8 + lane];
+      for (int w = 1; w < S; ++w) {
+        gv += red[parity][w0 + w][lane];
+        uv += red[parity][w0 + w][8 + lane];
+      }
+      h[(size_t)u * 8 + lane] = activate(g.act, gv, uv);
+    }
+  };
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    if (it + 2 < IT)
+      finish(bt[it & 1], it, std::true_type{});
+    else
+      finish(bt[it & 1], it, std::false_type{});
   }
 }
 
@@ -2117,9 +2646,91 @@ void glu_go(TimedLaunch& tl, int grid, int threads, size_t lds, hipStream_t st,
                  st, route, g, x, h, n_units, S, pl.s);
 }
 
+// Matrix-core gate/up (k_glu_mfma; k3_hip_set_decode_mfma): 0 never, 1 for
+// fp32 activations (the default), 2 for fp32 and bf16 activations.
+#ifndef K3_GLU_MFMA
+#define K3_GLU_MFMA 1
+#endif
+std::atomic<int> g_glu_mfma{K3_GLU_MFMA};
+
+// k_glu_mfma when the shape allows it: raw-v1 or scale4-v2 spans, hidden a
+// multiple of 256 (at most 8192) split into S waves of 7 or 8 K blocks,
+// intermediate a multiple of 8, a 16-byte aligned activation (and position
+// stride) and 4, 6 or 8 units per pipeline (the instantiated unrolled loops).
+// One position or a position batch (blockIdx.y).  *done says whether it
+// launched.
+template <typename XT, bool kS4, bool kPos>
+void glu_mfma_go(TimedLaunch& tl, int NB, int iters, int grid, size_t lds, hipStream_t st,
+                 const TokenRoute& route, const Geo& g, const XT* x, float* h, int n_units, int S,
+                 int xo, const PosLaunch& pl) {
+  constexpr int NT = sizeof(XT) == 4 ? 3 : 1;
+  const dim3 gd(grid, kPos ? pl.n : 1);
+#define K3_GM_GO(nb, it)                                                                      \
+  if (NB == nb && iters == it)                                                                \
+    launch_timed(tl, (k_glu_mfma<XT, NT, nb, it, kS4, kPos>), gd, dim3(kGmThreads),           \
+                 (unsigned)lds, st, route, g, x, h, n_units, S, xo, pl.s);
+  K3_GM_GO(7, 4) K3_GM_GO(7, 6) K3_GM_GO(7, 8) K3_GM_GO(8, 4) K3_GM_GO(8, 6) K3_GM_GO(8, 8)
+#undef K3_GM_GO
+}
+
+template <typename XT>
+int glu_mfma_try(const Geo& g, const TokenRoute& route, const XT* x, float* h, hipStream_t st,
+                 const PosLaunch& pl, bool* done) {
+  *done = false;
+  constexpr bool f32 = sizeof(XT) == 4;
+  constexpr int NT = f32 ? 3 : 1;
+  const int mode = g_glu_mfma.load(std::memory_order_relaxed);
+  if (mode == 0 || (!f32 && mode < 2)) return K3_HIP_OK;
+  const bool s4 = g.layout == K3_LAYOUT_SCALE4_V2;
+  if ((g.layout != K3_LAYOUT_RAW_V1 && !s4) || g.hidden % 256 != 0 || g.hidden > 8192 ||
+      g.inter % 8 != 0)
+    return K3_HIP_OK;
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || (pl.s.x * (int64_t)sizeof(XT)) % 16 != 0)
+    return K3_HIP_OK;
+  const int KB = g.hidden / 256;
+  int S = 0;
+  for (int s = 1; s <= 8; s *= 2)
+    if (KB % s == 0 && KB / s >= 7 && KB / s <= 8) {
+      S = s;
+      break;
+    }
+  if (S == 0) return K3_HIP_OK;
+  const int NB = KB / S;
+  const int groups = kGmThreads / (64 * S);
+  const int cus = std::max(1, device_cu_count());
+  const int n_units = route.n * (g.inter / 8);
+  const int iters = (n_units + cus * groups - 1) / (cus * groups);
+  if (iters != 4 && iters != 6 && iters != 8) return K3_HIP_OK;
+  const size_t xs_off = route.logits ? (route_scratch_bytes(route.n_bank, route.n) + 15) & ~(size_t)15
+                                     : 0;
+  const size_t lds = xs_off + (NT + 1) * gm_term_bytes(g.hidden);
+  if (lds > 64 * 1024) return K3_HIP_OK;
+  TimedLaunch tl(KC_GLU_DECODE, st);
+  const int xo = (int)xs_off;
+  if (s4) {
+    if (pl.n > 1)
+      glu_mfma_go<XT, true, true>(tl, NB, iters, cus, lds, st, route, g, x, h, n_units, S, xo, pl);
+    else
+      glu_mfma_go<XT, true, false>(tl, NB, iters, cus, lds, st, route, g, x, h, n_units, S, xo, pl);
+  } else {
+    if (pl.n > 1)
+      glu_mfma_go<XT, false, true>(tl, NB, iters, cus, lds, st, route, g, x, h, n_units, S, xo, pl);
+    else
+      glu_mfma_go<XT, false, false>(tl, NB, iters, cus, lds, st, route, g, x, h, n_units, S, xo,
+                                    pl);
+  }
+  *done = true;
+  return launched(tl, "decode gate/up launch");
+}
+
 template <typename XT>
 int glu_decode_dispatch(const Geo& g, const TokenRoute& route, const XT* x, float* h,
                         hipStream_t st, const PosLaunch& pl = PosLaunch{}) {
+  {
+    bool done = false;
+    const int rc = glu_mfma_try(g, route, x, h, st, pl, &done);
+    if (done) return rc;
+  }
   const int G = g.hidden / 32;
   const int S = (G + 63) / 64;
   if (S > 4) return fail(K3_HIP_E_INVALID, "decode layer: hidden %d exceeds 8192", g.hidden);
@@ -2391,6 +3002,11 @@ int fused_decode(const Geo& g, const TokenRoute& route, const uint16_t* x, OT* o
 
 int set_fused_decode(int enabled) {
   return g_fused_enabled.exchange(enabled ? 1 : 0);
+}
+
+int set_decode_mfma(int mode) {
+  if (mode < 0 || mode > 2) return fail(K3_HIP_E_INVALID, "decode dot mode %d unknown", mode);
+  return g_glu_mfma.exchange(mode);
 }
 
 size_t route_scratch_bytes(int n_bank, int top_k) {

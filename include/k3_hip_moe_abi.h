@@ -456,6 +456,21 @@ int k3_hip_timing_end(K3HipKernelTimingV1* out, int capacity, int* n_out,
  * slower on MI355X.  Returns the previous setting. */
 int k3_hip_set_fused_decode(int enabled);
 
+/* No reference counterpart.  Where the single-token gate/up dots of the layer
+ * calls above run: K3_DECODE_DOTS_VALU (0) on the vector ALUs for every
+ * activation type; K3_DECODE_DOTS_MFMA_F32 (1, the default) on the bf16
+ * matrix cores for fp32 activations (x split into three bf16 terms that sum
+ * to it exactly, so only the summation order differs) and on the vector ALUs
+ * for bf16 ones; K3_DECODE_DOTS_MFMA_ALL (2) on the matrix cores for both.
+ * The matrix-core kernel takes raw-v1 spans with hidden a multiple of 256 and
+ * 4, 6 or 8 gate/up units of 8 rows per unit pipeline; other shapes keep the
+ * vector kernel.  Process-wide; returns the previous setting, or
+ * K3_HIP_E_INVALID for another value. */
+#define K3_DECODE_DOTS_VALU 0
+#define K3_DECODE_DOTS_MFMA_F32 1
+#define K3_DECODE_DOTS_MFMA_ALL 2
+int k3_hip_set_decode_mfma(int mode);
+
 /* ============================== verify path selection */
 /* No reference counterpart.  How the two verify calls above run:
  *   K3_VERIFY_AUTO (default): batches of two or more positions whose unique

@@ -2,7 +2,12 @@
 of a verify call, position on the grid's y axis) against one routed decode
 layer per position: identical routes and outputs bit for bit, on both down
 kernels (intermediate 2048: k_down_g64; intermediate 3072: k_down_g96), with
-fp32 and bf16 outputs, and the first position against the oracle."""
+fp32 and bf16 outputs, and the first position against the oracle.
+
+Every case runs under both gate/up dot settings (k3_hip_set_decode_mfma):
+vector ALUs for every activation, and the default, where fp32 activations
+take the matrix-core gate/up in the batched and the one-position launches
+alike."""
 import numpy as np
 import pytest
 
@@ -23,11 +28,14 @@ def _t(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-@pytest.fixture
-def positions_mode(gpu):
+@pytest.fixture(params=["valu_dots", "mfma_f32_dots"])
+def positions_mode(gpu, request):
     from deltafin_amd import _lib
     prev = _lib.set_verify_mode(_lib.VERIFY_POSITIONS)
+    prev_dots = _lib.set_decode_mfma(_lib.DECODE_DOTS_VALU if request.param == "valu_dots"
+                                     else _lib.DECODE_DOTS_MFMA_F32)
     yield
+    _lib.set_decode_mfma(prev_dots)
     _lib.set_verify_mode(prev)
 
 
