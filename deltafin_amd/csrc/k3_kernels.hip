@@ -1494,6 +1494,78 @@ __global__ __launch_bounds__(down_max_threads<CPLB>()) void k_down_blocks(
   }
 }
 
+// Down + ordered combine for a few routed experts at intermediate 2048
+// (k_down_g64's row batches: 4 rows, one 16-byte chunk per lane, gathered
+// scales).  k_down_g64 gives each expert a wave that reloads that expert's
+// whole h (8 KB) from L2 for its own batches, which at one expert means 1,792
+// one-wave workgroups moving 14.7 MB of h for 7.3 MB of weights.  Here a
+// workgroup of kFewWaves waves stages the NE experts' h in LDS once (NE x 8 KB,
+// k_down_g64's padded layout) and each wave takes one row batch for every
+// expert: it requests the batch's rows of all NE experts up front, then sums
+// w_e * y_e over the experts in route order, the order k_down_g64's combine
+// uses, with the same per-row dot.
+constexpr int kFewWaves = 4;
+#ifndef K3_DOWN_FEW_MAX
+#define K3_DOWN_FEW_MAX 4  // routed experts up to which k_down_few replaces k_down_g64
+#endif
+
+template <typename OT, int NE>
+__global__ __launch_bounds__(64 * kFewWaves) void k_down_few(const TokenRoute route_arg,
+                                                             const Geo g,
+                                                             const float* __restrict__ h,
+                                                             OT* __restrict__ out) {
+  const TokenRoute& route = route_arg;  // read in place (see k_glu_decode)
+  constexpr int kB = 4;
+  extern __shared__ float4 hbuf[];  // NE x kHSliceF4
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nbt = (g.hidden + kB - 1) / kB;
+  const int batch = (int)blockIdx.x * kFewWaves + wave;
+  const int r0 = min(batch, nbt - 1) * kB;  // a batch past the end re-reads the last one
+  const int rows = min(kB, g.hidden - r0);
+  // h first (its waits never wait for the weights): 8 floats per thread and
+  // expert, float4 f = q 256 + t of expert e
+  const float4* h4 = reinterpret_cast<const float4*>(h);
+  float4 ht[NE][2];
+#pragma unroll
+  for (int e = 0; e < NE; ++e)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) ht[e][q] = h4[(size_t)e * (g.inter >> 2) + q * 256 + threadIdx.x];
+  __builtin_amdgcn_sched_barrier(0);
+  const RouteRegs rreg = route_regs(route, lane);
+  const int cc[1] = {lane};
+  DownBatch<1, kB, true> bt[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) down_load(bt[e], span_of(rreg, e), g, cc, r0, rows);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int e = 0; e < NE; ++e)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int f = q * 256 + (int)threadIdx.x;
+      hbuf[e * kHSliceF4 + 9 * (f >> 3) + (f & 7)] = ht[e][q];
+    }
+  lds_barrier();
+  float acc = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    XChunk<float> hs;
+    const float4* mine = hbuf + e * kHSliceF4 + 9 * lane;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float4 v = mine[q];
+      hs.v[4 * q + 0] = v.x;
+      hs.v[4 * q + 1] = v.y;
+      hs.v[4 * q + 2] = v.z;
+      hs.v[4 * q + 3] = v.w;
+    }
+    const float v = down_dots(bt[e], &hs, lane);
+    acc += weight_of(rreg, e) * v;
+  }
+  const int idx = lane >> 4;
+  if ((lane & 15) == 0 && batch < nbt && idx < rows) store_out(out + r0 + idx, acc);
+}
+
 // k_down_g64: the same split for intermediate 2048 (64 scale groups per row:
 // one chunk per lane, batches of 4 rows with gathered scales, h_e's slice
 // transposed through LDS).  Every workgroup runs exactly NB batch slots (a
@@ -2810,6 +2882,19 @@ template <typename OT>
 int down_g64_dispatch(const Geo& g, const TokenRoute& route, const float* h, OT* out,
                       hipStream_t st, const PosLaunch& pl) {
   const int nbt = (g.hidden + 3) / 4;
+  if (pl.n == 1 && route.n <= K3_DOWN_FEW_MAX && g.layout == K3_LAYOUT_RAW_V1) {
+    // A few experts: h shared per workgroup (k_down_few).
+    const unsigned lds = (unsigned)(route.n * kHSliceF4 * sizeof(float4));
+    const dim3 grid((nbt + kFewWaves - 1) / kFewWaves), block(64 * kFewWaves);
+    TimedLaunch tl(KC_DOWN_DECODE, st);
+    switch (route.n) {
+      case 1: launch_timed(tl, (k_down_few<OT, 1>), grid, block, lds, st, route, g, h, out); break;
+      case 2: launch_timed(tl, (k_down_few<OT, 2>), grid, block, lds, st, route, g, h, out); break;
+      case 3: launch_timed(tl, (k_down_few<OT, 3>), grid, block, lds, st, route, g, h, out); break;
+      default: launch_timed(tl, (k_down_few<OT, 4>), grid, block, lds, st, route, g, h, out); break;
+    }
+    return launched(tl, "decode down/combine launch");
+  }
   const int blocks = down_g64_blocks(g, route.n);
   const int nb = (nbt + blocks - 1) / blocks;
   switch (nb) {
