@@ -870,7 +870,10 @@ def _single_configs(moe, _lib, oracle, g, bank, stride, cpu_seconds: float, no_c
         torch.cuda.synchronize()
         kern, _ = _lib.timing_end()
         dev = sum(kern[k]["total_ms"] for k in cls if k in kern) / 1e3 / launches
+        seen[fn.__name__] = sorted(k for k in cls if k in kern)
         return wall, dev
+
+    seen: dict[str, list[str]] = {}
 
     wall0, dev0 = timed_calls(gemv, ["gemv"])
     gemv(0)
@@ -912,7 +915,7 @@ def _single_configs(moe, _lib, oracle, g, bank, stride, cpu_seconds: float, no_c
         if rc != 0:
             raise _lib.K3HipError(rc, "k3_hip_moe_layer_device")
 
-    wall1, dev1 = timed_calls(expert, ["glu_decode", "down_decode", "decode_fused"])
+    wall1, dev1 = timed_calls(expert, ["glu_decode", "down_decode", "decode_fused", "decode_chain"])
     expert(0)
     torch.cuda.synchronize()
     span0 = bank[:SPAN].cpu().numpy()
@@ -925,6 +928,7 @@ def _single_configs(moe, _lib, oracle, g, bank, stride, cpu_seconds: float, no_c
                      f"round-robin over {n_rot} distinct experts ({n_rot * SPAN / 1e9:.2f} GB)"),
         "algorithmic_bytes": CFG1_BYTES,
         "launches": launches,
+        "kernels": seen.get("expert", []),
         "us_per_call_wall": round(wall1 * 1e6, 3),
         "us_per_call_device": round(dev1 * 1e6, 3),
         "experts_per_s": round(1 / wall1, 1),

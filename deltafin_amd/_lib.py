@@ -192,6 +192,7 @@ SIGNATURES = {
     "k3_hip_timing_end": (_i32, [C.POINTER(K3HipKernelTimingV1), _i32, C.POINTER(_i32),
                                  C.POINTER(C.c_longlong)]),
     "k3_hip_set_fused_decode": (_i32, [_i32]),
+    "k3_hip_set_decode_chain": (_i32, [_i32]),
     "k3_hip_set_decode_mfma": (_i32, [_i32]),
     "k3_hip_set_verify_mode": (_i32, [_i32]),
     "k3_hip_scale4_check_header": (_i32, [_vp, _u64]),
@@ -314,6 +315,19 @@ def set_fused_decode(enabled: bool) -> bool:
     return bool(load().k3_hip_set_fused_decode(1 if enabled else 0))
 
 
+DECODE_CHAIN_OFF, DECODE_CHAIN_ON, DECODE_CHAIN_FALLBACK = 0, 1, 2
+
+
+def set_decode_chain(mode: int) -> int:
+    """Run one-expert layer calls as one launch (DECODE_CHAIN_ON, the
+    default), as the two launches (DECODE_CHAIN_OFF), or as one launch whose
+    workgroups compute missing gate/up shares at once (DECODE_CHAIN_FALLBACK);
+    returns the previous mode."""
+    prev = load().k3_hip_set_decode_chain(int(mode))
+    check(min(prev, 0), "k3_hip_set_decode_chain")
+    return prev
+
+
 DECODE_DOTS_VALU, DECODE_DOTS_MFMA_F32, DECODE_DOTS_MFMA_ALL = 0, 1, 2
 
 
@@ -343,10 +357,10 @@ def timing_begin(max_launches: int) -> None:
 
 def timing_end() -> tuple[dict[str, dict[str, float]], int]:
     """Close the window; returns ({kernel: {launches, total_ms, min_ms, max_ms, avg_ms}}, dropped)."""
-    rows = (K3HipKernelTimingV1 * 16)()
+    rows = (K3HipKernelTimingV1 * 32)()
     n = C.c_int()
     dropped = C.c_longlong()
-    check(load().k3_hip_timing_end(rows, 16, C.byref(n), C.byref(dropped)), "k3_hip_timing_end")
+    check(load().k3_hip_timing_end(rows, 32, C.byref(n), C.byref(dropped)), "k3_hip_timing_end")
     out = {}
     for r in rows[: n.value]:
         out[r.kernel.decode()] = {

@@ -1646,6 +1646,7 @@ int k3_hip_moe_verify_device(const K3HipGeometryV1* gd, const uint8_t* const* ed
 }
 
 int k3_hip_set_fused_decode(int enabled) { return set_fused_decode(enabled); }
+int k3_hip_set_decode_chain(int mode) { return set_decode_chain(mode); }
 
 int k3_hip_set_decode_mfma(int mode) { return set_decode_mfma(mode); }
 

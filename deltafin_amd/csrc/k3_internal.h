@@ -141,6 +141,10 @@ int launch_decode_positions(const Geo& g, const TokenRoute& route, int n_positio
 // Process-wide decode path switch (k3_hip_set_fused_decode); returns the
 // previous setting.
 int set_fused_decode(int enabled);
+// One-launch path for one-expert layers (k3_hip_set_decode_chain: 0 off, 1
+// on, 2 on with its missing-share fallback taken at once); returns the
+// previous setting, or K3_HIP_E_INVALID for another value.
+int set_decode_chain(int mode);
 // Process-wide choice of the single-token gate/up dots (k3_hip_set_decode_mfma:
 // 0 VALU, 1 matrix cores for fp32 activations, 2 also for bf16); returns the
 // previous setting, or K3_HIP_E_INVALID for another value.
@@ -204,6 +208,7 @@ enum KernelClass : int {
   KC_SPINE,
   KC_RMS_NORM,
   KC_SPINE_MFMA,
+  KC_DECODE_CHAIN,
   KC_COUNT
 };
 

@@ -491,13 +491,17 @@ __device__ __forceinline__ int glu_pair0(int q0, int Q, int n_units, int kR, int
 // nothing, so every wave of the workgroup reaches the same iters barriers.
 // The S wave partials of a unit meet in red (two slots by unit parity, one
 // barrier per unit); kR lanes of the pipeline's wave 0 sum them in wave
-// order, apply the activation and store h.
-template <typename XT, int kR, bool kG, bool kDeviceStore = false>
+// order, apply the activation and store h.  kIters > 0: iters is kIters (the
+// loop resolves at compile time, so no wait merges the paths of other counts).
+// kTagged (with kDeviceStore): h holds 64-bit entries {value bits, tag}, each
+// stored at once, and both units' loads are issued before anything waits.
+template <typename XT, int kR, bool kG, bool kDeviceStore = false, int kIters = 0,
+          bool kTagged = false>
 __device__ __forceinline__ void glu_sweep(const RouteRegs& rr, const Geo& g, const XChunk<XT>& xc,
                                           const ColSplit& cs, const GluGather& gg, int row_step,
                                           int S, int grp, int gw, int wave, int lane, int q0,
                                           int Q, int iters, int n_units, float* __restrict__ h,
-                                          float (*red)[16][2 * kR]) {
+                                          float (*red)[16][2 * kR], uint32_t tag = 0u) {
   constexpr int N = 2 * kR;
   constexpr int L = log2c<N>();
   auto unit_pair0 = [&](int it) { return glu_pair0(q0, Q, n_units, kR, it); };
@@ -527,25 +531,32 @@ __device__ __forceinline__ void glu_sweep(const RouteRegs& rr, const Geo& g, con
         uv += red[parity][w0 + w][kR + lane];
       }
       const float hv = activate(g.act, gv, uv);
-      if constexpr (kDeviceStore)  // written through to the device-coherent level
+      if constexpr (kTagged)
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(h) + (size_t)u * kR + lane,
+                           ((uint64_t)tag << 32) | __float_as_uint(hv), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      else if constexpr (kDeviceStore)  // written through to the device-coherent level
         __hip_atomic_store(h + (size_t)u * kR + lane, hv, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       else
         h[(size_t)u * kR + lane] = hv;
     }
   };
+  const int n_it = kIters > 0 ? kIters : iters;
   GluBatch<XT, kR, kG> A, B;
   glu_load(A, rr, g, unit_pair0(0), cs, gg);
-  glu_load(B, rr, g, unit_pair0(min(1, iters - 1)), cs, gg);
+  glu_load(B, rr, g, unit_pair0(min(1, n_it - 1)), cs, gg);
+  // kTagged: both units' loads are issued before anything waits for the first
+  if constexpr (kTagged) __builtin_amdgcn_sched_barrier(0);
   for (int it = 0;; it += 2) {
     finish(A, it);
-    if (it + 2 >= iters) {
-      if (it + 1 < iters) finish(B, it + 1);
+    if (it + 2 >= n_it) {
+      if (it + 1 < n_it) finish(B, it + 1);
       break;
     }
     glu_load(A, rr, g, unit_pair0(it + 2), cs, gg);
     finish(B, it + 1);
-    if (it + 3 >= iters) {
+    if (it + 3 >= n_it) {
       finish(A, it + 2);
       break;
     }
@@ -2037,6 +2048,234 @@ __global__ __launch_bounds__(1024) void k_decode_fused(const TokenRoute route, c
 }
 
 // ======================================================================
+// one launch for a one-expert layer: k_expert_chain
+// ======================================================================
+// A layer with one routed expert (one token, caller route, intermediate 2048)
+// is a 23 MB stream that two launches spend mostly on fixed costs: the
+// gate/up kernel ends ~5 us after its start, the down kernel starts ~1.1 us
+// later and its first row batch arrives ~2.5 us after that (h and weights
+// from a cold launch), ~10.8 us per expert on MI355X.  Here one launch of one
+// workgroup per CU runs the gate/up sweep of k_glu_decode's few-expert form
+// (units of 2 rows, the same per-row arithmetic; the expert's span pointer
+// read from the kernel argument at a uniform index, so no load precedes the
+// first unit's), then each wave requests its down row batch (k_down_few's
+// 4-row batch, one per wave: batch = workgroup + wave x grid; a batch past
+// the end re-reads the last one and stores nothing), the workgroup gathers
+// the expert's whole h into LDS (k_down_g64's padded layout) as soon as it is
+// stored, and each wave forms its rows as k_down_few does.  The outputs are
+// the two launches' bit for bit; ~9.3 us per expert.
+//
+// No counter: h goes through device memory as 64-bit entries {value, tag},
+// each a single store written through to the device-coherent level, and a
+// reader takes a pair of rows once both entries carry this call's tag (the
+// first read through the XCD's L2, re-reads at device scope).  The tag comes
+// from a per-workgroup call count (g_chain_calls, one word per workgroup and
+// workspace slot, read at the start and advanced at the end): every launch on
+// a slot runs one workgroup per CU, so all counts of a slot agree when a
+// launch starts, and the tag (a signalling-NaN pattern, which no arithmetic
+// result and so no earlier h value carries) differs from the previous
+// launch's.  The state stays on the device, so a captured graph replays
+// correctly.  (Counters measured slower: 256 increments of one word
+// serialize over ~5 us.)
+//
+// The reads need every gate/up share done, which a workgroup that is not
+// resident cannot do; with other work on the GPU (another stream's launch of
+// this kernel, say) not every workgroup may be resident.  So after
+// poll_limit rounds a waiting workgroup computes the missing shares itself
+// (the owner's sweep: bit-identical values and tag, a share done twice is
+// harmless), scanning from its own index and re-reading after each.  Every
+// loop is bounded; rows still missing after 2 x grid shares become NaN.
+struct ChainPlan {
+  int S;           // column-split waves per gate/up pipeline
+  int groups;      // gate/up pipelines per workgroup
+  int n_units;     // 2-row gate/up units (route.n * inter / 2)
+  int slot;        // workspace slot (g_chain_calls row)
+  int poll_limit;  // read rounds before a workgroup computes missing shares
+  int zero;        // 0 (a per-lane offset the compiler cannot fold)
+};
+#ifndef K3_EXPERT_CHAIN
+#define K3_EXPERT_CHAIN 1
+#endif
+constexpr int kChainMaxGrid = 1024;
+constexpr int kChainPollLimit = 256;
+constexpr int kChainSlots = 64;
+static __device__ __align__(256) unsigned g_chain_calls[kChainSlots][kChainMaxGrid] = {};
+
+// Tag of the call whose count is c: a signalling NaN (exponent all ones,
+// quiet bit clear, payload 1 .. 2^22 - 1).
+__device__ __forceinline__ uint32_t chain_tag(unsigned c) {
+  return 0x7F800000u | (1u + c % 0x3FFFFFu);
+}
+
+template <typename XT, typename OT, int NE, int kIters>
+__global__ __launch_bounds__(kGluMaxThreads) __attribute__((amdgpu_waves_per_eu(1, kGluMaxThreads / 256)))
+void k_expert_chain(const TokenRoute route_arg, const Geo g, const XT* __restrict__ x,
+                    uint64_t* ht, OT* __restrict__ out, const ChainPlan cp) {
+  const TokenRoute& route = route_arg;  // read in place (see k_glu_decode)
+  constexpr int kR = 2;
+  constexpr int kB = 4;
+  constexpr int kMaxPairs = NE * 1024;  // intermediate 2048
+  extern __shared__ __attribute__((aligned(16))) float4 hbuf[];  // NE x kHSliceF4
+  __shared__ float red[2][16][2 * kR];
+  __shared__ uint8_t s_have[kMaxPairs];
+  __shared__ int s_miss[2];
+  const int lane = threadIdx.x & 63;
+  // The call count: loaded per lane (the offset is zero) so that it stays a
+  // vector value, waited for only where the first h store needs the tag.
+  unsigned* calls = &g_chain_calls[cp.slot][blockIdx.x];
+  const unsigned count =
+      __hip_atomic_load(calls + lane * cp.zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int S = cp.S;
+  const int G = g.hidden >> 5;
+  const int grp = wave / S;
+  const int gw = wave - grp * S;
+  const ColSplit cs = col_split(G, S, gw, lane);
+  XChunk<XT> xc;
+  load_x_chunk<XT>(xc, x, cs);
+  // The caller's span pointers and weights, read at uniform indices (scalar
+  // loads of the kernel argument), in a wave's route registers.
+  RouteRegs rr;
+  rr.lo = rr.hi = 0u;
+  rr.w = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const uint64_t sp = reinterpret_cast<uint64_t>(route.ptr[e]);
+    if (lane == e) {
+      rr.lo = (uint32_t)sp;
+      rr.hi = (uint32_t)(sp >> 32);
+      rr.w = route.w[e];
+    }
+  }
+  const uint32_t tag = chain_tag(count);
+  const int Q = (int)gridDim.x * cp.groups;
+  const int row_step = (G + S - 1) / S;
+  auto sweep_as = [&](int b) {  // gate/up share of workgroup b
+    const int q0 = xcd_block_id(b, (int)gridDim.x) * cp.groups + grp;
+    glu_sweep<XT, kR, false, true, kIters, true>(rr, g, xc, cs, GluGather{0, 0}, row_step, S,
+                                                 grp, gw, wave, lane, q0, Q, kIters, cp.n_units,
+                                                 reinterpret_cast<float*>(ht), red, tag);
+  };
+  sweep_as((int)blockIdx.x);
+  // down: this wave's row batch of every expert, requested behind the h
+  // stores (issued with the gate/up units, the down bytes measured 0.2 us
+  // slower per call: they delay the last gate/up units, which everyone waits
+  // for)
+  const int nbt = (g.hidden + kB - 1) / kB;
+  const int batch = (int)blockIdx.x + wave * (int)gridDim.x;
+  const int r0 = min(batch, nbt - 1) * kB;
+  const int rows = min(kB, g.hidden - r0);
+  const int cc[1] = {lane};
+  DownBatch<1, kB, true> bt[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) down_load(bt[e], span_of(rr, e), g, cc, r0, rows);
+  __builtin_amdgcn_sched_barrier(0);
+  // the tagged h of all NE experts as one buffer; pairs per thread (the host
+  // launches at least 384 threads)
+  const Rsrc hr = make_rsrc(reinterpret_cast<const uint8_t*>(ht), (uint32_t)(NE * g.inter) * 8u);
+  constexpr int kPer = (kMaxPairs + 383) / 384;
+  // h into LDS (k_down_g64's padded layout) pair by pair (pair p = rows 2p,
+  // 2p + 1 = gate/up unit p, one 16-byte load), once both entries carry the
+  // tag: the first round through the L2 (one fetch per XCD), re-reads of the
+  // pairs still missing at device scope.  After poll_limit rounds with a pair
+  // missing (not every workgroup resident), the workgroup computes the shares
+  // it finds missing, scanning from its own index, re-reading after each.
+  const int np = NE * (g.inter >> 1);
+  const int T = (int)blockDim.x;
+  for (int p = threadIdx.x; p < np; p += T) s_have[p] = 0;
+  if (threadIdx.x == 0) s_miss[0] = s_miss[1] = 0;
+  lds_barrier();
+  bool ok = true;
+  int polls = 0, shares = 0, next = (int)blockIdx.x + 1;
+  for (int round = 0;; ++round) {
+    u32x4 v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const uint32_t off = (uint32_t)min((int)threadIdx.x + k * T, np - 1) * 16u;
+      v[k] = polls == 0 && shares == 0 ? __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0u, 0)
+                                       : __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0u, 16);
+    }
+    int miss = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int p = (int)threadIdx.x + k * T;
+      if (p >= np || s_have[p]) continue;
+      if (v[k][1] == tag && v[k][3] == tag) {
+        const int e = p / (g.inter >> 1), j = 2 * (p - e * (g.inter >> 1));  // row of expert e
+        const int f = j >> 2;
+        float* dst =
+            reinterpret_cast<float*>(hbuf + e * kHSliceF4 + 9 * (f >> 3) + (f & 7)) + (j & 3);
+        dst[0] = __uint_as_float(v[k][0]);
+        dst[1] = __uint_as_float(v[k][2]);
+        s_have[p] = 1;
+      } else {
+        miss = 1;
+      }
+    }
+    // any pair missing in the workgroup? (slot round % 2; the other slot,
+    // read by every thread last round, is cleared for the next)
+    if (miss) s_miss[round & 1] = 1;
+    lds_barrier();
+    const bool any_miss = s_miss[round & 1] != 0;
+    if (threadIdx.x == 0) s_miss[(round & 1) ^ 1] = 0;
+    if (!any_miss) break;
+    if (polls < cp.poll_limit) {
+      ++polls;
+      __builtin_amdgcn_s_sleep(2);
+      continue;
+    }
+    if (shares >= 2 * (int)gridDim.x) {  // rows still missing become NaN
+      ok = false;
+      break;
+    }
+    // the next share (from this workgroup's own index on) with a missing unit
+    int found = -1;
+    for (int k = 0; k < (int)gridDim.x && found < 0; ++k) {
+      const int b2 = (next + k) % (int)gridDim.x;
+      const int qb = xcd_block_id(b2, (int)gridDim.x) * cp.groups;
+      for (int gq = 0; gq < cp.groups; ++gq)
+        for (int it = 0; it < kIters; ++it) {
+          const int u = qb + gq + it * Q;
+          if (u < cp.n_units && !s_have[u]) found = b2;
+        }
+    }
+    if (found < 0) {
+      ok = false;
+      break;
+    }
+    next = found + 1;
+    ++shares;
+    sweep_as(found);
+    wait_vm_complete();  // this wave's h stores are done before the re-read
+    __syncthreads();
+  }
+  XChunk<float> hs[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const float4* mine = hbuf + e * kHSliceF4 + 9 * lane;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float4 t = mine[q];
+      hs[e].v[4 * q + 0] = t.x;
+      hs[e].v[4 * q + 1] = t.y;
+      hs[e].v[4 * q + 2] = t.z;
+      hs[e].v[4 * q + 3] = t.w;
+    }
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const float v = down_dots(bt[e], &hs[e], lane);
+    acc += weight_of(rr, e) * v;
+  }
+  const int idx = lane >> 4;
+  if ((lane & 15) == 0 && batch < nbt && idx < rows)
+    store_out(out + r0 + idx, ok ? acc : __builtin_nanf(""));
+  if (threadIdx.x == 0)
+    __hip_atomic_store(calls, count + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ======================================================================
 // elementwise activation (per-expert launch path)
 // ======================================================================
 __global__ void k_activate(const float* __restrict__ gate, const float* __restrict__ up,
@@ -3083,10 +3322,85 @@ int fused_decode(const Geo& g, const TokenRoute& route, const uint16_t* x, OT* o
   }
 }
 
+// One launch for a one-expert layer (k_expert_chain) where the two-launch
+// path would run k_glu_decode's 2-row units and k_down_few<OT, 1>: one
+// token, caller span pointers, bf16 activations (fp32 ones may take the
+// matrix-core gate/up, whose sums are ordered differently), raw-v1,
+// intermediate 2048, one workgroup per CU whose waves cover the down row
+// batches, and the workspace's h and y areas (the decode layer does not use
+// y) holding the tagged h.  g_chain_mode: 0 off, 1 on, 2 on with the
+// missing-share fallback taken at once (a test of that path).  *ran tells the
+// caller whether it launched.
+std::atomic<int> g_chain_mode{K3_EXPERT_CHAIN};
+
+template <typename OT>
+int chain_decode(const Geo& g, const TokenRoute& route, const float* x, OT* out,
+                 const Workspace& ws, hipStream_t st, bool* ran) {
+  *ran = false;
+  return K3_HIP_OK;
+}
+
+template <typename OT>
+int chain_decode(const Geo& g, const TokenRoute& route, const uint16_t* x, OT* out,
+                 const Workspace& ws, hipStream_t st, bool* ran) {
+  *ran = false;
+  const int mode = g_chain_mode.load(std::memory_order_relaxed);
+  if (mode == 0) return K3_HIP_OK;
+  if (route.logits || route.bank || route.pdev || route.n != 1 ||
+      g.layout != K3_LAYOUT_RAW_V1 || g.inter != 2048 || g.hidden % 32 != 0)
+    return K3_HIP_OK;
+  constexpr int NE = 1;
+  if (reinterpret_cast<const uint8_t*>(ws.ids) - reinterpret_cast<const uint8_t*>(ws.h) <
+      (ptrdiff_t)NE * g.inter * 8)
+    return K3_HIP_OK;
+  const int G = g.hidden / 32;
+  const int S = (G + 63) / 64;
+  if (S > 4) return K3_HIP_OK;
+  // glu_decode_dispatch's few-expert condition (2-row units)
+  const int groups = std::max(1, std::min(kGluMaxThreads / (64 * S), 16 / S));
+  const int cus = std::max(1, device_cu_count());
+  const int n_units4 = route.n * (g.inter / kRowsGlu);
+  if (!(kRowsGlu == 4 && (n_units4 + groups - 1) / groups <= cus)) return K3_HIP_OK;
+  ChainPlan cp;
+  cp.S = S;
+  cp.groups = groups;
+  cp.n_units = route.n * (g.inter / 2);
+  cp.poll_limit = mode == 2 ? 0 : kChainPollLimit;
+  cp.zero = 0;
+  const int grid = std::max(1, std::min(cus, (cp.n_units + groups - 1) / groups));
+  const int threads = 64 * S * groups;
+  const int nbt = (g.hidden + 3) / 4;
+  if (grid < cus || grid > kChainMaxGrid || threads < 384 || (int64_t)grid * (threads / 64) < nbt)
+    return K3_HIP_OK;
+  const int iters = (cp.n_units + grid * groups - 1) / (grid * groups);
+  if (iters != 1 && iters != 2) return K3_HIP_OK;
+  const void* kernel = iters == 1 ? (const void*)k_expert_chain<uint16_t, OT, NE, 1>
+                                  : (const void*)k_expert_chain<uint16_t, OT, NE, 2>;
+  const unsigned lds = (unsigned)(NE * kHSliceF4 * sizeof(float4));
+  if (!lds_fits(kernel, threads, lds)) return K3_HIP_OK;
+  cp.slot = fused_slot(ws.base);
+  if (cp.slot < 0 || cp.slot >= kChainSlots) return K3_HIP_OK;
+  *ran = true;
+  uint64_t* ht = reinterpret_cast<uint64_t*>(ws.h);
+  TimedLaunch tl(KC_DECODE_CHAIN, st);
+  if (iters == 1)
+    launch_timed(tl, (k_expert_chain<uint16_t, OT, NE, 1>), dim3(grid), dim3(threads), lds, st,
+                 route, g, x, ht, out, cp);
+  else
+    launch_timed(tl, (k_expert_chain<uint16_t, OT, NE, 2>), dim3(grid), dim3(threads), lds, st,
+                 route, g, x, ht, out, cp);
+  return launched(tl, "one-expert decode launch");
+}
+
 }  // namespace
 
 int set_fused_decode(int enabled) {
   return g_fused_enabled.exchange(enabled ? 1 : 0);
+}
+
+int set_decode_chain(int mode) {
+  if (mode < 0 || mode > 2) return fail(K3_HIP_E_INVALID, "decode chain mode %d unknown", mode);
+  return g_chain_mode.exchange(mode);
 }
 
 int set_decode_mfma(int mode) {
@@ -3118,6 +3432,19 @@ int launch_decode_layer(const Geo& g, const TokenRoute& route, const void* x, in
                  : fused_decode(g, route, static_cast<const float*>(x), static_cast<float*>(out),
                                 ws, st, &ran));
   if (frc != K3_HIP_OK || ran) return frc;
+  const int crc =
+      x_dtype == K3_DTYPE_BF16
+          ? (out_dtype == K3_DTYPE_BF16
+                 ? chain_decode(g, route, static_cast<const uint16_t*>(x),
+                                static_cast<uint16_t*>(out), ws, st, &ran)
+                 : chain_decode(g, route, static_cast<const uint16_t*>(x),
+                                static_cast<float*>(out), ws, st, &ran))
+          : (out_dtype == K3_DTYPE_BF16
+                 ? chain_decode(g, route, static_cast<const float*>(x),
+                                static_cast<uint16_t*>(out), ws, st, &ran)
+                 : chain_decode(g, route, static_cast<const float*>(x), static_cast<float*>(out),
+                                ws, st, &ran));
+  if (crc != K3_HIP_OK || ran) return crc;
   int rc = x_dtype == K3_DTYPE_BF16
                ? glu_decode_dispatch<uint16_t>(g, route, static_cast<const uint16_t*>(x), ws.h, st)
                : glu_decode_dispatch<float>(g, route, static_cast<const float*>(x), ws.h, st);

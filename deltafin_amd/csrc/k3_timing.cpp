@@ -26,7 +26,7 @@ const char* const kClassNames[KC_COUNT] = {
     "gemv",        "activate",    "route",       "glu_decode", "down_decode",
     "verify_plan", "glu_verify",  "down_verify", "combine",    "synth",
     "decode_fused", "split_terms", "glu_mfma",   "down_mfma",  "spine_gemv",
-    "rms_norm",    "spine_mfma",
+    "rms_norm",    "spine_mfma",  "decode_chain",
 };
 
 struct TimingState {

@@ -456,6 +456,20 @@ int k3_hip_timing_end(K3HipKernelTimingV1* out, int capacity, int* n_out,
  * slower on MI355X.  Returns the previous setting. */
 int k3_hip_set_fused_decode(int enabled);
 
+/* No reference counterpart.  A single-token layer call with one routed
+ * expert given as a span pointer (bf16 x, raw-v1, intermediate 2048) runs,
+ * by default (mode K3_DECODE_CHAIN_ON), as one launch whose workgroups hand h
+ * to the down rows through device memory instead of a second launch.
+ * K3_DECODE_CHAIN_OFF makes such calls take the two launches;
+ * K3_DECODE_CHAIN_FALLBACK runs the one launch with every workgroup computing
+ * the gate/up shares it finds missing at once (the path taken when not every
+ * workgroup is resident; for tests).  All compute bit-identical outputs.
+ * Returns the previous mode, or K3_HIP_E_INVALID for another value. */
+#define K3_DECODE_CHAIN_OFF 0
+#define K3_DECODE_CHAIN_ON 1
+#define K3_DECODE_CHAIN_FALLBACK 2
+int k3_hip_set_decode_chain(int mode);
+
 /* No reference counterpart.  Where the single-token gate/up dots of the layer
  * calls above run: K3_DECODE_DOTS_VALU (0) on the vector ALUs for every
  * activation type; K3_DECODE_DOTS_MFMA_F32 (1, the default) on the bf16
