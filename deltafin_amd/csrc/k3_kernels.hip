@@ -2101,6 +2101,11 @@ constexpr int kChainPollLimit = 256;
 constexpr int kChainSlots = 64;
 static __device__ __align__(256) unsigned g_chain_calls[kChainSlots][kChainMaxGrid] = {};
 
+// Cache policy of a re-read of tagged h: sc0 and sc1, so that neither the
+// CU's vector cache nor the XCD's L2 answers with the copy an earlier read of
+// the same lines brought in.
+constexpr int kReread = 17;
+
 // Tag of the call whose count is c: a signalling NaN (exponent all ones,
 // quiet bit clear, payload 1 .. 2^22 - 1).
 __device__ __forceinline__ uint32_t chain_tag(unsigned c) {
@@ -2193,7 +2198,7 @@ void k_expert_chain(const TokenRoute route_arg, const Geo g, const XT* __restric
     for (int k = 0; k < kPer; ++k) {
       const uint32_t off = (uint32_t)min((int)threadIdx.x + k * T, np - 1) * 16u;
       v[k] = polls == 0 && shares == 0 ? __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0u, 0)
-                                       : __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0u, 16);
+                                       : __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0u, kReread);
     }
     int miss = 0;
 #pragma unroll
