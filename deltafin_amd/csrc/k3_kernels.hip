@@ -1822,8 +1822,9 @@ __global__ __launch_bounds__(1024) void k_down_g96(const TokenRoute route_arg, c
 // a slot at once).  Slots are zero when the code object loads, and the last
 // workgroup of every launch returns its slot to zero.
 //
-// Opt-in only: on MI355X at config 2 it takes 83 us per token against 67 us
-// for k_glu_decode + k_down_g64.  Per-workgroup phase stamps put the loss in
+// Opt-in only: on MI355X at config 2 it takes 76-77 us per token against
+// 64-65 us for k_glu_decode + k_down_g64 (the bench's other_decode_path on
+// one box).  Per-workgroup phase stamps put the loss in
 // three places: 1024-thread workgroups start over ~4 us (512-thread ones over
 // 0.8 us) and so finish gate/up later; every down ticket waits for the last
 // gate/up ticket plus a poll of the counter; then all workgroups read the
