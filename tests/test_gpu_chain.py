@@ -130,6 +130,43 @@ def test_chain_matches_two_launch_and_oracle(gpu, hidden, act):
             assert err <= TOL, f"cond rel err {err:.3e}"
 
 
+def test_chain_special_scales(gpu):
+    """Scale bytes the reference treats specially, in both phases: a gate
+    row with scale byte 255 (NaN: its h, and so every output, is NaN), a group
+    of an up row with scale byte 0 (the group contributes +0.0), a down row
+    with 255 (that output NaN) and a group of another with 0.  One launch and
+    two launches agree bit for bit, NaN payloads included."""
+    import torch
+    from deltafin_amd import _lib, moe
+    g = _geo(7168, "silu")
+    say("chain special scale bytes")
+    bank, stride = _bank(g, 91)
+    off = moe.span_offsets(g)
+    G, GI = g.hidden // 32, g.intermediate // 32
+    ws = moe.workspace(g, 1)
+    rng = np.random.default_rng(91)
+    x = _bf16_dev(rng.standard_normal(g.hidden).astype(np.float32))
+    cases = [
+        ("up row 5 scale 0, down rows 17 / 4000 scales 255 / 0",
+         [(off["w3s"] + 5 * G + 3, 0), (off["w2s"] + 17 * GI + 9, 255), (off["w2s"] + 4000 * GI, 0)]),
+        ("gate row 1000 scale 255", [(off["w1s"] + 1000 * G + 100, 255)]),
+    ]
+    for name, edits in cases:
+        span = bank[:stride].clone()
+        for o, v in edits:
+            span[o] = v
+        y2, k2 = _call(g, span.data_ptr(), x, ws, torch.float32, _lib.DECODE_CHAIN_OFF)
+        y1, k1 = _call(g, span.data_ptr(), x, ws, torch.float32, _lib.DECODE_CHAIN_ON)
+        torch.cuda.synchronize()
+        assert "decode_chain" in k1 and "glu_decode" in k2, (k1, k2)
+        assert _same(y1, y2), name
+        yh = y1.cpu().numpy()
+        if "gate row" in name:
+            assert np.isnan(yh).all(), name
+        else:
+            assert np.isnan(yh[17]) and np.isfinite(np.delete(yh, 17)).all(), name
+
+
 def test_chain_back_to_back(gpu):
     """40 calls queued on one workspace without a host sync, experts and
     activations changing: each call's tag must differ from the last, or a
