@@ -362,7 +362,7 @@ def test_verify_table_matches_layer(gpu):
         assert oracle.cond_rel_err(out[p], ref, mag, g.intermediate) <= TOL
 
 
-@pytest.mark.parametrize("m", [4, 16])
+@pytest.mark.parametrize("m", [4, 8, 16])
 def test_verify_route_bank384(gpu, m):
     """Device-routed verify over a config-3-sized bank (384 experts, 8.98 GB:
     span addresses on both sides of every 2^31 boundary of the low word)."""
