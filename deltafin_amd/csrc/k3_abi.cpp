@@ -814,9 +814,10 @@ int verify_table(const Geo& g, const EdgeTable& tbl, const void* x, int x_dtype,
     }
   }
   if (mfma || valu) {
-    int rc = launch_verify_plan_table(tbl, ws, st);
+    int rc = launch_verify_plan_table(g, tbl, ws, st, mfma ? x : nullptr, x_dtype);
     if (rc != K3_HIP_OK) return rc;
-    return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
+    return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st,
+                                     true)
                 : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
   }
   // One decode layer per position: a run of two or more consecutive
@@ -962,9 +963,11 @@ int experts_on_device_routes(const Geo& g, const uint8_t* bank, uint64_t stride,
   const bool mfma = P >= 2 && (mode == K3_VERIFY_UNION_MFMA ||
                                (mode == K3_VERIFY_AUTO && shared && verify_mfma_supported(g)));
   if (mfma || (P >= 2 && mode == K3_VERIFY_UNION_VALU)) {
-    int rc = launch_verify_plan_bank(g, bank, stride, P, top_k, ws, st);
+    int rc = launch_verify_plan_bank(g, bank, stride, n_bank, P, top_k, ws, st,
+                                     mfma ? x : nullptr, K3_DTYPE_F32);
     if (rc != K3_HIP_OK) return rc;
-    return mfma ? launch_verify_mfma(g, n_edges, P, x, K3_DTYPE_F32, out, K3_DTYPE_F32, ws, st)
+    return mfma ? launch_verify_mfma(g, n_edges, P, x, K3_DTYPE_F32, out, K3_DTYPE_F32, ws, st,
+                                     true)
                 : launch_verify_layer(g, n_edges, P, x, K3_DTYPE_F32, out, K3_DTYPE_F32, ws, st);
   }
   TokenRoute route;
@@ -1565,9 +1568,11 @@ int k3_hip_moe_verify_route_device(const K3HipGeometryV1* gd, const uint8_t* ban
     int rc = launch_route(logits, n_bank, top_k, n_positions, ws.ids, ws.w, route_ids,
                           route_weights, st);
     if (rc == K3_HIP_OK)
-      rc = launch_verify_plan_bank(g, bank, expert_stride, n_positions, top_k, ws, st);
+      rc = launch_verify_plan_bank(g, bank, expert_stride, n_bank, n_positions, top_k, ws, st,
+                                   mfma ? x : nullptr, x_dtype);
     if (rc != K3_HIP_OK) return rc;
-    return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st)
+    return mfma ? launch_verify_mfma(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st,
+                                     true)
                 : launch_verify_layer(g, n_edges, n_positions, x, x_dtype, out, out_dtype, ws, st);
   }
   // One routed decode layer per position: each position's gate/up workgroups

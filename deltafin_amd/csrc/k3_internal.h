@@ -151,11 +151,16 @@ int set_decode_chain(int mode);
 int set_decode_mfma(int mode);
 // LDS bytes the in-kernel router needs for a bank of n_bank logits and top_k.
 size_t route_scratch_bytes(int n_bank, int top_k);
-int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride,
+// The verify plan (edges grouped by expert) in ws.  x_split (the positions'
+// activations, x_dtype bf16 or fp32): the same launch also writes their
+// matrix-core terms, and launch_verify_mfma is then called with x_split_done.
+int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride, int n_bank,
                             int n_positions, int top_k, const Workspace& ws,
-                            hipStream_t stream);
-int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws,
-                             hipStream_t stream);
+                            hipStream_t stream, const void* x_split = nullptr,
+                            int x_dtype = 0);
+int launch_verify_plan_table(const Geo& g, const EdgeTable& table, const Workspace& ws,
+                             hipStream_t stream, const void* x_split = nullptr,
+                             int x_dtype = 0);
 // Edges e0 .. e0 + n - 1 of a caller route table into the workspace as a
 // table-mode route (ws.uptr span pointers, ws.w weights).
 int launch_route_table(const EdgeTable& table, int e0, int n, const Workspace& ws,
@@ -173,7 +178,7 @@ int launch_verify_combine(const Geo& g, int n_positions, void* out, int out_dtyp
 bool verify_mfma_supported(const Geo& g);
 int launch_verify_mfma(const Geo& g, int n_edges, int n_positions, const void* x,
                        int x_dtype, void* out, int out_dtype, const Workspace& ws,
-                       hipStream_t stream);
+                       hipStream_t stream, bool x_split_done = false);
 int launch_synth_bank(const Geo& g, uint8_t* bank, uint64_t stride,
                       int n_experts, uint64_t first_expert, uint64_t seed,
                       int lo, int hi, hipStream_t stream);

@@ -32,6 +32,7 @@
 #include "k3_device.h"
 #include "k3_internal.h"
 #include "k3_launch.h"
+#include "k3_terms.h"
 
 namespace k3 {
 
@@ -2476,8 +2477,9 @@ __global__ __launch_bounds__(1024) void k_route_sigmoid_bias(
 // list groups every expert's edges together, in edge order within a group.
 // Group heads are counted with a ballot prefix scan, which numbers the unique
 // experts in pointer order.  All loops are over the 256 edges in LDS.
+// ranked (workgroup-uniform): rank_in is edge e's rank, computed by the caller.
 __device__ void plan_core(const uint8_t* key, int e, int n_edges, int n_positions,
-                          const Workspace& ws) {
+                          const Workspace& ws, bool ranked = false, int rank_in = 0) {
   __shared__ uint64_t kp[K3_HIP_MAX_EDGES];
   __shared__ int srt[K3_HIP_MAX_EDGES];
   __shared__ int wave_heads[K3_HIP_MAX_EDGES / 64];
@@ -2485,10 +2487,13 @@ __device__ void plan_core(const uint8_t* key, int e, int n_edges, int n_position
   if (e < n_edges) kp[e] = k;
   __syncthreads();
   if (e < n_edges) {
-    int rank = 0;
-    for (int j = 0; j < n_edges; ++j) {
-      const uint64_t kj = kp[j];
-      rank += (kj < k) || (kj == k && j < e);
+    int rank = rank_in;
+    if (!ranked) {
+      rank = 0;
+      for (int j = 0; j < n_edges; ++j) {
+        const uint64_t kj = kp[j];
+        rank += (kj < k) || (kj == k && j < e);
+      }
     }
     srt[rank] = e;
   }
@@ -2525,22 +2530,113 @@ __device__ void plan_core(const uint8_t* key, int e, int n_edges, int n_position
   }
 }
 
+// Exclusive prefix sums of c[0 .. n) in place, n <= 16 * 256, by the 256
+// threads of the workgroup (each owns a run of consecutive entries); ends
+// with a barrier.
+__device__ void scan_bins_256(uint32_t* c, int n) {
+  __shared__ uint32_t wtot[4];
+  const int t = threadIdx.x, lane = t & 63;
+  const int per = (n + 255) >> 8;
+  const int b0 = t * per;
+  uint32_t s = 0;
+  for (int i = 0; i < per; ++i)
+    if (b0 + i < n) s += c[b0 + i];
+  uint32_t inc = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t v = __shfl_up(inc, o);
+    if (lane >= o) inc += v;
+  }
+  if (lane == 63) wtot[t >> 6] = inc;
+  __syncthreads();
+  uint32_t run = inc - s;
+  for (int w = 0; w < (t >> 6); ++w) run += wtot[w];
+  for (int i = 0; i < per; ++i)
+    if (b0 + i < n) {
+      const uint32_t v = c[b0 + i];
+      c[b0 + i] = run;
+      run += v;
+    }
+  __syncthreads();
+}
+
+// The activation's term split (k3_terms.h) that a matrix-core verify call
+// needs next, run by workgroups 1 .. of the plan launch beside the plan in
+// workgroup 0 (T = 0: none).
+template <int T, typename SrcT>
+__device__ __forceinline__ bool plan_split_block(const SrcT* xs, int n_rows, int K,
+                                                 const Workspace& ws) {
+  if constexpr (T > 0) {
+    if (blockIdx.x > 0) {
+      split_terms_at<T, SrcT>(xs, n_rows, K, ws.xq, ws.xqs,
+                              (int)((blockIdx.x - 1) * blockDim.x + threadIdx.x));
+      return true;
+    }
+  }
+  return false;
+}
+
+constexpr int kPlanMaxBank = 4096;  // experts the counting rank bins
+
+// Bank routes: an edge's key is its expert's span, bank + id * stride, so key
+// order is id order and the rank of edge e (position p) is the number of
+// edges with a smaller id plus the edges of earlier positions with the same
+// id.  A position's ids are distinct (the router ranks distinct experts), so
+// a per-expert mask of positions gives the second term; with an id outside
+// the bank or a repeated id within a position (the masks' popcounts then
+// differ from the edge counts), the comparison rank over every pair of keys
+// takes over.  Both give the same order.
+template <int T, typename SrcT>
 __global__ __launch_bounds__(256) void k_verify_plan_bank(const uint8_t* bank, uint64_t stride,
-                                                          int n_positions, int top_k,
-                                                          const Workspace ws) {
+                                                          int n_bank, int n_positions, int top_k,
+                                                          const Workspace ws, const SrcT* xs,
+                                                          int K) {
+  if (plan_split_block<T, SrcT>(xs, n_positions, K, ws)) return;
+  __shared__ uint32_t pmask[kPlanMaxBank];  // bit p: position p routes to the expert
+  __shared__ uint32_t pcnt[kPlanMaxBank];   // edges routed to the expert, then their prefix
+  __shared__ int fallback;
   const int e = threadIdx.x;
   const int n_edges = n_positions * top_k;
   const uint8_t* key = nullptr;
+  int id = -1, p = 0;
   if (e < n_edges) {
-    key = bank + (uint64_t)ws.ids[e] * stride;
-    ws.epos[e] = e / top_k;
+    id = ws.ids[e];
+    p = e / top_k;
+    key = bank + (uint64_t)id * stride;
+    ws.epos[e] = p;
   }
   if (e <= n_positions) ws.poff[e] = e * top_k;
-  plan_core(key, e, n_edges, n_positions, ws);
+  const bool bins = n_bank >= 1 && n_bank <= kPlanMaxBank && stride > 0;  // uniform
+  if (bins)
+    for (int i = e; i < n_bank; i += blockDim.x) {
+      pmask[i] = 0u;
+      pcnt[i] = 0u;
+    }
+  if (e == 0) fallback = bins ? 0 : 1;
+  __syncthreads();
+  const bool in = bins && e < n_edges && id >= 0 && id < n_bank;
+  if (bins && e < n_edges && !in) fallback = 1;
+  if (in) {
+    atomicOr(&pmask[id], 1u << p);
+    atomicAdd(&pcnt[id], 1u);
+  }
+  __syncthreads();
+  if (in && (uint32_t)__popc(pmask[id]) != pcnt[id]) fallback = 1;
+  __syncthreads();
+  const bool ranked = fallback == 0;  // uniform
+  int rank = 0;
+  if (ranked) {
+    scan_bins_256(pcnt, n_bank);
+    if (in) rank = (int)pcnt[id] + __popc(pmask[id] & ((1u << p) - 1u));
+  }
+  plan_core(key, e, n_edges, n_positions, ws, ranked, rank);
 }
 
+template <int T, typename SrcT>
 __global__ __launch_bounds__(256) void k_verify_plan_table(const EdgeTable tbl,
-                                                           const Workspace ws) {
+                                                           const Workspace ws, const SrcT* xs,
+                                                           int K) {
+  if (plan_split_block<T, SrcT>(xs, tbl.n_positions, K, ws)) return;
   const int e = threadIdx.x;
   const uint8_t* key = nullptr;
   if (e < tbl.n_edges) {
@@ -2713,6 +2809,9 @@ __global__ void k_combine_positions(const Workspace ws, int hidden, int n_positi
   const int p = (int)(i / hidden);
   const int col = (int)(i - (int64_t)p * hidden);
   float acc = 0.0f;
+  // Unrolled so that the edges' loads are in flight together; the sum still
+  // runs in edge order.
+#pragma unroll 8
   for (int e = ws.poff[p]; e < ws.poff[p + 1]; ++e)
     acc += ws.w[e] * ws.y[(size_t)e * hidden + col];
   store_out(out + i, acc);
@@ -3496,20 +3595,46 @@ int launch_decode_positions(const Geo& g, const TokenRoute& route, int n_positio
              : down_decode_dispatch<float>(g, down_route, ws, static_cast<float*>(out), st, pl);
 }
 
-int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride, int n_positions,
-                            int top_k, const Workspace& ws, hipStream_t st) {
-  (void)g;
+// Workgroups of the plan launch: the plan, plus the activation split's when
+// x_split is set (one thread per 8 elements of the n_rows x hidden rows).
+static dim3 plan_grid(const Geo& g, int n_rows, const void* x_split) {
+  const int64_t threads = x_split ? (int64_t)n_rows * (g.hidden / 32) * 4 : 0;
+  return dim3((unsigned)(1 + (threads + 255) / 256));
+}
+
+int launch_verify_plan_bank(const Geo& g, const uint8_t* bank, uint64_t stride, int n_bank,
+                            int n_positions, int top_k, const Workspace& ws, hipStream_t st,
+                            const void* x_split, int x_dtype) {
   // Rank-sorted plan: unique experts in span-pointer order, each expert's
   // edges in edge order (every union kernel takes any expert order).
   TimedLaunch tl(KC_VERIFY_PLAN, st);
-  launch_timed(tl, k_verify_plan_bank, dim3(1), dim3(256), 0, st, bank, stride, n_positions,
-               top_k, ws);
+  const dim3 grid = plan_grid(g, n_positions, x_split);
+  if (!x_split)
+    launch_timed(tl, (k_verify_plan_bank<0, float>), grid, dim3(256), 0, st, bank, stride,
+                 n_bank, n_positions, top_k, ws, nullptr, g.hidden);
+  else if (x_dtype == K3_DTYPE_BF16)
+    launch_timed(tl, (k_verify_plan_bank<2, uint16_t>), grid, dim3(256), 0, st, bank, stride,
+                 n_bank, n_positions, top_k, ws, static_cast<const uint16_t*>(x_split),
+                 g.hidden);
+  else
+    launch_timed(tl, (k_verify_plan_bank<3, float>), grid, dim3(256), 0, st, bank, stride,
+                 n_bank, n_positions, top_k, ws, static_cast<const float*>(x_split), g.hidden);
   return launched(tl, "verify plan launch");
 }
 
-int launch_verify_plan_table(const EdgeTable& table, const Workspace& ws, hipStream_t st) {
+int launch_verify_plan_table(const Geo& g, const EdgeTable& table, const Workspace& ws,
+                             hipStream_t st, const void* x_split, int x_dtype) {
   TimedLaunch tl(KC_VERIFY_PLAN, st);
-  launch_timed(tl, k_verify_plan_table, dim3(1), dim3(256), 0, st, table, ws);
+  const dim3 grid = plan_grid(g, table.n_positions, x_split);
+  if (!x_split)
+    launch_timed(tl, (k_verify_plan_table<0, float>), grid, dim3(256), 0, st, table, ws, nullptr,
+                 g.hidden);
+  else if (x_dtype == K3_DTYPE_BF16)
+    launch_timed(tl, (k_verify_plan_table<2, uint16_t>), grid, dim3(256), 0, st, table, ws,
+                 static_cast<const uint16_t*>(x_split), g.hidden);
+  else
+    launch_timed(tl, (k_verify_plan_table<3, float>), grid, dim3(256), 0, st, table, ws,
+                 static_cast<const float*>(x_split), g.hidden);
   return launched(tl, "verify plan launch");
 }
 

@@ -143,6 +143,39 @@ def test_verify_mfma_shared_table(gpu, verify_mode, preset_id, xdt):
         assert err <= TOL, f"position {p}: {err:.3e}"
 
 
+@pytest.mark.parametrize("n_bank,m", [(48, 16), (384, 16), (48, 3)])
+@pytest.mark.parametrize("mode", ["mfma", "valu"])
+def test_verify_bank_plan_matches_table(gpu, verify_mode, n_bank, m, mode):
+    """The device-routed verify groups its edges by expert id (counts and
+    position masks over the bank's experts); the caller-table verify groups
+    the same edges by comparing span pointers.  On the same routes the two
+    calls give the same outputs, bit for bit, on both union paths; with 16
+    positions over 48 experts most experts carry several positions."""
+    import torch
+    from deltafin_amd import moe
+    g = moe.preset(2)
+    k = 16
+    say(f"verify bank plan vs table mode={mode} M={m} bank={n_bank}")
+    verify_mode(MODES[mode])
+    stride = g.expert_span
+    bank = torch.empty(n_bank * stride, dtype=torch.uint8, device="cuda")
+    moe.synth_bank(g, bank, stride, n_bank, 0, 905)
+    rng = np.random.default_rng(40 + m + n_bank)
+    logits = rng.standard_normal((m, n_bank)).astype(np.float32)
+    x = _bf16(rng.standard_normal((m, g.hidden)).astype(np.float32)).reshape(m, g.hidden)
+    ws = moe.workspace(g, m * k, m)
+    out_r, ids, wts = moe.moe_verify_route(g, bank, stride, n_bank, _t(logits), k, x, ws)
+    torch.cuda.synchronize()
+    ids_h, wts_h = ids.cpu().numpy().reshape(-1), wts.cpu().numpy().reshape(-1)
+    assert len(set(ids_h.tolist())) < m * k or m < 16
+    edges = [bank.data_ptr() + int(e) * stride for e in ids_h]
+    out_t = moe.moe_verify(g, edges, wts_h.tolist(), [p * k for p in range(m + 1)], x, ws)
+    torch.cuda.synchronize()
+    a, b = out_r.cpu().numpy(), out_t.cpu().numpy()
+    assert np.all(np.isfinite(a))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_verify_mfma_bf16_out_empty_position(gpu, verify_mode):
     """bf16 outputs within one bf16 ulp of the oracle plus the fp32 band; an
     empty position gives a zero row; one expert repeated inside a position."""
