@@ -2481,14 +2481,30 @@ __global__ __launch_bounds__(1024) void k_route_sigmoid_bias(
 __device__ void plan_core(const uint8_t* key, int e, int n_edges, int n_positions,
                           const Workspace& ws, bool ranked = false, int rank_in = 0) {
   __shared__ uint64_t kp[K3_HIP_MAX_EDGES];
+  __shared__ uint64_t kpe[K3_HIP_MAX_EDGES];  // key * 256 + edge
   __shared__ int srt[K3_HIP_MAX_EDGES];
   __shared__ int wave_heads[K3_HIP_MAX_EDGES / 64];
+  __shared__ int wide_keys;
   const uint64_t k = reinterpret_cast<uint64_t>(key);
-  if (e < n_edges) kp[e] = k;
+  if (e == 0) wide_keys = 0;
   __syncthreads();
   if (e < n_edges) {
+    kp[e] = k;
+    kpe[e] = (k << 8) | (uint64_t)e;
+    if ((k >> 56) != 0) wide_keys = 1;
+  }
+  __syncthreads();
+  // Keys below 2^56 (every device address) rank by one 64-bit comparison
+  // per pair: key * 256 + edge orders as (key, edge).
+  const bool wide = wide_keys != 0;  // uniform
+  if (e < n_edges) {
     int rank = rank_in;
-    if (!ranked) {
+    if (!ranked && !wide) {
+      rank = 0;
+      const uint64_t ke = kpe[e];
+#pragma unroll 8
+      for (int j = 0; j < n_edges; ++j) rank += kpe[j] < ke;
+    } else if (!ranked) {
       rank = 0;
       for (int j = 0; j < n_edges; ++j) {
         const uint64_t kj = kp[j];
