@@ -911,8 +911,9 @@ uint64_t block_layout(const K3HipMoeSpineV1& sp, const Geo& g, int max_positions
   const int wmax = (int)std::max(sp.hidden, std::max(sp.routed_hidden, sp.shared_intermediate));
   if (b) b->terms = base + off;
   off += align256(spine_mfma_terms_bytes(max_positions, wmax));
-  if (b) b->terms2 = base + off;
-  off += align256(spine_mfma_terms_bytes(max_positions, (int)sp.hidden));
+  if (b) b->terms2 = base + off;  // the side stream's: hidden rows, then the shared h
+  off += align256(spine_mfma_terms_bytes(
+      max_positions, (int)std::max(sp.hidden, sp.shared_intermediate)));
   return off;
 }
 
@@ -1079,9 +1080,12 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
     };
     // With the side stream the shared expert reads its own copy of the hidden
     // rows' terms (the main stream's buffer is reused for the routed output
-    // and h while the side work may still run).
-    if (side.parallel() &&
-        (rc = side.fork([&](hipStream_t s) { return shared_glu(b.terms2, true, s); })))
+    // while the side work may still run), and the side stream also splits
+    // its h into that buffer for shared_down, off the main stream's path.
+    if (side.parallel() && (rc = side.fork([&](hipStream_t s) {
+                              const int r = shared_glu(b.terms2, true, s);
+                              return r ? r : split(b.gate, S, b.terms2, s);
+                            })))
       return rc;
     // The router logits stay on the fp32 kernels at every P: each position's
     // logit is then summed in the same order whatever the batch (the fp32
@@ -1104,10 +1108,11 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
       return rc;
     if ((rc = split(b.routed_out, R, b.terms, st)) ||
         (rc = mm(sp.routed_up, b.terms, out, H, R, false, st, "routed_up")) ||
-        (rc = side.join()) || (rc = split(b.gate, S, b.terms, st)) ||
-        (rc = mm(sp.shared_down, b.terms, out, H, S, true, st, "shared_down")))
+        (rc = side.join()))
       return rc;
-    return K3_HIP_OK;
+    if (!side.parallel() && (rc = split(b.gate, S, b.terms, st))) return rc;
+    return mm(sp.shared_down, side.parallel() ? b.terms2 : b.terms, out, H, S, true, st,
+              "shared_down");
   }
   // the shared expert: h = situ(gate, up), one launch reading each gate row
   // and its up row together (two launches and the activation where the shape
