@@ -1103,11 +1103,18 @@ int k3_hip_moe_block_device(const K3HipMoeSpineV1* spine, const K3HipGeometryV1*
     if ((rc = experts_on_device_routes(g, bank, expert_stride, E, P, top_k, b.routed_in,
                                        b.routed_out, ws, st)))
       return rc;
-    if ((rc = from_spine(spine_rms_norm(b.routed_out, sp.routed_norm, b.routed_out, P, R,
-                                        K3_RMS_EPSILON, st), "routed RMS norm")))
+    // the routed RMS norm writes routed_up's terms in the same launch
+    rc = spine_rms_norm_terms(b.routed_out, sp.routed_norm, b.routed_out, P, R, K3_RMS_EPSILON,
+                              b.terms, st);
+    if (rc == K3_SPINE_E_UNSUPPORTED) {
+      if ((rc = from_spine(spine_rms_norm(b.routed_out, sp.routed_norm, b.routed_out, P, R,
+                                          K3_RMS_EPSILON, st), "routed RMS norm")) ||
+          (rc = split(b.routed_out, R, b.terms, st)))
+        return rc;
+    } else if ((rc = from_spine(rc, "routed RMS norm"))) {
       return rc;
-    if ((rc = split(b.routed_out, R, b.terms, st)) ||
-        (rc = mm(sp.routed_up, b.terms, out, H, R, false, st, "routed_up")) ||
+    }
+    if ((rc = mm(sp.routed_up, b.terms, out, H, R, false, st, "routed_up")) ||
         (rc = side.join()))
       return rc;
     if (!side.parallel() && (rc = split(b.gate, S, b.terms, st))) return rc;

@@ -277,5 +277,10 @@ int spine_mfma_gemv(const void* w, const void* terms, float* y, int rows, int co
 int spine_decode_bits(const uint16_t* in, uint32_t* out, int count, hipStream_t stream);
 int spine_rms_norm(const float* in, const float* weight, float* out, int rows, int cols,
                    float eps, hipStream_t stream);
+// The same norm (rows <= 16, cols a multiple of 64, 16-byte aligned), which
+// also writes the normalised rows' matrix-core terms (spine_mfma_split's
+// layout and values) into terms; K3_SPINE_E_UNSUPPORTED for other shapes.
+int spine_rms_norm_terms(const float* in, const float* weight, float* out, int rows, int cols,
+                         float eps, void* terms, hipStream_t stream);
 
 }  // namespace k3

@@ -444,10 +444,20 @@ __global__ __launch_bounds__(kSpineThreads) void k_rms_norm(const float* __restr
 // index order (x, y, z, w), then wave sums, then the waves in order.
 constexpr int kNormIter = 8;
 
+// kTerms: the workgroup of row p also writes the row's three BF16 terms into
+// the matrix-core spine's term buffer (k_split_bf16_terms' layout: column
+// n = 3 p + t of 16-column block n / 16, 16 bytes per (block, K32 step s,
+// lane 16 (k % 32) / 8 + n % 16)), each thread its float4's 8 bytes of each
+// term; workgroup 0 also writes the zero columns past 3 P and the two zero
+// steps after the last.  The terms are those k_split_bf16_terms forms from
+// the stored row.
+template <bool kTerms>
 __global__ __launch_bounds__(kSpineThreads) void k_rms_norm_vec(const float* __restrict__ in,
                                                                 const float* __restrict__ weight,
                                                                 float* __restrict__ out, int cols,
-                                                                float eps) {
+                                                                float eps,
+                                                                uint8_t* __restrict__ terms,
+                                                                int nb_count) {
   __shared__ float part[kSpineWaves];
   const float4* xp = reinterpret_cast<const float4*>(in + (uint64_t)blockIdx.x * cols);
   const float4* wp = reinterpret_cast<const float4*>(weight);
@@ -475,12 +485,57 @@ __global__ __launch_bounds__(kSpineThreads) void k_rms_norm_vec(const float* __r
 #pragma unroll
   for (int w = 1; w < kSpineWaves; ++w) total += part[w];
   const float r = 1.0f / sqrtf(total / (float)cols + eps);
+  const int tsteps = cols / 32 + 2;
 #pragma unroll
   for (int i = 0; i < kNormIter; ++i) {
     const int c = (int)threadIdx.x + kSpineThreads * i;
-    if (c < n4)
-      op[c] = make_float4(nw[i].x * (v[i].x * r), nw[i].y * (v[i].y * r), nw[i].z * (v[i].z * r),
-                          nw[i].w * (v[i].w * r));
+    if (c < n4) {
+      const float y[4] = {nw[i].x * (v[i].x * r), nw[i].y * (v[i].y * r),
+                          nw[i].z * (v[i].z * r), nw[i].w * (v[i].w * r)};
+      op[c] = make_float4(y[0], y[1], y[2], y[3]);
+      if constexpr (kTerms) {
+        uint32_t t[3][2];
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          uint32_t b[3][2];
+#pragma unroll
+          for (int o = 0; o < 2; ++o) {
+            const float f = y[e + o];
+            b[0][o] = f32_to_bf16_bits(f);
+            const float r1 = f - __uint_as_float(b[0][o] << 16);
+            b[1][o] = f32_to_bf16_bits(r1);
+            b[2][o] = f32_to_bf16_bits(r1 - __uint_as_float(b[1][o] << 16));
+          }
+#pragma unroll
+          for (int q = 0; q < 3; ++q) t[q][e >> 1] = b[q][0] | (b[q][1] << 16);
+        }
+        const int k = 4 * c;  // first K element of the float4
+        const int ks = k >> 5, lane16 = 16 * ((k & 31) >> 3), half = (k >> 2) & 1;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+          const int n = 3 * (int)blockIdx.x + q;
+          const size_t slot = ((size_t)(n >> 4) * tsteps + ks) * 64 + lane16 + (n & 15);
+          *reinterpret_cast<uint2*>(terms + 16 * slot + 8 * half) = make_uint2(t[q][0], t[q][1]);
+        }
+      }
+    }
+  }
+  if constexpr (kTerms) {
+    if (blockIdx.x == 0) {
+      // zero columns past 3 P (every step), then the two zero steps (every column)
+      const int n0 = 3 * (int)gridDim.x, ncol = 16 * nb_count;
+      const int zc = (ncol - n0) * tsteps * 4;
+      for (int z = threadIdx.x; z < zc; z += blockDim.x) {
+        const int n = n0 + z / (tsteps * 4), rem = z % (tsteps * 4);
+        const size_t slot = ((size_t)(n >> 4) * tsteps + rem / 4) * 64 + 16 * (rem % 4) + (n & 15);
+        *reinterpret_cast<uint4*>(terms + 16 * slot) = make_uint4(0u, 0u, 0u, 0u);
+      }
+      for (int z = threadIdx.x; z < nb_count * 2 * 64; z += blockDim.x) {
+        const int nb = z / 128, st = cols / 32 + (z / 64) % 2;
+        const size_t slot = ((size_t)nb * tsteps + st) * 64 + (z & 63);
+        *reinterpret_cast<uint4*>(terms + 16 * slot) = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
   }
 }
 
@@ -710,11 +765,29 @@ int spine_rms_norm(const float* in, const float* weight, float* out, int rows, i
                    ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(weight) |
                      reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
   if (vec)
-    launch_timed(tl, k_rms_norm_vec, dim3(rows), dim3(kSpineThreads), 0, st, in, weight, out, cols,
-                 eps);
+    launch_timed(tl, k_rms_norm_vec<false>, dim3(rows), dim3(kSpineThreads), 0, st, in, weight,
+                 out, cols, eps, nullptr, 0);
   else
     launch_timed(tl, k_rms_norm, dim3(rows), dim3(kSpineThreads), 0, st, in, weight, out, cols,
                  eps);
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return K3_SPINE_OK;
+  tl.failed();
+  return spine_fail(K3_SPINE_E_RUNTIME, "RMS norm launch: %s", hipGetErrorString(e));
+}
+
+int spine_rms_norm_terms(const float* in, const float* weight, float* out, int rows, int cols,
+                         float eps, void* terms, hipStream_t st) {
+  if (!in || !weight || !out || !terms || rows <= 0 || rows > 16 || cols < 64 || cols % 64 != 0 ||
+      cols > 4 * kSpineThreads * kNormIter || !(eps >= 0.f) || eps == INFINITY ||
+      ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(weight) |
+        reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(terms)) & 15u) != 0)
+    return K3_SPINE_E_UNSUPPORTED;
+  int rc = preflight("RMS norm");
+  if (rc != K3_SPINE_OK) return rc;
+  TimedLaunch tl(KC_RMS_NORM, st);
+  launch_timed(tl, k_rms_norm_vec<true>, dim3(rows), dim3(kSpineThreads), 0, st, in, weight, out,
+               cols, eps, static_cast<uint8_t*>(terms), (3 * rows + 15) / 16);
   const hipError_t e = hipGetLastError();
   if (e == hipSuccess) return K3_SPINE_OK;
   tl.failed();
